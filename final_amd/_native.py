@@ -1,0 +1,100 @@
+"""ctypes binding of libfinal_amd_moe.so (the C-ABI of include/moe_capi.h and
+include/moe_synth.h).  The library is built in-tree by final_amd/csrc/Makefile;
+loading fails loudly when it is missing - there is no fallback path."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libfinal_amd_moe.so")
+
+MOE_OK = 0
+MOE_ERR_INVALID_ARG = 1
+MOE_ERR_UNSUPPORTED = 2
+MOE_ERR_HIP = 3
+MOE_ERR_OUT_OF_MEMORY = 4
+MOE_ERR_NOT_READY = 5
+MOE_ERR_TOO_MANY_TOKENS = 6
+MOE_ERR_DEVICE_TIMEOUT = 7
+MOE_ERR_INTERNAL = 8
+
+# every symbol include/moe_capi.h and include/moe_synth.h declare
+CAPI_SYMBOLS = (
+    "moe_create", "moe_destroy", "moe_set_weights", "moe_forward", "moe_route",
+    "moe_experts", "moe_route_logits", "moe_last_routing", "moe_device_status",
+    "moe_plan_tile_rows", "moe_force_tile_rows", "moe_set_wait_divisor",
+    "moe_strerror", "moe_version",
+)
+SYNTH_SYMBOLS = (
+    "moe_synth_normal", "moe_synth_stream_gate", "moe_synth_stream_bias",
+    "moe_synth_stream_w1", "moe_synth_stream_w3", "moe_synth_stream_w2",
+    "moe_synth_stream_x", "moe_synth_set_threads",
+)
+
+
+class MoeDims(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("inter", ctypes.c_int),
+                ("num_experts", ctypes.c_int), ("top_k", ctypes.c_int),
+                ("max_tokens", ctypes.c_int)]
+
+
+class MoeError(RuntimeError):
+    def __init__(self, status: int, what: str):
+        self.status = status
+        super().__init__(f"{what}: {strerror(status)} (status {status})")
+
+
+_lib = None
+_vp = ctypes.c_void_p
+_i = ctypes.c_int
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(
+            f"final_amd native library not built: {LIB_PATH} is missing "
+            "(run `make -C final_amd/csrc` or __graft_entry__.build())")
+    L = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+    L.moe_create.argtypes = [ctypes.POINTER(MoeDims), ctypes.POINTER(_vp)]
+    L.moe_destroy.argtypes = [_vp]
+    L.moe_set_weights.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]
+    L.moe_forward.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
+    L.moe_route.argtypes = [_vp, _vp, _i, _vp]
+    L.moe_experts.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
+    L.moe_route_logits.argtypes = [_vp, _vp, _i, _vp]
+    L.moe_last_routing.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp]
+    L.moe_device_status.argtypes = [_vp, _vp]
+    L.moe_plan_tile_rows.argtypes = [_vp, _i]
+    L.moe_force_tile_rows.argtypes = [_vp, _i]
+    L.moe_set_wait_divisor.argtypes = [_vp, _i]
+    L.moe_strerror.argtypes = [_i]
+    L.moe_strerror.restype = ctypes.c_char_p
+    L.moe_version.restype = ctypes.c_char_p
+    L.moe_synth_normal.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_float,
+                                   ctypes.c_uint64, _vp, ctypes.c_size_t]
+    for n in ("gate", "bias"):
+        getattr(L, f"moe_synth_stream_{n}").restype = ctypes.c_uint64
+    for n in ("w1", "w3", "w2", "x"):
+        f = getattr(L, f"moe_synth_stream_{n}")
+        f.argtypes = [_i]
+        f.restype = ctypes.c_uint64
+    L.moe_synth_set_threads.argtypes = [_i]
+    _lib = L
+    return L
+
+
+def strerror(status: int) -> str:
+    return lib().moe_strerror(int(status)).decode()
+
+
+def check(status: int, what: str) -> None:
+    if status != MOE_OK:
+        raise MoeError(status, what)
+
+
+def version() -> str:
+    return lib().moe_version().decode()

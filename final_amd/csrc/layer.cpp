@@ -1,0 +1,235 @@
+// MLP / SparseMoeBlock (include/layer.h) on top of the C-ABI.
+// Reference: src/layer.cu:1200-1229 (MLP), 1274-1503 (SparseMoeBlock).
+#include "layer.h"
+
+#include <sstream>
+#include <stdexcept>
+#include <string>
+
+#include "model_loader.h"
+
+namespace {
+
+void check(int rc, const char *what) {
+  if (rc != MOE_OK)
+    throw std::runtime_error(std::string(what) + ": " + moe_strerror(rc));
+}
+
+void check_hip(hipError_t e, const char *what) {
+  if (e != hipSuccess)
+    throw std::runtime_error(std::string(what) + ": " + hipGetErrorString(e));
+}
+
+std::string expert_name(int layer, size_t e, const char *w) {
+  std::ostringstream ss;
+  ss << "layers." << layer << ".feed_forward.experts." << e << "." << w << ".weight";
+  return ss.str();
+}
+
+// Device buffer freed on scope exit.
+struct DevBuf {
+  void *p = nullptr;
+  explicit DevBuf(size_t bytes) {
+    if (bytes) check_hip(hipMalloc(&p, bytes), "hipMalloc");
+  }
+  ~DevBuf() {
+    if (p) (void)hipFree(p);
+  }
+  float *f() { return static_cast<float *>(p); }
+};
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// MLP
+// ---------------------------------------------------------------------------
+
+MLP::MLP(const std::string &w1_file, const std::string &w2_file,
+         const std::string &w3_file)
+    : w1_(Tensor::load_from_file(w1_file)), w3_(Tensor::load_from_file(w3_file)),
+      w2_(Tensor::load_from_file(w2_file)) {}
+
+MLP::MLP(Tensor w1, Tensor w2, Tensor w3)
+    : w1_(std::move(w1)), w3_(std::move(w3)), w2_(std::move(w2)) {}
+
+MLP::~MLP() { release_gpu(); }
+
+MLP::MLP(MLP &&o) noexcept
+    : w1_gpu_(o.w1_gpu_), w3_gpu_(o.w3_gpu_), w2_gpu_(o.w2_gpu_),
+      temp_buf_gpu_(o.temp_buf_gpu_), w1_(std::move(o.w1_)), w3_(std::move(o.w3_)),
+      w2_(std::move(o.w2_)) {
+  o.w1_gpu_ = o.w3_gpu_ = o.w2_gpu_ = o.temp_buf_gpu_ = nullptr;
+}
+
+MLP &MLP::operator=(MLP &&o) noexcept {
+  if (this != &o) {
+    release_gpu();
+    w1_ = std::move(o.w1_);
+    w2_ = std::move(o.w2_);
+    w3_ = std::move(o.w3_);
+    w1_gpu_ = o.w1_gpu_;
+    w2_gpu_ = o.w2_gpu_;
+    w3_gpu_ = o.w3_gpu_;
+    temp_buf_gpu_ = o.temp_buf_gpu_;
+    o.w1_gpu_ = o.w3_gpu_ = o.w2_gpu_ = o.temp_buf_gpu_ = nullptr;
+  }
+  return *this;
+}
+
+void MLP::release_gpu() {
+  if (w1_gpu_) (void)hipFree(w1_gpu_);
+  if (w2_gpu_) (void)hipFree(w2_gpu_);
+  if (w3_gpu_) (void)hipFree(w3_gpu_);
+  w1_gpu_ = w2_gpu_ = w3_gpu_ = nullptr;
+}
+
+void MLP::init_gpu() {
+  release_gpu();
+  auto up = [](const Tensor &t, float **dst) {
+    check_hip(hipMalloc(reinterpret_cast<void **>(dst), t.size() * sizeof(float)),
+              "hipMalloc");
+    check_hip(hipMemcpy(*dst, t.data(), t.size() * sizeof(float), hipMemcpyHostToDevice),
+              "hipMemcpy");
+  };
+  up(w1_, &w1_gpu_);
+  up(w2_, &w2_gpu_);
+  up(w3_, &w3_gpu_);
+}
+
+void MLP::forward(const Tensor &, Tensor &) {
+  throw std::logic_error("MLP::forward: the dense FFN is not part of this MoE build");
+}
+
+void MLP::forward_gpu(float *, float *, int, int, int, hipStream_t) {
+  throw std::logic_error("MLP::forward_gpu: the dense FFN is not part of this MoE build");
+}
+
+// ---------------------------------------------------------------------------
+// SparseMoeBlock
+// ---------------------------------------------------------------------------
+
+SparseMoeBlock::SparseMoeBlock(int layer_idx) : layer_idx_(layer_idx) {
+  std::ostringstream ss;
+  ss << "layers." << layer_idx << ".feed_forward.gate.weight";
+  gate_ = Tensor::load_from_file(ss.str());
+  experts_.reserve(NUM_EXPERTS);
+  for (size_t e = 0; e < NUM_EXPERTS; ++e)
+    experts_.emplace_back(expert_name(layer_idx, e, "w1"), expert_name(layer_idx, e, "w2"),
+                          expert_name(layer_idx, e, "w3"));
+  if (USE_EXPERT_BIAS) {
+    std::ostringstream sb;
+    sb << "layers." << layer_idx << ".feed_forward.expert_bias";
+    expert_bias_ = Tensor::load_from_file(sb.str());
+  }
+  check_shapes();
+}
+
+SparseMoeBlock::SparseMoeBlock(int layer_idx, Tensor gate, std::vector<MLP> experts,
+                               Tensor expert_bias)
+    : gate_(std::move(gate)), experts_(std::move(experts)),
+      expert_bias_(std::move(expert_bias)), layer_idx_(layer_idx) {
+  check_shapes();
+}
+
+SparseMoeBlock::~SparseMoeBlock() { moe_destroy(ctx_); }
+
+void SparseMoeBlock::check_shapes() const {
+  if (gate_.ndim() != 2 || gate_.shape()[0] != NUM_EXPERTS)
+    throw std::invalid_argument("SparseMoeBlock: gate must be [32][hidden]");
+  const size_t H = gate_.shape()[1];
+  if (experts_.size() != NUM_EXPERTS)
+    throw std::invalid_argument("SparseMoeBlock: need 32 experts");
+  const size_t I = experts_[0].w1().ndim() == 2 ? experts_[0].w1().shape()[0] : 0;
+  for (const MLP &m : experts_) {
+    if (m.w1().shape() != std::vector<size_t>{I, H} ||
+        m.w3().shape() != std::vector<size_t>{I, H} ||
+        m.w2().shape() != std::vector<size_t>{H, I})
+      throw std::invalid_argument("SparseMoeBlock: expert shapes must be w1,w3 [I][H], w2 [H][I]");
+  }
+  if (expert_bias_.size() != 0 && expert_bias_.size() != NUM_EXPERTS)
+    throw std::invalid_argument("SparseMoeBlock: expert_bias must have 32 entries");
+}
+
+void SparseMoeBlock::set_max_tokens(int n) {
+  if (ctx_) throw std::logic_error("SparseMoeBlock::set_max_tokens after init_gpu");
+  if (n <= 0) throw std::invalid_argument("SparseMoeBlock::set_max_tokens: n <= 0");
+  max_tokens_ = n;
+}
+
+void SparseMoeBlock::init_gpu() {
+  if (ctx_) {
+    moe_destroy(ctx_);
+    ctx_ = nullptr;
+  }
+  moe_dims d{};
+  d.hidden = (int)gate_.shape()[1];
+  d.inter = (int)experts_[0].w1().shape()[0];
+  d.num_experts = (int)NUM_EXPERTS;
+  d.top_k = (int)NUM_EXPERTS_PER_TOK;
+  d.max_tokens = max_tokens_;
+  check(moe_create(&d, &ctx_), "moe_create");
+  std::vector<const float *> w1(NUM_EXPERTS), w2(NUM_EXPERTS), w3(NUM_EXPERTS);
+  for (size_t e = 0; e < NUM_EXPERTS; ++e) {
+    w1[e] = experts_[e].w1().data();
+    w2[e] = experts_[e].w2().data();
+    w3[e] = experts_[e].w3().data();
+  }
+  check(moe_set_weights(ctx_, gate_.data(),
+                        expert_bias_.size() ? expert_bias_.data() : nullptr, w1.data(),
+                        w3.data(), w2.data(), 0, nullptr),
+        "moe_set_weights");
+}
+
+void SparseMoeBlock::forward_gpu(float *x, float *y, int batch, int seq_len,
+                                 int hidden_size, hipStream_t stream) {
+  forward_gpu(x, y, nullptr, batch, seq_len, hidden_size, stream);
+}
+
+void SparseMoeBlock::forward_gpu(float *x, float *y, const float *residual, int batch,
+                                 int seq_len, int hidden_size, hipStream_t stream) {
+  if (!ctx_) throw std::logic_error("SparseMoeBlock::forward_gpu before init_gpu");
+  if ((size_t)hidden_size != gate_.shape()[1])
+    throw std::invalid_argument("SparseMoeBlock::forward_gpu: hidden_size mismatch");
+  if (batch < 0 || seq_len < 0) throw std::invalid_argument("negative batch/seq_len");
+  check(moe_forward(ctx_, x, y, residual, batch * seq_len, stream), "moe_forward");
+}
+
+void SparseMoeBlock::forward(const Tensor &x, Tensor &y, Tensor &router_logits) {
+  if (!ctx_) throw std::logic_error("SparseMoeBlock::forward before init_gpu");
+  const size_t H = gate_.shape()[1];
+  if (x.ndim() < 1 || x.size() % H != 0)
+    throw std::invalid_argument("SparseMoeBlock::forward: x must be [T][hidden]");
+  const size_t T = x.size() / H;
+  y = Tensor({T, H});
+  router_logits = Tensor({T, NUM_EXPERTS});
+  if (T == 0) return;
+  DevBuf dx(T * H * sizeof(float)), dy(T * H * sizeof(float));
+  check_hip(hipMemcpy(dx.p, x.data(), T * H * sizeof(float), hipMemcpyHostToDevice),
+            "hipMemcpy");
+  check(moe_forward(ctx_, dx.f(), dy.f(), nullptr, (int)T, nullptr), "moe_forward");
+  check_hip(hipMemcpy(y.data(), dy.p, T * H * sizeof(float), hipMemcpyDeviceToHost),
+            "hipMemcpy");
+  check(moe_last_routing(ctx_, nullptr, nullptr, nullptr, router_logits.data(), nullptr),
+        "moe_last_routing");
+  check(moe_device_status(ctx_, nullptr), "device status");
+}
+
+void SparseMoeBlock::route_tokens(const Tensor &router_logits,
+                                  std::vector<int> &top_k_indices,
+                                  std::vector<float> &top_k_weights) {
+  if (!ctx_) throw std::logic_error("SparseMoeBlock::route_tokens before init_gpu");
+  if (router_logits.ndim() != 2 || router_logits.shape()[1] != NUM_EXPERTS)
+    throw std::invalid_argument("route_tokens: logits must be [T][32]");
+  const size_t T = router_logits.shape()[0];
+  top_k_indices.assign(T * NUM_EXPERTS_PER_TOK, -1);
+  top_k_weights.assign(T * NUM_EXPERTS_PER_TOK, 0.0f);
+  if (T == 0) return;
+  DevBuf dl(T * NUM_EXPERTS * sizeof(float));
+  check_hip(hipMemcpy(dl.p, router_logits.data(), T * NUM_EXPERTS * sizeof(float),
+                      hipMemcpyHostToDevice),
+            "hipMemcpy");
+  check(moe_route_logits(ctx_, dl.f(), (int)T, nullptr), "moe_route_logits");
+  check(moe_last_routing(ctx_, top_k_indices.data(), top_k_weights.data(), nullptr,
+                         nullptr, nullptr),
+        "moe_last_routing");
+}

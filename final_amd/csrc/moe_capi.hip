@@ -1,0 +1,444 @@
+// C-ABI of the MI355X sparse-MoE block (include/moe_capi.h).
+//
+// Host orchestration of SparseMoeBlock (reference src/layer.cu:1274-1503):
+// owns the repacked weights and the scratch, plans the expert kernel from the
+// token count and launches router + expert kernels on the caller's stream
+// with no host synchronisation.
+#include "moe_capi.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+#include <new>
+#include <vector>
+
+#include "moe_internal.h"
+
+using namespace moe;
+
+namespace {
+
+constexpr int kDefaultWaitLimit = 1 << 20;
+constexpr int kMaxTokensLimit = 1 << 20;
+
+// Switches to the context's device for the duration of a call.
+struct DeviceGuard {
+  int prev = -1;
+  bool ok = true;
+  explicit DeviceGuard(int dev) {
+    if (hipGetDevice(&prev) != hipSuccess) {
+      ok = false;
+      return;
+    }
+    if (prev != dev && hipSetDevice(dev) != hipSuccess) ok = false;
+  }
+  ~DeviceGuard() {
+    int cur = -1;
+    if (prev >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev)
+      (void)hipSetDevice(prev);
+  }
+};
+
+bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+struct moe_ctx {
+  moe_dims d{};
+  int device = 0;
+  int cus = 1;
+  int tile_override = -1;
+  int wait_div = 1;
+  bool weights_set = false;
+  bool has_bias = false;
+  int max_units = 0;
+  int grid[4] = {1, 1, 1, 1};  // plans 0, 32, 64, 128
+  // last routing state
+  int routed_T = -1;
+  int routed_plan = -1;
+  // device memory
+  float4 *gate4 = nullptr;
+  float *bias = nullptr;
+  float *w13 = nullptr;
+  float *w2 = nullptr;
+  Scratch s{};
+  std::vector<void *> allocs;
+};
+
+static int plan_index(int rows) {
+  switch (rows) {
+    case 0: return 0;
+    case 32: return 1;
+    case 64: return 2;
+    case 128: return 3;
+    default: return -1;
+  }
+}
+
+static int auto_plan(int T) {
+  if (T <= 64) return 0;
+  if (T < 512) return 32;
+  if (T < 2048) return 64;
+  return 128;
+}
+
+static int ctx_plan(const moe_ctx *ctx, int T) {
+  return ctx->tile_override >= 0 ? ctx->tile_override : auto_plan(T);
+}
+
+template <typename T>
+static int dev_alloc(moe_ctx *ctx, T **p, size_t count) {
+  void *v = nullptr;
+  if (hipMalloc(&v, count * sizeof(T) + 16) != hipSuccess) {
+    (void)hipGetLastError();
+    return MOE_ERR_OUT_OF_MEMORY;
+  }
+  ctx->allocs.push_back(v);
+  *p = static_cast<T *>(v);
+  return MOE_OK;
+}
+
+static void free_all(moe_ctx *ctx) {
+  for (void *p : ctx->allocs) (void)hipFree(p);
+  ctx->allocs.clear();
+}
+
+extern "C" {
+
+const char *moe_strerror(int status) {
+  switch (status) {
+    case MOE_OK: return "ok";
+    case MOE_ERR_INVALID_ARG: return "invalid argument";
+    case MOE_ERR_UNSUPPORTED: return "unsupported dimensions";
+    case MOE_ERR_HIP: return "HIP runtime error";
+    case MOE_ERR_OUT_OF_MEMORY: return "device out of memory";
+    case MOE_ERR_NOT_READY: return "weights not set";
+    case MOE_ERR_TOO_MANY_TOKENS: return "num_tokens exceeds max_tokens";
+    case MOE_ERR_DEVICE_TIMEOUT: return "device-side dependency wait expired";
+    case MOE_ERR_INTERNAL: return "inconsistent device dispatch plan";
+    default: return "unknown status";
+  }
+}
+
+const char *moe_version(void) { return "final_amd-moe 0.1.0 gfx950"; }
+
+int moe_create(const moe_dims *dims, moe_ctx **out) {
+  if (!dims || !out) return MOE_ERR_INVALID_ARG;
+  *out = nullptr;
+  const moe_dims d = *dims;
+  if (d.hidden <= 0 || d.inter <= 0 || d.max_tokens <= 0 ||
+      d.max_tokens > kMaxTokensLimit)
+    return MOE_ERR_INVALID_ARG;
+  if (d.num_experts != kExperts || d.top_k != kTopK || d.hidden % 256 != 0 ||
+      d.inter % 256 != 0)
+    return MOE_ERR_UNSUPPORTED;
+  moe_ctx *ctx = new (std::nothrow) moe_ctx();
+  if (!ctx) return MOE_ERR_OUT_OF_MEMORY;
+  ctx->d = d;
+  if (hipGetDevice(&ctx->device) != hipSuccess) {
+    delete ctx;
+    return MOE_ERR_HIP;
+  }
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, ctx->device) != hipSuccess) {
+    delete ctx;
+    return MOE_ERR_HIP;
+  }
+  ctx->cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
+  const size_t H = d.hidden, I = d.inter, E = kExperts;
+  const size_t Tm = d.max_tokens, S = Tm * kTopK;
+  const size_t nb = (Tm + kRouterTokens - 1) / kRouterTokens;
+  ctx->max_units = (int)(S / 32 + E + 1);
+  int rc = MOE_OK;
+  float *gate_f = nullptr;
+  if ((rc = dev_alloc(ctx, &gate_f, E * H)) ||
+      (rc = dev_alloc(ctx, &ctx->bias, E)) ||
+      (rc = dev_alloc(ctx, &ctx->w13, E * 2 * I * H)) ||
+      (rc = dev_alloc(ctx, &ctx->w2, E * H * I)) ||
+      (rc = dev_alloc(ctx, &ctx->s.logits, Tm * E)) ||
+      (rc = dev_alloc(ctx, &ctx->s.idx, S)) ||
+      (rc = dev_alloc(ctx, &ctx->s.wts, S)) ||
+      (rc = dev_alloc(ctx, &ctx->s.pos, S)) ||
+      (rc = dev_alloc(ctx, &ctx->s.blk, nb * E)) ||
+      (rc = dev_alloc(ctx, &ctx->s.slot_token, S)) ||
+      (rc = dev_alloc(ctx, &ctx->s.inter, S * I)) ||
+      (rc = dev_alloc(ctx, &ctx->s.sout, S * H))) {
+    free_all(ctx);
+    delete ctx;
+    return rc;
+  }
+  ctx->gate4 = reinterpret_cast<float4 *>(gate_f);
+  char *ctrl_mem = nullptr;
+  const size_t ctrl_bytes = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
+  if ((rc = dev_alloc(ctx, &ctrl_mem, ctrl_bytes))) {
+    free_all(ctx);
+    delete ctx;
+    return rc;
+  }
+  ctx->s.ctrl = reinterpret_cast<Ctrl *>(ctrl_mem);
+  ctx->s.dep = reinterpret_cast<int *>(ctrl_mem + sizeof(Ctrl));
+  if (hipMemset(ctrl_mem, 0, ctrl_bytes) != hipSuccess ||
+      hipDeviceSynchronize() != hipSuccess) {
+    free_all(ctx);
+    delete ctx;
+    return MOE_ERR_HIP;
+  }
+  for (int p = 0; p < 4; ++p) {
+    static const int rows[4] = {0, 32, 64, 128};
+    ctx->grid[p] = ctx->cus * expert_blocks_per_cu(rows[p]);
+  }
+  *out = ctx;
+  return MOE_OK;
+}
+
+int moe_destroy(moe_ctx *ctx) {
+  if (!ctx) return MOE_OK;
+  DeviceGuard g(ctx->device);
+  free_all(ctx);
+  delete ctx;
+  return MOE_OK;
+}
+
+int moe_set_weights(moe_ctx *ctx, const float *gate, const float *bias,
+                    const float *const *w1, const float *const *w3,
+                    const float *const *w2, int src_on_device,
+                    moe_stream_t stream) {
+  if (!ctx || !gate || !w1 || !w3 || !w2) return MOE_ERR_INVALID_ARG;
+  for (int e = 0; e < kExperts; ++e)
+    if (!w1[e] || !w3[e] || !w2[e]) return MOE_ERR_INVALID_ARG;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t H = ctx->d.hidden, I = ctx->d.inter, E = kExperts;
+  const hipMemcpyKind kind =
+      src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  float *stage = nullptr;  // [2][I][H] (or E*H for the gate) staging on device
+  const size_t stage_n = 2 * I * H > E * H ? 2 * I * H : E * H;
+  if (!src_on_device) {
+    if (hipMalloc(&stage, stage_n * sizeof(float)) != hipSuccess) {
+      (void)hipGetLastError();
+      return MOE_ERR_OUT_OF_MEMORY;
+    }
+  }
+  int rc = MOE_OK;
+  auto fail = [&](int code) {
+    rc = code;
+    return code;
+  };
+  do {
+    // gate -> [H/4][E] float4
+    const float *gsrc = gate;
+    if (!src_on_device) {
+      if (hipMemcpyAsync(stage, gate, E * H * sizeof(float), kind, st) != hipSuccess) {
+        fail(MOE_ERR_HIP);
+        break;
+      }
+      gsrc = stage;
+    }
+    if (launch_pack_gate(ctx->gate4, gsrc, (int)E, (int)H, st) != hipSuccess) {
+      fail(MOE_ERR_HIP);
+      break;
+    }
+    if (!src_on_device && hipStreamSynchronize(st) != hipSuccess) {
+      fail(MOE_ERR_HIP);
+      break;
+    }
+    ctx->has_bias = bias != nullptr;
+    if (bias && hipMemcpyAsync(ctx->bias, bias, E * sizeof(float), kind, st) != hipSuccess) {
+      fail(MOE_ERR_HIP);
+      break;
+    }
+    for (size_t e = 0; e < E && rc == MOE_OK; ++e) {
+      const float *s1 = w1[e], *s3 = w3[e];
+      if (!src_on_device) {
+        if (hipMemcpyAsync(stage, w1[e], I * H * sizeof(float), kind, st) != hipSuccess ||
+            hipMemcpyAsync(stage + I * H, w3[e], I * H * sizeof(float), kind, st) != hipSuccess) {
+          fail(MOE_ERR_HIP);
+          break;
+        }
+        s1 = stage;
+        s3 = stage + I * H;
+      }
+      if (launch_pack_w13(ctx->w13 + e * 2 * I * H, s1, s3, (int)H, (int)I, st) !=
+          hipSuccess) {
+        fail(MOE_ERR_HIP);
+        break;
+      }
+      if (hipMemcpyAsync(ctx->w2 + e * H * I, w2[e], H * I * sizeof(float), kind, st) !=
+          hipSuccess) {
+        fail(MOE_ERR_HIP);
+        break;
+      }
+      // the staging buffer is reused by the next expert
+      if (!src_on_device && hipStreamSynchronize(st) != hipSuccess) {
+        fail(MOE_ERR_HIP);
+        break;
+      }
+    }
+    if (rc == MOE_OK && hipStreamSynchronize(st) != hipSuccess) fail(MOE_ERR_HIP);
+  } while (0);
+  if (stage) (void)hipFree(stage);
+  if (rc == MOE_OK) ctx->weights_set = true;
+  return rc;
+}
+
+static int check_tokens(const moe_ctx *ctx, int T) {
+  if (T < 0) return MOE_ERR_INVALID_ARG;
+  if (T > ctx->d.max_tokens) return MOE_ERR_TOO_MANY_TOKENS;
+  return MOE_OK;
+}
+
+static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
+                    moe_stream_t stream) {
+  if (!ctx) return MOE_ERR_INVALID_ARG;
+  int rc = check_tokens(ctx, T);
+  if (rc) return rc;
+  if (!ctx->weights_set) return MOE_ERR_NOT_READY;
+  if (T == 0) {
+    ctx->routed_T = 0;
+    return MOE_OK;
+  }
+  if (logits ? !aligned16(logits) : (!x || !aligned16(x))) return MOE_ERR_INVALID_ARG;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  RouterArgs a{};
+  a.x = x;
+  a.logits_in = logits;
+  a.w.gate4 = ctx->gate4;
+  a.w.bias = ctx->has_bias ? ctx->bias : nullptr;
+  a.w.w13 = ctx->w13;
+  a.w.w2 = ctx->w2;
+  a.s = ctx->s;
+  a.T = T;
+  a.H = ctx->d.hidden;
+  a.inter = ctx->d.inter;
+  a.tile_rows = ctx_plan(ctx, T);
+  a.bn = expert_bn(a.tile_rows);
+  a.max_units = ctx->max_units;
+  if (launch_router(a, logits != nullptr, static_cast<hipStream_t>(stream)) != hipSuccess)
+    return MOE_ERR_HIP;
+  ctx->routed_T = T;
+  ctx->routed_plan = a.tile_rows;
+  return MOE_OK;
+}
+
+int moe_route(moe_ctx *ctx, const float *x, int num_tokens, moe_stream_t stream) {
+  return do_route(ctx, x, nullptr, num_tokens, stream);
+}
+
+int moe_route_logits(moe_ctx *ctx, const float *logits, int num_tokens,
+                     moe_stream_t stream) {
+  if (num_tokens > 0 && !logits) return MOE_ERR_INVALID_ARG;
+  return do_route(ctx, nullptr, logits, num_tokens, stream);
+}
+
+int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
+                int num_tokens, moe_stream_t stream) {
+  if (!ctx) return MOE_ERR_INVALID_ARG;
+  int rc = check_tokens(ctx, num_tokens);
+  if (rc) return rc;
+  if (!ctx->weights_set) return MOE_ERR_NOT_READY;
+  if (num_tokens == 0) return MOE_OK;
+  if (ctx->routed_T != num_tokens) return MOE_ERR_INVALID_ARG;
+  if (!x || !y || !aligned16(x) || !aligned16(y) || (residual && !aligned16(residual)))
+    return MOE_ERR_INVALID_ARG;
+  if (x == y) return MOE_ERR_INVALID_ARG;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  ExpertArgs a{};
+  a.x = x;
+  a.y = y;
+  a.residual = residual;
+  a.w.gate4 = ctx->gate4;
+  a.w.bias = ctx->has_bias ? ctx->bias : nullptr;
+  a.w.w13 = ctx->w13;
+  a.w.w2 = ctx->w2;
+  a.s = ctx->s;
+  a.T = num_tokens;
+  a.H = ctx->d.hidden;
+  a.I = ctx->d.inter;
+  a.wait_limit = kDefaultWaitLimit / (ctx->wait_div > 0 ? ctx->wait_div : 1);
+  if (a.wait_limit < 1) a.wait_limit = 1;
+  const int plan = ctx->routed_plan;
+  const int pi = plan_index(plan);
+  if (pi < 0) return MOE_ERR_INVALID_ARG;
+  if (launch_experts(a, plan, ctx->grid[pi], static_cast<hipStream_t>(stream)) != hipSuccess)
+    return MOE_ERR_HIP;
+  return MOE_OK;
+}
+
+int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
+                int num_tokens, moe_stream_t stream) {
+  int rc = moe_route(ctx, x, num_tokens, stream);
+  if (rc) return rc;
+  return moe_experts(ctx, x, y, residual, num_tokens, stream);
+}
+
+int moe_last_routing(moe_ctx *ctx, int *idx, float *w, int *counts, float *logits,
+                     moe_stream_t stream) {
+  if (!ctx) return MOE_ERR_INVALID_ARG;
+  if (ctx->routed_T < 0) return MOE_ERR_NOT_READY;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t T = (size_t)ctx->routed_T;
+  if (T == 0) {
+    if (counts) memset(counts, 0, sizeof(int) * kExperts);
+    return MOE_OK;
+  }
+  if (idx && hipMemcpyAsync(idx, ctx->s.idx, T * kTopK * sizeof(int),
+                            hipMemcpyDeviceToHost, st) != hipSuccess)
+    return MOE_ERR_HIP;
+  if (w && hipMemcpyAsync(w, ctx->s.wts, T * kTopK * sizeof(float),
+                          hipMemcpyDeviceToHost, st) != hipSuccess)
+    return MOE_ERR_HIP;
+  if (counts && hipMemcpyAsync(counts, ctx->s.ctrl->counts, kExperts * sizeof(int),
+                               hipMemcpyDeviceToHost, st) != hipSuccess)
+    return MOE_ERR_HIP;
+  if (logits && hipMemcpyAsync(logits, ctx->s.logits, T * kExperts * sizeof(float),
+                               hipMemcpyDeviceToHost, st) != hipSuccess)
+    return MOE_ERR_HIP;
+  if (hipStreamSynchronize(st) != hipSuccess) return MOE_ERR_HIP;
+  return MOE_OK;
+}
+
+int moe_device_status(moe_ctx *ctx, moe_stream_t stream) {
+  if (!ctx) return MOE_ERR_INVALID_ARG;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  int err = 0;
+  if (hipMemcpyAsync(&err, &ctx->s.ctrl->err, sizeof(int), hipMemcpyDeviceToHost, st) !=
+          hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return MOE_ERR_HIP;
+  if (err) {
+    const int zero = 0;
+    if (hipMemcpyAsync(&ctx->s.ctrl->err, &zero, sizeof(int), hipMemcpyHostToDevice, st) !=
+            hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+      return MOE_ERR_HIP;
+    return err == 1 ? MOE_ERR_DEVICE_TIMEOUT : MOE_ERR_INTERNAL;
+  }
+  return MOE_OK;
+}
+
+int moe_plan_tile_rows(const moe_ctx *ctx, int num_tokens) {
+  if (!ctx) return -1;
+  return ctx_plan(ctx, num_tokens);
+}
+
+int moe_force_tile_rows(moe_ctx *ctx, int rows) {
+  if (!ctx) return MOE_ERR_INVALID_ARG;
+  if (rows != -1 && plan_index(rows) < 0) return MOE_ERR_INVALID_ARG;
+  ctx->tile_override = rows;
+  return MOE_OK;
+}
+
+int moe_set_wait_divisor(moe_ctx *ctx, int divisor) {
+  if (!ctx || divisor < 1) return MOE_ERR_INVALID_ARG;
+  ctx->wait_div = divisor;
+  return MOE_OK;
+}
+
+}  // extern "C"

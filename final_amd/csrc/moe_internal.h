@@ -1,0 +1,102 @@
+// Internal layout shared by the HIP kernels (moe_kernels.hip) and the C-ABI
+// host code (moe_capi.hip).  Not installed; the public boundary is
+// include/moe_capi.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace moe {
+
+constexpr int kExperts = 32;     // NUM_EXPERTS, reference include/config.h:14
+constexpr int kTopK = 4;         // NUM_EXPERTS_PER_TOK, config.h:15
+constexpr int kRouterTokens = 64;  // tokens per router block (one wave of lanes)
+constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
+constexpr int kCombineTokens = 8;  // tokens per combine task
+constexpr int kStreamRowsPerWave = 4;   // weight rows per wave, streaming kernel
+constexpr int kStreamRows = kStreamRowsPerWave * 4;  // rows per streaming task
+constexpr int kStreamTokens = 8;  // token rows per streaming pass (LDS staged)
+
+// Device control block.  Filled by the last router block of a forward and
+// consumed by the expert kernel of the same forward.  All counters are reset
+// by that router block, so a forward needs no memset (and no host round trip).
+struct Ctrl {
+  int router_done;  // router blocks finished (last-block election)
+  int head;         // expert-kernel task queue head
+  int assign_done;  // dispatch (slot assignment) tasks finished
+  int p2_done;      // down-projection tasks finished
+  int err;          // sticky: 1 = a bounded wait expired
+  int num_tokens;
+  int tile_rows;    // 0 = streaming kernel, else MFMA rows per tile
+  int n_rblocks;    // router blocks = dispatch tasks
+  int n_p1;         // gate/up (W1,W3) tasks
+  int n_p2;         // down (W2) tasks
+  int n_comb;       // combine tasks
+  int n_total;      // sum of the four
+  int p1_per_unit;  // W1W3 tasks per m-tile (MFMA) or per expert (streaming)
+  int p2_per_unit;
+  int n_active;     // experts with count > 0
+  int pad_;
+  int counts[kExperts];
+  int offsets[kExperts + 1];
+  int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)
+  int active[kExperts];
+  // followed in memory by int dep[max_units]: W1W3 tasks finished per unit
+};
+
+struct Weights {
+  const float4 *gate4;   // [H/4][E] float4: gate[e][4k..4k+3] at [k][e]
+  const float *bias;     // [E] (may be null)
+  const float *w13;      // [E][I/32][2][32][H]: 32 rows of W1 then 32 of W3
+  const float *w2;       // [E][H][I]
+};
+
+struct Scratch {
+  float *logits;         // [Tmax][E]
+  int *idx;              // [Tmax][4]
+  float *wts;            // [Tmax][4]
+  int *pos;              // [Tmax][4]: local rank, then slot
+  int *blk;              // [Tmax/64][E]: block counts, then block bases
+  int *slot_token;       // [4 Tmax]
+  float *inter;          // [4 Tmax][I]
+  float *sout;           // [4 Tmax][H]
+  Ctrl *ctrl;
+  int *dep;              // [max_units]
+};
+
+struct RouterArgs {
+  const float *x;        // [T][H] (null when routing from logits)
+  const float *logits_in;  // [T][E] or null
+  Weights w;
+  Scratch s;
+  int T, H;
+  int tile_rows;         // plan: 0 streaming, else MFMA tile rows
+  int inter;             // I (for task counts)
+  int bn;                // MFMA n-tile width (columns of the B tile)
+  int max_units;
+};
+
+struct ExpertArgs {
+  const float *x;        // [T][H]
+  float *y;              // [T][H]
+  const float *residual; // [T][H] or null
+  Weights w;
+  Scratch s;
+  int T, H, I;
+  int wait_limit;        // bounded-wait iterations before giving up
+};
+
+// Launchers (moe_kernels.hip).  Return hipSuccess or the launch error.
+hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st);
+hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
+                          hipStream_t st);
+hipError_t launch_pack_w13(float *dst, const float *w1, const float *w3, int H,
+                           int I, hipStream_t st);
+hipError_t launch_pack_gate(float4 *dst, const float *gate, int E, int H,
+                            hipStream_t st);
+// Max resident blocks per CU of the expert kernel for a plan.
+int expert_blocks_per_cu(int tile_rows);
+// Columns of the B tile of the MFMA kernel for a plan.
+int expert_bn(int tile_rows);
+
+}  // namespace moe

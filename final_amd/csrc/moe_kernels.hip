@@ -1,0 +1,934 @@
+// HIP kernels of the MI355X (gfx950) sparse-MoE block.
+//
+// Two launches per forward:
+//   1. router_kernel   -- gate GEMM as fp32 FMA chains (bit-exact with the
+//      reference's attn_matmul_tiled_kernel, layer.cu:9-141), sigmoid with a
+//      double exp, top-4 insertion (layer.cu:439-499), per-block expert
+//      histogram and in-block ranks by wavefront ballots; the last block to
+//      finish scans the histograms and writes the expert kernel's task plan.
+//   2. expert kernel   -- persistent, one dynamic task queue with four phases:
+//      dispatch (slot assignment, replaces moe_scatter_kernel layer.cu:501-542
+//      without copying x), gate/up projection with SwiGLU epilogue
+//      (layer.cu:773-972), down projection (layer.cu:974-1126) and the weighted
+//      top-4 combine with the residual add (layer.cu:695-721, 1860-1880).
+//      Large T uses MFMA 32x32x2 f32 tiles (expert_mfma_kernel); small T streams
+//      weights through VALU dot products (expert_stream_kernel).
+//
+// Phase dependencies are counters in the control block.  Tasks are taken in
+// increasing order from one atomic head and a task only waits on tasks with a
+// smaller index, so the smallest unfinished task is always running and every
+// wait ends; each wait is still bounded and reports MOE_ERR_DEVICE_TIMEOUT
+// instead of spinning forever.
+#include "moe_internal.h"
+
+namespace moe {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// ---------------------------------------------------------------------------
+// Cross-block synchronisation (agent scope: coherent across the 8 XCD L2s)
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ int load_acquire(const int *p) {
+  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ int fetch_add(int *p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Block-wide: wait until *p >= target (thread 0 polls), then acquire.
+__device__ void block_wait(const int *p, int target, int limit, int *err) {
+  if (threadIdx.x == 0) {
+    int spins = 0;
+    while (load_acquire(p) < target) {
+      __builtin_amdgcn_s_sleep(2);
+      if (++spins > limit) {
+        __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+    }
+  }
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Block-wide: release every thread's global writes, then count one.
+__device__ void block_signal(int *p) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) fetch_add(p, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Router
+// ---------------------------------------------------------------------------
+
+// Exactly layer.cu:434: exp in double, add and IEEE divide in float.
+__device__ __forceinline__ float ref_sigmoid(float x) {
+#pragma clang fp contract(off)
+  const float e = (float)exp(-(double)x);
+  return 1.0f / (1.0f + e);
+}
+
+// One block = 64 tokens.  Lane map for the gate chains: e = tid % 32,
+// tokens (tid / 32) * 8 + j, j < 8: each lane runs 8 independent FMA chains.
+template <bool FROM_LOGITS>
+__global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
+#pragma clang fp contract(off)
+  __shared__ float s_score[kRouterTokens][kExperts + 1];
+  __shared__ float s_prob[kRouterTokens][kExperts + 1];
+  __shared__ int s_cnt[kExperts];
+  __shared__ int s_part[8][kExperts];
+  __shared__ int s_off[kExperts + 1];
+  __shared__ int s_last;
+  __shared__ int s_units;
+
+  const int tid = threadIdx.x;
+  const int b = blockIdx.x;
+  const int t0 = b * kRouterTokens;
+  const int T = a.T;
+  const int e = tid & (kExperts - 1);
+  const int g = tid >> 5;
+  Ctrl *ctrl = a.s.ctrl;
+
+  float lg[8];
+  if (!FROM_LOGITS) {
+    const int H4 = a.H >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+    const float4 *gp = a.w.gate4 + e;
+    const float4 *xr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      int tok = t0 + g * 8 + j;
+      tok = tok < T ? tok : T - 1;  // rows past T compute a copy, never stored
+      xr[j] = x4 + (size_t)tok * H4;
+      lg[j] = 0.0f;
+    }
+    // logits[t][e]: acc = fma(x[t][k], gate[e][k], acc), k = 0..H-1 ascending,
+    // the reference's per-output accumulation order (layer.cu:109-127).
+    for (int k4 = 0; k4 < H4; ++k4) {
+      const float4 gv = gp[(size_t)k4 * kExperts];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float4 xv = xr[j][k4];
+        lg[j] = __builtin_fmaf(xv.x, gv.x, lg[j]);
+        lg[j] = __builtin_fmaf(xv.y, gv.y, lg[j]);
+        lg[j] = __builtin_fmaf(xv.z, gv.z, lg[j]);
+        lg[j] = __builtin_fmaf(xv.w, gv.w, lg[j]);
+      }
+    }
+  }
+  const float bias_e = a.w.bias ? a.w.bias[e] : 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int tl = g * 8 + j;
+    const int tok = t0 + tl;
+    float l;
+    if (FROM_LOGITS) {
+      l = tok < T ? a.logits_in[(size_t)tok * kExperts + e] : 0.0f;
+    } else {
+      l = lg[j];
+    }
+    if (tok < T) a.s.logits[(size_t)tok * kExperts + e] = l;
+    const float p = ref_sigmoid(l);
+    s_prob[tl][e] = p;
+    s_score[tl][e] = p + bias_e;  // layer.cu:462
+  }
+  __syncthreads();
+
+  if (tid < kRouterTokens) {  // wave 0: lane = token of the block
+    const int tl = tid;
+    const int tok = t0 + tl;
+    const bool valid = tok < T;
+    float ms[kTopK], mp[kTopK];
+    int mi[kTopK];
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i) {
+      ms[i] = -1e30f;
+      mp[i] = 0.0f;
+      mi[i] = -1;
+    }
+    // Insertion with strict '>' (layer.cu:465-476): rank order is score
+    // descending, lower expert index first among equal scores.
+    for (int ee = 0; ee < kExperts; ++ee) {
+      const float score = s_score[tl][ee];
+      const float prob = s_prob[tl][ee];
+      if (score > ms[3]) {
+        if (score > ms[2]) {
+          ms[3] = ms[2]; mp[3] = mp[2]; mi[3] = mi[2];
+          if (score > ms[1]) {
+            ms[2] = ms[1]; mp[2] = mp[1]; mi[2] = mi[1];
+            if (score > ms[0]) {
+              ms[1] = ms[0]; mp[1] = mp[0]; mi[1] = mi[0];
+              ms[0] = score; mp[0] = prob; mi[0] = ee;
+            } else {
+              ms[1] = score; mp[1] = prob; mi[1] = ee;
+            }
+          } else {
+            ms[2] = score; mp[2] = prob; mi[2] = ee;
+          }
+        } else {
+          ms[3] = score; mp[3] = prob; mi[3] = ee;
+        }
+      }
+    }
+    float sum = 0.0f;  // layer.cu:480-482, rank order
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i) sum += mp[i];
+    const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;  // layer.cu:484
+    if (valid) {
+#pragma unroll
+      for (int i = 0; i < kTopK; ++i) {
+        a.s.idx[(size_t)tok * kTopK + i] = mi[i];
+        a.s.wts[(size_t)tok * kTopK + i] = mp[i] * scale * 1.0f;  // :489
+      }
+    }
+    // In-block rank of this token among the block's tokens that chose ee:
+    // a 64-lane ballot per expert (deterministic, no atomics).
+    int rank[kTopK] = {-1, -1, -1, -1};
+    const unsigned long long below = (1ull << tl) - 1ull;
+    for (int ee = 0; ee < kExperts; ++ee) {
+      const bool sel = valid && (mi[0] == ee || mi[1] == ee || mi[2] == ee ||
+                                 mi[3] == ee);
+      const unsigned long long m = __ballot(sel);
+      if (sel) {
+        const int r = __popcll(m & below);
+#pragma unroll
+        for (int i = 0; i < kTopK; ++i)
+          if (mi[i] == ee) rank[i] = r;
+      }
+      if (tl == 0) s_cnt[ee] = __popcll(m);
+    }
+    if (valid) {
+#pragma unroll
+      for (int i = 0; i < kTopK; ++i) a.s.pos[(size_t)tok * kTopK + i] = rank[i];
+    }
+  }
+  __syncthreads();
+  if (tid < kExperts) a.s.blk[b * kExperts + tid] = s_cnt[tid];
+
+  // ---- last-block election: the block that finishes last builds the plan --
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (tid == 0) s_last = (fetch_add(&ctrl->router_done, 1) == (int)gridDim.x - 1);
+  __syncthreads();
+  if (!s_last) return;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+
+  const int nb = gridDim.x;
+  const int part = tid >> 5;  // 8 parts x 32 experts
+  const int per = (nb + 7) / 8;
+  const int lo = part * per;
+  const int hi = min(nb, lo + per);
+  {
+    int sum = 0;
+    for (int bb = lo; bb < hi; ++bb) sum += a.s.blk[bb * kExperts + e];
+    s_part[part][e] = sum;
+  }
+  __syncthreads();
+  if (tid < kExperts) {
+    int run = 0;
+    for (int p = 0; p < 8; ++p) {
+      const int v = s_part[p][tid];
+      s_part[p][tid] = run;
+      run += v;
+    }
+    s_cnt[tid] = run;
+  }
+  __syncthreads();
+  if (tid == 0) {  // exclusive scan over experts (layer.cu:737-760)
+    int run = 0;
+    for (int ee = 0; ee < kExperts; ++ee) {
+      s_off[ee] = run;
+      run += s_cnt[ee];
+    }
+    s_off[kExperts] = run;
+  }
+  __syncthreads();
+  {
+    // block bases: offsets[e] + tokens of e in earlier router blocks
+    int base = s_off[e] + s_part[part][e];
+    for (int bb = lo; bb < hi; ++bb) {
+      const int c = a.s.blk[bb * kExperts + e];
+      a.s.blk[bb * kExperts + e] = base;
+      base += c;
+    }
+  }
+  if (tid < kExperts) ctrl->counts[tid] = s_cnt[tid];
+  if (tid <= kExperts) ctrl->offsets[tid] = s_off[tid];
+  if (tid == 0) {
+    const int tr = a.tile_rows;
+    int units = 0, nact = 0;
+    for (int ee = 0; ee < kExperts; ++ee) {
+      ctrl->unit_off[ee] = units;
+      const int c = s_cnt[ee];
+      if (c > 0) ctrl->active[nact++] = ee;
+      units += tr > 0 ? (c + tr - 1) / tr : (c > 0 ? 1 : 0);
+    }
+    ctrl->unit_off[kExperts] = units;
+    for (int i = nact; i < kExperts; ++i) ctrl->active[i] = -1;
+    ctrl->n_active = nact;
+    const int p1u = tr > 0 ? a.inter / (a.bn / 2) : a.inter / (kStreamRows / 2);
+    const int p2u = tr > 0 ? a.H / a.bn : a.H / kStreamRows;
+    ctrl->p1_per_unit = p1u;
+    ctrl->p2_per_unit = p2u;
+    ctrl->n_rblocks = nb;
+    ctrl->n_p1 = units * p1u;
+    ctrl->n_p2 = units * p2u;
+    ctrl->n_comb = (T + kCombineTokens - 1) / kCombineTokens;
+    ctrl->n_total = nb + units * p1u + units * p2u + ctrl->n_comb;
+    ctrl->num_tokens = T;
+    ctrl->tile_rows = tr;
+    ctrl->head = 0;
+    ctrl->assign_done = 0;
+    ctrl->p2_done = 0;
+    s_units = units;
+  }
+  __syncthreads();
+  const int units = min(s_units, a.max_units);
+  for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
+  if (tid == 0) ctrl->router_done = 0;  // every block has counted in
+}
+
+// ---------------------------------------------------------------------------
+// Expert kernel building blocks
+// ---------------------------------------------------------------------------
+
+// Dispatch task q: slots of the 64 tokens of router block q (replaces
+// moe_scatter_kernel layer.cu:501-542: slot = block base + in-block rank, so
+// slots are stable by token; x itself is not copied, the GEMM gathers rows).
+__device__ void assign_task(const ExpertArgs &a, int q) {
+  const int tl = threadIdx.x >> 2, k = threadIdx.x & 3;
+  const int tok = q * kRouterTokens + tl;
+  if (tok < a.T) {
+    const int ee = a.s.idx[(size_t)tok * kTopK + k];
+    if (ee >= 0 && ee < kExperts) {
+      const int slot = a.s.blk[q * kExperts + ee] + a.s.pos[(size_t)tok * kTopK + k];
+      if (slot >= 0 && slot < a.T * kTopK) {
+        a.s.pos[(size_t)tok * kTopK + k] = slot;
+        a.s.slot_token[slot] = tok;
+      } else {  // inconsistent plan: flag it, never write out of range
+        a.s.pos[(size_t)tok * kTopK + k] = -1;
+        __hip_atomic_store(&a.s.ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      a.s.pos[(size_t)tok * kTopK + k] = -1;
+    }
+  }
+}
+
+// Combine task q: tokens [8q, 8q+8).  y = residual + sum_k w_k * out_k with
+// the reference's order: sum from 0.0f, fma over k ascending
+// (layer.cu:708-720), then the residual add (layer.cu:1866-1871).
+__device__ void combine_task(const ExpertArgs &a, int q) {
+#pragma clang fp contract(off)
+  const int H4 = a.H >> 2;
+  const int n = kCombineTokens * H4;
+  const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
+  const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
+  float4 *y4 = reinterpret_cast<float4 *>(a.y);
+  for (int f = threadIdx.x; f < n; f += kThreads) {
+    const int tok = q * kCombineTokens + f / H4;
+    const int c4 = f % H4;
+    if (tok >= a.T) break;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+      const int slot = a.s.pos[(size_t)tok * kTopK + k];
+      if (slot >= 0 && slot < a.T * kTopK) {
+        const float wk = a.s.wts[(size_t)tok * kTopK + k];
+        const float4 v = so[(size_t)slot * H4 + c4];
+        acc.x = __builtin_fmaf(v.x, wk, acc.x);
+        acc.y = __builtin_fmaf(v.y, wk, acc.y);
+        acc.z = __builtin_fmaf(v.z, wk, acc.z);
+        acc.w = __builtin_fmaf(v.w, wk, acc.w);
+      }
+    }
+    if (r4) {
+      const float4 r = r4[(size_t)tok * H4 + c4];
+      acc.x = r.x + acc.x;
+      acc.y = r.y + acc.y;
+      acc.z = r.z + acc.z;
+      acc.w = r.w + acc.w;
+    }
+    y4[(size_t)tok * H4 + c4] = acc;
+  }
+}
+
+// Token of a slot, clamped into [0, T) so a bad plan can never address
+// outside x (the dispatch guards flag such plans in ctrl->err).
+__device__ __forceinline__ int slot_tok(const ExpertArgs &a, int slot) {
+  const int t = a.s.slot_token[slot];
+  return t < 0 ? 0 : (t >= a.T ? a.T - 1 : t);
+}
+
+// layer.cu:728 d_silu_opt.
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
+
+// Expert owning unit u: the largest e with unit_off[e] <= u (skips experts
+// without units, whose unit_off equals the next one's).
+__device__ __forceinline__ int unit_expert(const int *unit_off, int u) {
+  int lo = 0, hi = kExperts;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (unit_off[mid] <= u) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+// ---------------------------------------------------------------------------
+// MFMA grouped GEMM tile
+// ---------------------------------------------------------------------------
+
+template <int BM> struct TileCfg;
+// 4 waves as WAVES_M x WAVES_N; a wave owns WM 32-row blocks x 2 32-column
+// blocks (for the gate/up phase: 32 columns of W1 and the same 32 of W3).
+template <> struct TileCfg<128> {
+  static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, BK = 32;
+};
+template <> struct TileCfg<64> {
+  static constexpr int WAVES_M = 1, WM = 2, WAVES_N = 4, BK = 16;
+};
+template <> struct TileCfg<32> {
+  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, BK = 16;
+};
+
+template <int BM> struct Tile {
+  using C = TileCfg<BM>;
+  static constexpr int WAVES_M = C::WAVES_M, WM = C::WM, WAVES_N = C::WAVES_N;
+  static constexpr int BK = C::BK;
+  static constexpr int BN = WAVES_N * 64;
+  static constexpr int PITCH = BK + 4;           // floats per LDS row
+  static constexpr int KV = BK / 4;              // float4 per row per slab
+  static constexpr int A_F4 = BM * KV;           // float4 per A slab
+  static constexpr int B_F4 = BN * KV;
+  static constexpr int A_PER = (A_F4 + kThreads - 1) / kThreads;
+  static constexpr int B_PER = (B_F4 + kThreads - 1) / kThreads;
+  static constexpr int CPITCH = BN + 8;          // epilogue tile row pitch
+  static constexpr int SLAB_FLOATS = 2 * (BM + BN) * PITCH;
+  static constexpr int EPI_FLOATS = BM * CPITCH;
+  static constexpr int LDS_FLOATS = SLAB_FLOATS > EPI_FLOATS ? SLAB_FLOATS : EPI_FLOATS;
+  static_assert(BM == WAVES_M * WM * 32, "tile rows");
+  static_assert(BK % 8 == 0, "k groups of 8");
+};
+
+// One output tile of C[rows][cols] = A[rows][K] . B[cols][K]^T.
+// A rows are gathered: row r starts at abase + aoff[r] (aoff in LDS; rows at
+// or past rows_valid are zero).  B rows are contiguous with stride K from
+// brow0.  GATED: per wave the B tile holds 32 rows of W1 then the same 32 of
+// W3 and the epilogue writes silu(W1 x) * (W3 x); otherwise the product.
+//
+// Slab pipeline: global loads of slab s+1 are in flight while the MFMAs of
+// slab s run from LDS; one barrier per slab (double-buffered LDS).
+template <int BM, bool GATED>
+__device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
+                                          const int *aoff, int rows_valid,
+                                          const float *brow0, int K, float *out,
+                                          int ldo, int col0) {
+  using TL = Tile<BM>;
+  constexpr int WM = TL::WM, BK = TL::BK, PITCH = TL::PITCH, KV = TL::KV;
+  constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
+  constexpr int ROWS_PER_PASS = kThreads / KV;  // rows one pass of loads covers
+  static_assert(TL::B_F4 % kThreads == 0, "B slab splits evenly");
+  float *As = lds;                      // [2][BM][PITCH]
+  float *Bs = lds + 2 * BM * PITCH;     // [2][BN][PITCH]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % TL::WAVES_M, wn = wave / TL::WAVES_M;
+  const int lrow = tid / KV, lc4 = (tid % KV) * 4;
+
+  int a_src[A_PER];  // element offset of this thread's A float4, -1 = zero
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i) {
+    const int r = lrow + i * ROWS_PER_PASS;
+    a_src[i] = (r < BM && r < rows_valid) ? aoff[r] + lc4 : -1;
+  }
+  const float *bsrc = brow0 + (size_t)lrow * K + lc4;
+  const int lds_st = lrow * PITCH + lc4;
+
+  float4 ra[A_PER], rb[B_PER];
+#define MOE_LOAD_SLAB(k0)                                                      \
+  do {                                                                         \
+    _Pragma("unroll") for (int i = 0; i < A_PER; ++i) ra[i] =                  \
+        a_src[i] >= 0 ? *reinterpret_cast<const float4 *>(abase + a_src[i] + (k0)) \
+                      : make_float4(0.f, 0.f, 0.f, 0.f);                       \
+    _Pragma("unroll") for (int i = 0; i < B_PER; ++i) rb[i] =                  \
+        *reinterpret_cast<const float4 *>(bsrc + (size_t)i * ROWS_PER_PASS * K + (k0)); \
+  } while (0)
+#define MOE_STORE_SLAB(buf)                                                    \
+  do {                                                                         \
+    _Pragma("unroll") for (int i = 0; i < A_PER; ++i) if (lrow + i * ROWS_PER_PASS < BM) \
+        *reinterpret_cast<float4 *>(As + (buf) * BM * PITCH + lds_st +         \
+                                    i * ROWS_PER_PASS * PITCH) = ra[i];        \
+    _Pragma("unroll") for (int i = 0; i < B_PER; ++i)                          \
+        *reinterpret_cast<float4 *>(Bs + (buf) * TL::BN * PITCH + lds_st +     \
+                                    i * ROWS_PER_PASS * PITCH) = rb[i];        \
+  } while (0)
+
+  floatx16 acc[WM][2];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.0f;
+
+  // Rows of this wave that hold data: 0 = skip the MFMAs, <= 32 with WM == 2
+  // = only the first row block (wave-uniform branches).
+  const int wrow0 = wm * WM * 32;
+  const int wrows = min(max(rows_valid - wrow0, 0), WM * 32);
+
+  const int nslab = K / BK;
+  MOE_LOAD_SLAB(0);
+  MOE_STORE_SLAB(0);
+  __syncthreads();
+  const int lr = lane & 31, lh = (lane >> 5) * 4;
+  const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
+  const float *b_rd = Bs + (wn * 64 + lr) * PITCH + lh;
+  for (int s = 0; s < nslab; ++s) {
+    const int cur = s & 1;
+    if (s + 1 < nslab) MOE_LOAD_SLAB((s + 1) * BK);
+    const float *Ac = a_rd + cur * BM * PITCH;
+    const float *Bc = b_rd + cur * TL::BN * PITCH;
+    if (wrows > 0) {
+#pragma unroll
+      for (int g8 = 0; g8 < BK / 8; ++g8) {
+        float4 af[WM], bf[2];
+#pragma unroll
+        for (int i = 0; i < WM; ++i)
+          af[i] = *reinterpret_cast<const float4 *>(Ac + i * 32 * PITCH + g8 * 8);
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+          bf[c] = *reinterpret_cast<const float4 *>(Bc + c * 32 * PITCH + g8 * 8);
+#pragma unroll
+        for (int i = 0; i < WM; ++i) {
+          if (i > 0 && wrows <= 32) break;
+#pragma unroll
+          for (int c = 0; c < 2; ++c) {
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].x, bf[c].x, acc[i][c], 0, 0, 0);
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].y, bf[c].y, acc[i][c], 0, 0, 0);
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].z, bf[c].z, acc[i][c], 0, 0, 0);
+            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].w, bf[c].w, acc[i][c], 0, 0, 0);
+          }
+        }
+      }
+    }
+    if (s + 1 < nslab) MOE_STORE_SLAB(cur ^ 1);
+    __syncthreads();
+  }
+#undef MOE_LOAD_SLAB
+#undef MOE_STORE_SLAB
+
+  // Epilogue through LDS (the slab buffers are free after the last barrier):
+  // results are written as a [BM][NC] tile, then stored as whole-row float4s.
+  // 32x32 f32 MFMA result layout: lane l holds column l % 32 and rows
+  // 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
+  constexpr int NC = GATED ? TL::BN / 2 : TL::BN;  // output columns of the tile
+  constexpr int CP = TL::CPITCH;
+  float *Cs = lds;
+  if (wrows > 0) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wrow0 + i * 32 + 8 * (r >> 2) + (lane >> 5) * 4 + (r & 3);
+        if (GATED) {
+          Cs[row * CP + wn * 32 + lr] = silu(acc[i][0][r]) * acc[i][1][r];
+        } else {
+          Cs[row * CP + wn * 64 + lr] = acc[i][0][r];
+          Cs[row * CP + wn * 64 + 32 + lr] = acc[i][1][r];
+        }
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int NC4 = NC / 4;
+  for (int f = tid; f < BM * NC4; f += kThreads) {
+    const int row = f / NC4, c4 = (f % NC4) * 4;
+    if (row < rows_valid)
+      *reinterpret_cast<float4 *>(out + (size_t)row * ldo + col0 + c4) =
+          *reinterpret_cast<const float4 *>(Cs + row * CP + c4);
+  }
+  __syncthreads();  // Cs aliases the slab buffers of the next tile
+}
+
+template <int BM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void expert_mfma_kernel(ExpertArgs a) {
+  using TL = Tile<BM>;
+  extern __shared__ float lds[];
+  __shared__ int s_task;
+  __shared__ int s_unit_off[kExperts + 1];
+  __shared__ int s_offsets[kExperts + 1];
+  __shared__ int s_counts[kExperts];
+  __shared__ int s_aoff[BM];
+  Ctrl *c = a.s.ctrl;
+  const int tid = threadIdx.x;
+  if (tid <= kExperts) {
+    s_unit_off[tid] = c->unit_off[tid];
+    s_offsets[tid] = c->offsets[tid];
+  }
+  if (tid < kExperts) s_counts[tid] = c->counts[tid];
+  const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
+  const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
+  const int H = a.H, I = a.I;
+  if (tid == 0) s_task = fetch_add(&c->head, 1);
+  __syncthreads();
+  int task = s_task;
+  while (task < ntot) {
+    int next = 0;
+    if (tid == 0) next = fetch_add(&c->head, 1);  // claim ahead
+    if (task < nb) {
+      assign_task(a, task);
+      block_signal(&c->assign_done);
+    } else if (task < nb + n1) {
+      const int q = task - nb;
+      const int u = q / p1u, nt = q % p1u;
+      const int e = unit_expert(s_unit_off, u);
+      const int m0 = (u - s_unit_off[e]) * BM;
+      const int rows = min(BM, s_counts[e] - m0);
+      const int slot0 = s_offsets[e] + m0;
+      block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
+      if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
+      __syncthreads();
+      const float *brow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TL::BN) * H;
+      mfma_tile<BM, true>(lds, a.x, s_aoff, rows, brow0, H,
+                          a.s.inter + (size_t)slot0 * I, I, nt * (TL::BN / 2));
+      block_signal(&a.s.dep[u]);
+    } else if (task < nb + n1 + n2) {
+      const int q = task - nb - n1;
+      const int u = q / p2u, ht = q % p2u;
+      const int e = unit_expert(s_unit_off, u);
+      const int m0 = (u - s_unit_off[e]) * BM;
+      const int rows = min(BM, s_counts[e] - m0);
+      const int slot0 = s_offsets[e] + m0;
+      block_wait(&a.s.dep[u], p1u, a.wait_limit, &c->err);
+      if (tid < BM) s_aoff[tid] = tid < rows ? tid * I : -1;
+      __syncthreads();
+      const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
+      mfma_tile<BM, false>(lds, a.s.inter + (size_t)slot0 * I, s_aoff, rows, brow0, I,
+                           a.s.sout + (size_t)slot0 * H, H, ht * TL::BN);
+      block_signal(&c->p2_done);
+    } else {
+      const int q = task - nb - n1 - n2;
+      block_wait(&c->p2_done, n2, a.wait_limit, &c->err);
+      combine_task(a, q);
+    }
+    __syncthreads();
+    if (tid == 0) s_task = next;
+    __syncthreads();
+    task = s_task;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Weight-streaming kernel (small T): every weight byte is read once, as
+// coalesced 1 KiB wave loads; dot products on VALU against token rows staged
+// in LDS, then a wave butterfly reduction.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// rows[r] (r < 4): this wave's weight rows, length K (K % 256 == 0).
+// xs: [ntok][K] staged token rows.  acc[r][m] = rows[r] . xs[m].
+__device__ __forceinline__ void stream_dots(const float *const rows[kStreamRowsPerWave],
+                                            const float *xs, int K, int ntok,
+                                            float acc[kStreamRowsPerWave][kStreamTokens]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kStreamRowsPerWave; ++r)
+#pragma unroll
+    for (int m = 0; m < kStreamTokens; ++m) acc[r][m] = 0.0f;
+  const int nch = K >> 8;
+  for (int c0 = 0; c0 < nch; c0 += 8) {
+    float4 wv[kStreamRowsPerWave][8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+      for (int r = 0; r < kStreamRowsPerWave; ++r)
+        if (c0 + c < nch)
+          wv[r][c] = *reinterpret_cast<const float4 *>(rows[r] + (c0 + c) * 256 + lane * 4);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      if (c0 + c >= nch) break;
+#pragma unroll
+      for (int m = 0; m < kStreamTokens; ++m) {
+        if (m >= ntok) break;
+        const float4 xv =
+            *reinterpret_cast<const float4 *>(xs + (size_t)m * K + (c0 + c) * 256 + lane * 4);
+#pragma unroll
+        for (int r = 0; r < kStreamRowsPerWave; ++r) {
+          acc[r][m] = __builtin_fmaf(wv[r][c].x, xv.x, acc[r][m]);
+          acc[r][m] = __builtin_fmaf(wv[r][c].y, xv.y, acc[r][m]);
+          acc[r][m] = __builtin_fmaf(wv[r][c].z, xv.z, acc[r][m]);
+          acc[r][m] = __builtin_fmaf(wv[r][c].w, xv.w, acc[r][m]);
+        }
+      }
+    }
+  }
+}
+
+// Stage up to kStreamTokens rows (row_of[m], length K) into xs.
+__device__ __forceinline__ void stage_rows(float *xs, const float *const *row_of,
+                                           int ntok, int K) {
+  const int K4 = K >> 2;
+  float4 *d = reinterpret_cast<float4 *>(xs);
+  for (int f = threadIdx.x; f < ntok * K4; f += kThreads) {
+    const int m = f / K4, c4 = f % K4;
+    d[f] = reinterpret_cast<const float4 *>(row_of[m])[c4];
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void expert_stream_kernel(ExpertArgs a) {
+  extern __shared__ float xs[];  // [kStreamTokens][max(H, I)]
+  __shared__ int s_task;
+  __shared__ const float *s_row[kStreamTokens];
+  Ctrl *c = a.s.ctrl;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
+  const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
+  const int H = a.H, I = a.I;
+  if (tid == 0) s_task = fetch_add(&c->head, 1);
+  __syncthreads();
+  int task = s_task;
+  while (task < ntot) {
+    int next = 0;
+    if (tid == 0) next = fetch_add(&c->head, 1);
+    if (task < nb) {
+      assign_task(a, task);
+      block_signal(&c->assign_done);
+    } else if (task < nb + n1) {
+      // gate/up: 8 consecutive n of one expert; wave w owns n0+2w, n0+2w+1
+      const int q = task - nb;
+      const int u = q / p1u, ch = q % p1u;
+      const int e = c->active[u];
+      const int cnt = c->counts[e], slot0 = c->offsets[e];
+      const int n = ch * (kStreamRows / 2) + wave * 2;
+      const float *wb = a.w.w13 + (size_t)e * 2 * I * H;
+      const float *rows[kStreamRowsPerWave];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int nn = n + j;
+        const size_t prow = (size_t)(nn >> 5) * 64 + (nn & 31);
+        rows[j] = wb + prow * H;             // W1 row nn
+        rows[2 + j] = wb + (prow + 32) * H;  // W3 row nn
+      }
+      block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
+      for (int m0 = 0; m0 < cnt; m0 += kStreamTokens) {
+        const int nt = min(kStreamTokens, cnt - m0);
+        if (tid < nt) s_row[tid] = a.x + (size_t)slot_tok(a, slot0 + m0 + tid) * H;
+        __syncthreads();
+        stage_rows(xs, s_row, nt, H);
+        __syncthreads();
+        float acc[kStreamRowsPerWave][kStreamTokens];
+        stream_dots(rows, xs, H, nt, acc);
+#pragma unroll
+        for (int m = 0; m < kStreamTokens; ++m) {
+          if (m >= nt) break;
+          const float h1a = wave_sum(acc[0][m]), h1b = wave_sum(acc[1][m]);
+          const float h3a = wave_sum(acc[2][m]), h3b = wave_sum(acc[3][m]);
+          if (lane == 0) {
+            float *irow = a.s.inter + (size_t)(slot0 + m0 + m) * I;
+            irow[n] = silu(h1a) * h3a;
+            irow[n + 1] = silu(h1b) * h3b;
+          }
+        }
+        __syncthreads();
+      }
+      block_signal(&a.s.dep[u]);
+    } else if (task < nb + n1 + n2) {
+      // down: 16 consecutive rows h of W2[e]; wave w owns h0+4w .. h0+4w+3
+      const int q = task - nb - n1;
+      const int u = q / p2u, ch = q % p2u;
+      const int e = c->active[u];
+      const int cnt = c->counts[e], slot0 = c->offsets[e];
+      const int h = ch * kStreamRows + wave * kStreamRowsPerWave;
+      const float *rows[kStreamRowsPerWave];
+#pragma unroll
+      for (int r = 0; r < kStreamRowsPerWave; ++r)
+        rows[r] = a.w.w2 + ((size_t)e * H + h + r) * I;
+      block_wait(&a.s.dep[u], p1u, a.wait_limit, &c->err);
+      for (int m0 = 0; m0 < cnt; m0 += kStreamTokens) {
+        const int nt = min(kStreamTokens, cnt - m0);
+        if (tid < nt) s_row[tid] = a.s.inter + (size_t)(slot0 + m0 + tid) * I;
+        __syncthreads();
+        stage_rows(xs, s_row, nt, I);
+        __syncthreads();
+        float acc[kStreamRowsPerWave][kStreamTokens];
+        stream_dots(rows, xs, I, nt, acc);
+#pragma unroll
+        for (int m = 0; m < kStreamTokens; ++m) {
+          if (m >= nt) break;
+          float v[kStreamRowsPerWave];
+#pragma unroll
+          for (int r = 0; r < kStreamRowsPerWave; ++r) v[r] = wave_sum(acc[r][m]);
+          if (lane == 0) {
+            float4 *o = reinterpret_cast<float4 *>(a.s.sout + (size_t)(slot0 + m0 + m) * H + h);
+            *o = make_float4(v[0], v[1], v[2], v[3]);
+          }
+        }
+        __syncthreads();
+      }
+      block_signal(&c->p2_done);
+    } else {
+      const int q = task - nb - n1 - n2;
+      block_wait(&c->p2_done, n2, a.wait_limit, &c->err);
+      combine_task(a, q);
+    }
+    __syncthreads();
+    if (tid == 0) s_task = next;
+    __syncthreads();
+    task = s_task;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Weight packing (once per set_weights)
+// ---------------------------------------------------------------------------
+
+// dst [I/32][2][32][H] from w1, w3 [I][H] of one expert.
+__global__ void pack_w13_kernel(float4 *dst, const float4 *w1, const float4 *w3,
+                                int H4, int I) {
+  const size_t n = (size_t)2 * I * H4;
+  for (size_t f = blockIdx.x * (size_t)blockDim.x + threadIdx.x; f < n;
+       f += (size_t)gridDim.x * blockDim.x) {
+    const size_t prow = f / H4, c4 = f % H4;
+    const size_t g = prow / 64, w = (prow % 64) / 32, j = prow % 32;
+    const size_t srow = g * 32 + j;
+    dst[f] = (w == 0 ? w1 : w3)[srow * H4 + c4];
+  }
+}
+
+// dst[k4][e] = gate[e][4k4 .. 4k4+3]
+__global__ void pack_gate_kernel(float4 *dst, const float4 *gate, int E, int H4) {
+  const int n = E * H4;
+  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < n;
+       f += gridDim.x * blockDim.x) {
+    const int k4 = f / E, e = f % E;
+    dst[f] = gate[(size_t)e * H4 + k4];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Launchers
+// ---------------------------------------------------------------------------
+
+hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) {
+  const int nb = (a.T + kRouterTokens - 1) / kRouterTokens;
+  if (from_logits)
+    hipLaunchKernelGGL(router_kernel<true>, dim3(nb), dim3(kThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(router_kernel<false>, dim3(nb), dim3(kThreads), 0, st, a);
+  return hipGetLastError();
+}
+
+static size_t stream_lds_bytes(int H, int I) {
+  return (size_t)kStreamTokens * (size_t)(H > I ? H : I) * sizeof(float);
+}
+
+template <int BM> static void *mfma_fn() {
+  return reinterpret_cast<void *>(&expert_mfma_kernel<BM>);
+}
+
+static hipError_t ensure_lds_attr(const void *fn, size_t bytes) {
+  if (bytes <= 65536) return hipSuccess;
+  return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)bytes);
+}
+
+hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
+                          hipStream_t st) {
+  hipError_t err = hipSuccess;
+  switch (tile_rows) {
+    case 0: {
+      const size_t lds = stream_lds_bytes(a.H, a.I);
+      err = ensure_lds_attr(reinterpret_cast<const void *>(&expert_stream_kernel), lds);
+      if (err != hipSuccess) return err;
+      hipLaunchKernelGGL(expert_stream_kernel, dim3(grid), dim3(kThreads), lds, st, a);
+      break;
+    }
+    case 32: {
+      const size_t lds = Tile<32>::LDS_FLOATS * sizeof(float);
+      err = ensure_lds_attr(mfma_fn<32>(), lds);
+      if (err != hipSuccess) return err;
+      hipLaunchKernelGGL(expert_mfma_kernel<32>, dim3(grid), dim3(kThreads), lds, st, a);
+      break;
+    }
+    case 64: {
+      const size_t lds = Tile<64>::LDS_FLOATS * sizeof(float);
+      err = ensure_lds_attr(mfma_fn<64>(), lds);
+      if (err != hipSuccess) return err;
+      hipLaunchKernelGGL(expert_mfma_kernel<64>, dim3(grid), dim3(kThreads), lds, st, a);
+      break;
+    }
+    case 128: {
+      const size_t lds = Tile<128>::LDS_FLOATS * sizeof(float);
+      err = ensure_lds_attr(mfma_fn<128>(), lds);
+      if (err != hipSuccess) return err;
+      hipLaunchKernelGGL(expert_mfma_kernel<128>, dim3(grid), dim3(kThreads), lds, st, a);
+      break;
+    }
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+int expert_bn(int tile_rows) {
+  switch (tile_rows) {
+    case 32: return Tile<32>::BN;
+    case 64: return Tile<64>::BN;
+    case 128: return Tile<128>::BN;
+    default: return kStreamRows;
+  }
+}
+
+int expert_blocks_per_cu(int tile_rows) {
+  int n = 0;
+  hipError_t e = hipSuccess;
+  switch (tile_rows) {
+    case 0:
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &n, reinterpret_cast<const void *>(&expert_stream_kernel), kThreads,
+          stream_lds_bytes(2048, 2048));
+      break;
+    case 32:
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &n, mfma_fn<32>(), kThreads, Tile<32>::LDS_FLOATS * sizeof(float));
+      break;
+    case 64:
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &n, mfma_fn<64>(), kThreads, Tile<64>::LDS_FLOATS * sizeof(float));
+      break;
+    case 128:
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+          &n, mfma_fn<128>(), kThreads, Tile<128>::LDS_FLOATS * sizeof(float));
+      break;
+    default:
+      return 1;
+  }
+  if (e != hipSuccess || n < 1) return 1;
+  return n;
+}
+
+hipError_t launch_pack_w13(float *dst, const float *w1, const float *w3, int H,
+                           int I, hipStream_t st) {
+  hipLaunchKernelGGL(pack_w13_kernel, dim3(1024), dim3(256), 0, st,
+                     reinterpret_cast<float4 *>(dst), reinterpret_cast<const float4 *>(w1),
+                     reinterpret_cast<const float4 *>(w3), H / 4, I);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_gate(float4 *dst, const float *gate, int E, int H,
+                            hipStream_t st) {
+  hipLaunchKernelGGL(pack_gate_kernel, dim3(64), dim3(256), 0, st, dst,
+                     reinterpret_cast<const float4 *>(gate), E, H / 4);
+  return hipGetLastError();
+}
+
+}  // namespace moe

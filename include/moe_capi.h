@@ -1,0 +1,139 @@
+/*
+ * moe_capi.h -- C-ABI of the MI355X (gfx950) sparse-MoE block.
+ *
+ * The drop-in boundary for the MoE FFN path of a decoder layer: the
+ * reference's SparseMoeBlock (risepower20/final include/layer.h:72-123,
+ * src/layer.cu:1274-1503) re-implemented on hand-written HIP kernels.  Plain
+ * pointers and sizes only; every call returns an int status (0 = MOE_OK) and
+ * never exits the process (the reference's CHECK_CUDA calls exit(),
+ * include/tensor.h:9-17).
+ *
+ * Semantics of one forward (SparseMoeBlock::forward_gpu, layer.cu:1428-1498):
+ *   logits = x . gate^T                      (fp32, one FMA chain per output)
+ *   p      = 1 / (1 + exp(-logit))          (exp in double)
+ *   top-4 of p + bias, renormalised over the four p  (layer.cu:439-499)
+ *   y[t]   = sum_k w[t,k] * W2_e (silu(W1_e x[t]) * (W3_e x[t]))   e = idx[t,k]
+ *   y[t]  += residual[t]   when residual != NULL (add_kernel, layer.cu:1917)
+ *
+ * Threading: a context runs one forward at a time.  Calls on one context must
+ * be ordered on one stream (the reference serialises a layer's forwards with a
+ * per-stage event, model.cu:435,447); two streams sharing a context race on
+ * its scratch.
+ */
+#ifndef MOE_CAPI_H
+#define MOE_CAPI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct moe_ctx moe_ctx;
+
+/* hipStream_t without pulling in the HIP headers; 0 = the null stream. */
+typedef void *moe_stream_t;
+
+enum moe_status {
+  MOE_OK = 0,
+  MOE_ERR_INVALID_ARG = 1,   /* null pointer, bad size, misaligned buffer */
+  MOE_ERR_UNSUPPORTED = 2,   /* dims the kernels are not built for */
+  MOE_ERR_HIP = 3,           /* a HIP runtime call failed */
+  MOE_ERR_OUT_OF_MEMORY = 4, /* device allocation failed */
+  MOE_ERR_NOT_READY = 5,     /* forward before weights were set */
+  MOE_ERR_TOO_MANY_TOKENS = 6, /* num_tokens > max_tokens of the context */
+  MOE_ERR_DEVICE_TIMEOUT = 7, /* a kernel's bounded dependency wait expired */
+  MOE_ERR_INTERNAL = 8       /* a kernel found an inconsistent dispatch plan */
+};
+
+/* Shapes.  Reference values (include/config.h:5,14-17): hidden 2048,
+ * inter 1792, num_experts 32, top_k 4.  Supported: num_experts == 32,
+ * top_k == 4, hidden % 256 == 0, inter % 256 == 0.  max_tokens sizes the
+ * scratch (the reference hard-codes 4096, layer.cu:1399). */
+typedef struct moe_dims {
+  int hidden;
+  int inter;
+  int num_experts;
+  int top_k;
+  int max_tokens;
+} moe_dims;
+
+/* Replaces SparseMoeBlock::init_gpu's scratch allocation (layer.cu:1399-1425).
+ * Allocates on the current HIP device. */
+int moe_create(const moe_dims *dims, moe_ctx **out);
+
+/* Replaces ~SparseMoeBlock (layer.cu:1302-1355).  Null is accepted. */
+int moe_destroy(moe_ctx *ctx);
+
+/* Replaces the weight upload of SparseMoeBlock::init_gpu (layer.cu:1358-1396)
+ * and MLP::init_gpu (layer.cu:1216-1228).  gate [E][H], bias [E] (may be
+ * NULL: no expert bias), w1[e]/w3[e] [I][H], w2[e] [H][I], fp32 row-major, the
+ * layouts the reference loads by name (layer.cu:1277-1298).  Pointers are host
+ * memory when src_on_device == 0, device memory otherwise.  The weights are
+ * repacked once into the kernels' layout; the caller's buffers may be freed
+ * afterwards.  Synchronises `stream` before returning. */
+int moe_set_weights(moe_ctx *ctx, const float *gate, const float *bias,
+                    const float *const *w1, const float *const *w3,
+                    const float *const *w2, int src_on_device,
+                    moe_stream_t stream);
+
+/* Replaces SparseMoeBlock::forward_gpu (layer.cu:1428-1498) and, when
+ * residual != NULL, the residual add_kernel after it (layer.cu:1917-1918).
+ * x, y, residual: device [num_tokens][hidden] fp32, 16-byte aligned; y may
+ * alias residual (in-place residual add) but not x.  Asynchronous on `stream`;
+ * no host synchronisation inside. num_tokens == 0 is a no-op. */
+int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
+                int num_tokens, moe_stream_t stream);
+
+/* The two halves of moe_forward, for callers that time or inspect them:
+ * moe_route = gate GEMM + sigmoid/top-4 + per-expert histogram and scan
+ * (layer.cu:1438-1464); moe_experts = dispatch + grouped SwiGLU experts +
+ * weighted combine (layer.cu:1466-1497).  moe_experts must follow moe_route on
+ * the same stream with the same x and num_tokens. */
+int moe_route(moe_ctx *ctx, const float *x, int num_tokens, moe_stream_t stream);
+int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
+                int num_tokens, moe_stream_t stream);
+
+/* Routing from caller-supplied logits [num_tokens][E] (device): the sigmoid,
+ * bias, top-4 and histogram of moe_router_topk_kernel (layer.cu:439-499)
+ * without the gate GEMM.  Used by SparseMoeBlock::route_tokens (layer.h:91-93)
+ * and by parity tests that craft ties.  Follow with moe_experts or read the
+ * result with moe_last_routing. */
+int moe_route_logits(moe_ctx *ctx, const float *logits, int num_tokens,
+                     moe_stream_t stream);
+
+/* Copies the routing of the last moe_route/moe_forward to host memory:
+ * idx [T][4] (rank order, -1 = none), w [T][4], counts [E], logits [T][E]
+ * (any may be NULL).  Synchronises `stream`.  The topk_indices_gpu_,
+ * topk_weights_gpu_ and expert_counts_gpu_ of the reference (layer.h:99-107). */
+int moe_last_routing(moe_ctx *ctx, int *idx, float *w, int *counts,
+                     float *logits, moe_stream_t stream);
+
+/* Reads and clears the device status word: MOE_ERR_DEVICE_TIMEOUT if a
+ * kernel's bounded dependency wait expired since the last call,
+ * MOE_ERR_INTERNAL if a kernel met an out-of-range slot (and skipped it), else
+ * MOE_OK.  Synchronises `stream`. */
+int moe_device_status(moe_ctx *ctx, moe_stream_t stream);
+
+/* Which expert kernel moe_forward picks for num_tokens: 0 = weight-streaming
+ * (small T), 32/64/128 = MFMA grouped GEMM with that many rows per tile. */
+int moe_plan_tile_rows(const moe_ctx *ctx, int num_tokens);
+
+/* Overrides the plan (tests): rows = -1 automatic, 0 streaming, 32/64/128. */
+int moe_force_tile_rows(moe_ctx *ctx, int rows);
+
+/* Test hook: scales the kernels' bounded-wait limit (1 = default, >1 shorter).
+ * A value > 1 makes waits give up early and raise MOE_ERR_DEVICE_TIMEOUT;
+ * every kernel still exits normally. */
+int moe_set_wait_divisor(moe_ctx *ctx, int divisor);
+
+const char *moe_strerror(int status);
+
+/* Library version string ("final_amd-moe <semver> gfx950"). */
+const char *moe_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,180 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, by the smoke check in
+__graft_entry__.py and by the cpu_baseline leg of bench.py, always as the
+checker.  The product package (final_amd) never imports this module.
+
+The oracle restates the reference's MoE arithmetic (risepower20/final,
+src/layer.cu:9-141, 434-542, 695-1126, 1428-1498, 1860-1880); each C function
+cites the lines it follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+TOPK = 4
+
+_lib = None
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+_i32p = ctypes.POINTER(ctypes.c_int)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
+_i64 = ctypes.c_int64
+
+
+def build(force: bool = False) -> str:
+    """Compile liboracle.so with the committed Makefile (gcc, -ffp-contract=off)."""
+    if force or not os.path.exists(LIB_PATH):
+        subprocess.run(["make", "-s", "-C", HERE], check=True)
+    return LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"oracle library missing: {LIB_PATH} (run make -C oracle)")
+        L = ctypes.CDLL(LIB_PATH)
+        L.orc_force_scalar.argtypes = [ctypes.c_int]
+        L.orc_set_threads.argtypes = [ctypes.c_int]
+        L.orc_get_threads.restype = ctypes.c_int
+        L.orc_gemm_nt_chain.argtypes = [_f32p, _i64, _f32p, _i64, _i64, _f32p]
+        L.orc_gate_logits.argtypes = [_f32p, _f32p, _i64, ctypes.c_int, ctypes.c_int, _f32p]
+        L.orc_gate_logits_muladd.argtypes = [_f32p, _f32p, _i64, ctypes.c_int, ctypes.c_int, _f32p]
+        L.orc_sigmoid.argtypes = [ctypes.c_float]
+        L.orc_sigmoid.restype = ctypes.c_float
+        L.orc_silu.argtypes = [ctypes.c_float]
+        L.orc_silu.restype = ctypes.c_float
+        L.orc_route.argtypes = [_f32p, _f32p, _i64, ctypes.c_int, _i32p, _f32p, _i32p]
+        L.orc_dispatch.argtypes = [_i32p, _i64, ctypes.c_int, _i32p, _i32p, _i32p]
+        L.orc_expert_w1w3.argtypes = [_f32p, _i64, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p]
+        L.orc_expert_w2.argtypes = [_f32p, _i64, _f32p, ctypes.c_int, ctypes.c_int, _f32p]
+        L.orc_combine.argtypes = [_f32p, _i32p, _f32p, _f32p, _i64, ctypes.c_int, _f32p]
+        L.orc_moe_forward.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                      _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                      _u8p, _f32p, _f32p, _i32p, _f32p, _i32p]
+        L.orc_moe_forward.restype = ctypes.c_int
+        _lib = L
+    return _lib
+
+
+def _f(a):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_f32p)
+
+
+def _i(a):
+    if a is None:
+        return None
+    assert a.dtype == np.int32 and a.flags.c_contiguous
+    return a.ctypes.data_as(_i32p)
+
+
+def force_scalar(on: bool) -> None:
+    lib().orc_force_scalar(1 if on else 0)
+
+
+def set_threads(n: int) -> None:
+    lib().orc_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().orc_get_threads())
+
+
+def gemm_nt_chain(A: np.ndarray, B: np.ndarray) -> np.ndarray:
+    M, K = A.shape
+    N, K2 = B.shape
+    assert K == K2
+    C = np.empty((M, N), np.float32)
+    lib().orc_gemm_nt_chain(_f(A), M, _f(B), N, K, _f(C))
+    return C
+
+
+def gate_logits(x, gate, muladd: bool = False):
+    T, H = x.shape
+    E = gate.shape[0]
+    out = np.empty((T, E), np.float32)
+    fn = lib().orc_gate_logits_muladd if muladd else lib().orc_gate_logits
+    fn(_f(x), _f(gate), T, H, E, _f(out))
+    return out
+
+
+def sigmoid(v: float) -> float:
+    return float(np.float32(lib().orc_sigmoid(float(v))))
+
+
+def silu(v: float) -> float:
+    return float(np.float32(lib().orc_silu(float(v))))
+
+
+def route(logits, bias):
+    T, E = logits.shape
+    idx = np.empty((T, TOPK), np.int32)
+    w = np.empty((T, TOPK), np.float32)
+    counts = np.empty((E,), np.int32)
+    lib().orc_route(_f(logits), _f(bias), T, E, _i(idx), _f(w), _i(counts))
+    return idx, w, counts
+
+
+def dispatch(idx, E):
+    T = idx.shape[0]
+    offsets = np.empty((E + 1,), np.int32)
+    pos = np.empty((T, TOPK), np.int32)
+    slot_token = np.full((T * TOPK,), -1, np.int32)
+    lib().orc_dispatch(_i(idx), T, E, _i(offsets), _i(pos), _i(slot_token))
+    return offsets, pos, slot_token
+
+
+def expert_w1w3(xrows, w1, w3):
+    M, H = xrows.shape
+    I = w1.shape[0]
+    inter = np.empty((M, I), np.float32)
+    lib().orc_expert_w1w3(_f(xrows), M, _f(w1), _f(w3), H, I, _f(inter))
+    return inter
+
+
+def expert_w2(inter, w2):
+    M, I = inter.shape
+    H = w2.shape[0]
+    out = np.empty((M, H), np.float32)
+    lib().orc_expert_w2(_f(inter), M, _f(w2), H, I, _f(out))
+    return out
+
+
+def combine(sorted_out, pos, w, residual=None):
+    T = pos.shape[0]
+    H = sorted_out.shape[1]
+    y = np.empty((T, H), np.float32)
+    lib().orc_combine(_f(sorted_out), _i(pos), _f(w), _f(residual), T, H, _f(y))
+    return y
+
+
+def moe_forward(x, gate, bias, w1, w3, w2, residual=None, token_mask=None):
+    """Full block.  w1/w3: [E][I][H], w2: [E][H][I].  Returns dict with y
+    (rows of unselected tokens are NaN), logits, idx, w, counts."""
+    T, H = x.shape
+    E, I, _ = w1.shape
+    y = np.full((T, H), np.nan, np.float32)
+    logits = np.empty((T, E), np.float32)
+    idx = np.empty((T, TOPK), np.int32)
+    w = np.empty((T, TOPK), np.float32)
+    counts = np.empty((E,), np.int32)
+    mask = None
+    if token_mask is not None:
+        mask = np.ascontiguousarray(token_mask, dtype=np.uint8)
+    rc = lib().orc_moe_forward(
+        _f(x), _f(gate), _f(bias), _f(w1), _f(w3), _f(w2), _f(residual),
+        T, H, I, E, mask.ctypes.data_as(_u8p) if mask is not None else None,
+        _f(y), _f(logits), _i(idx), _f(w), _i(counts))
+    if rc != 0:
+        raise RuntimeError("orc_moe_forward failed")
+    return {"y": y, "logits": logits, "idx": idx, "w": w, "counts": counts}
