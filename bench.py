@@ -1,0 +1,185 @@
+"""MoE-block benchmark on one MI355X.
+
+One step = one forward of the MoE block (router kernel + expert kernel) over a
+batch of synthetic tokens already resident in HBM.  Default workload: T=4096
+tokens (prefill), hidden 2048, 32 experts top-4, intermediate 1792, fp32.
+
+Prints ONE JSON line on stdout (progress goes to stderr):
+  value         tokens/s of the whole block over the timed steps
+  roofline      the expert kernel (dominant): algorithmic FLOPs (MFMA-bound
+                workloads) or bytes (weight-streaming workloads) per launch,
+                divided by its average launch time from HIP events recorded on
+                the launch stream around each expert-kernel launch
+  cpu_baseline  the CPU oracle (a restatement of the reference's arithmetic)
+                on this host, median of a few runs
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "MoE-block tokens/sec at T=4096 fp32, 1 GPU; % of MFMA / HBM roofline"
+PEAK_MFMA_F32_TFLOPS = 157.3   # MI355X dense fp32 matrix
+PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--workload", default="prefill_t4096")
+    p.add_argument("--weight-sets", type=int, default=0,
+                   help="distinct weight copies cycled per step (0 = auto: enough to "
+                        "exceed the 256 MB Infinity Cache for small T)")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--cpu-threads", type=int, default=0)
+    return p.parse_args()
+
+
+def cpu_baseline(w, x, threads: int):
+    from oracle import oracle as O
+    O.set_threads(threads)
+    T = x.shape[0]
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.moe_forward(x, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+        times.append(time.perf_counter() - t0)
+        if sum(times) > 30.0:
+            break
+    med = statistics.median(times)
+    return {"value": round(T / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"whole workload ({T} tokens), median of {len(times)} runs, "
+                      f"{med:.3f} s each, OpenMP {threads} threads"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build runs the MoE block on ONE GPU; multi-GPU runs are not "
+              "part of it (see DESIGN.md for how the block would shard).", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+
+    from final_amd import SparseMoeBlock, hip
+    from final_amd import workloads as W
+
+    wl = W.WORKLOADS[args.workload]
+    T = wl.T
+    if hip.device_count() < 1:
+        raise RuntimeError("no HIP device visible")
+    log(f"[bench] workload={wl.name} T={T}: generating weights")
+    w = W.gen_weights(wl.seed, bias=wl.bias)
+    x = W.gen_x(T, wl.seed)
+
+    nsets = args.weight_sets
+    if nsets <= 0:
+        # a set's active experts for small T can sit in the 256 MB Infinity
+        # Cache; cycle copies so every step streams its weights from HBM
+        nsets = 1 if T >= 512 else 4
+    blocks = []
+    for i in range(nsets):
+        b = SparseMoeBlock(max_tokens=max(T, 64))
+        b.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+        blocks.append(b)
+    stream = hip.Stream()
+    dx = hip.DeviceArray.from_numpy(x)
+    dy = hip.DeviceArray((T, W.H))
+    plan = blocks[0].plan(T)
+    log(f"[bench] plan={plan} (0 = weight streaming, else MFMA tile rows), weight sets={nsets}")
+
+    for i in range(args.warmup):
+        blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream)
+    stream.synchronize()
+    blocks[0].check_device(stream)
+
+    K = args.steps
+    ev = [(hip.Event(), hip.Event(), hip.Event()) for _ in range(K)]
+    start, stop = hip.Event(), hip.Event()
+    hip.synchronize()
+    t_wall = time.perf_counter()
+    start.record(stream)
+    for i in range(K):
+        b = blocks[i % nsets]
+        e0, e1, e2 = ev[i]
+        e0.record(stream)
+        b.route(dx, T, stream=stream)
+        e1.record(stream)
+        b.experts(dx, dy, T, stream=stream)
+        e2.record(stream)
+    stop.record(stream)
+    stop.synchronize()
+    wall = time.perf_counter() - t_wall
+    hip.synchronize()
+    total_ms = start.elapsed_ms(stop)
+    route_ms = [e0.elapsed_ms(e1) for e0, e1, _ in ev]
+    exp_ms = [e1.elapsed_ms(e2) for _, e1, e2 in ev]
+    for b in blocks:
+        b.check_device(stream)
+    rt = blocks[0].last_routing()
+    counts = rt["counts"]
+
+    ms_step = total_ms / K
+    value = T * K / (total_ms / 1e3)
+    exp_avg = statistics.mean(exp_ms)
+    route_avg = statistics.mean(route_ms)
+    expert_flops = T * (W.flops_per_token() - 2 * W.H * W.E)  # W1, W3, W2 of 4 slots/token
+    expert_bytes = W.algorithmic_bytes(counts, T) - (W.E * W.H * 4 + W.E * 4)
+    mfma_bound = plan != 0
+    if mfma_bound:
+        achieved = expert_flops / (exp_avg / 1e3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_F32_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_F32_TFLOPS, 4)}
+    else:
+        achieved = expert_bytes / (exp_avg / 1e3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    roof["traffic"] = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            tr = json.load(f).get(wl.name)
+        if tr:
+            roof["traffic"] = tr.get("bytes_per_launch")
+    roof["kernel"] = "expert_mfma_kernel<%d>" % plan if mfma_bound else "expert_stream_kernel"
+    roof["kernel_ms"] = round(exp_avg, 4)
+    roof["router_ms"] = round(route_avg, 4)
+    roof["per_launch"] = ({"flop": expert_flops} if mfma_bound else {"bytes": expert_bytes})
+
+    out = {
+        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) tokens)",
+        "config": {"workload": wl.name, "tokens": T, "hidden": W.H, "inter": W.I,
+                   "experts": W.E, "top_k": W.K, "plan_tile_rows": plan,
+                   "active_experts": int((counts > 0).sum()), "weight_sets": nsets,
+                   "wall_s": round(wall, 4)},
+        "roofline": roof,
+    }
+    if not args.no_cpu:
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        log(f"[bench] CPU oracle baseline, {threads} threads")
+        out["cpu_baseline"] = cpu_baseline(w, x, threads)
+    else:
+        out["cpu_baseline"] = None
+    for b in blocks:
+        b.close()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

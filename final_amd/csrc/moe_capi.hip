@@ -51,13 +51,14 @@ struct moe_ctx {
   int wait_div = 1;
   bool weights_set = false;
   bool has_bias = false;
+  bool stream_ok = false;  // streaming kernel compiled for (H, I)
   int max_units = 0;
   int grid[4] = {1, 1, 1, 1};  // plans 0, 32, 64, 128
   // last routing state
   int routed_T = -1;
   int routed_plan = -1;
   // device memory
-  float4 *gate4 = nullptr;
+  float *gate = nullptr;
   float *bias = nullptr;
   float *w13 = nullptr;
   float *w2 = nullptr;
@@ -75,15 +76,15 @@ static int plan_index(int rows) {
   }
 }
 
-static int auto_plan(int T) {
-  if (T <= 64) return 0;
+static int auto_plan(int T, bool stream_ok) {
+  if (T <= 64) return stream_ok ? 0 : 32;
   if (T < 512) return 32;
   if (T < 2048) return 64;
   return 128;
 }
 
 static int ctx_plan(const moe_ctx *ctx, int T) {
-  return ctx->tile_override >= 0 ? ctx->tile_override : auto_plan(T);
+  return ctx->tile_override >= 0 ? ctx->tile_override : auto_plan(T, ctx->stream_ok);
 }
 
 template <typename T>
@@ -145,13 +146,13 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
     return MOE_ERR_HIP;
   }
   ctx->cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
+  ctx->stream_ok = stream_supported(d.hidden, d.inter);
   const size_t H = d.hidden, I = d.inter, E = kExperts;
   const size_t Tm = d.max_tokens, S = Tm * kTopK;
-  const size_t nb = (Tm + kRouterTokens - 1) / kRouterTokens;
+  const size_t nb = (Tm + kMinRouterTokens - 1) / kMinRouterTokens;
   ctx->max_units = (int)(S / 32 + E + 1);
   int rc = MOE_OK;
-  float *gate_f = nullptr;
-  if ((rc = dev_alloc(ctx, &gate_f, E * H)) ||
+  if ((rc = dev_alloc(ctx, &ctx->gate, E * H)) ||
       (rc = dev_alloc(ctx, &ctx->bias, E)) ||
       (rc = dev_alloc(ctx, &ctx->w13, E * 2 * I * H)) ||
       (rc = dev_alloc(ctx, &ctx->w2, E * H * I)) ||
@@ -160,6 +161,7 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
       (rc = dev_alloc(ctx, &ctx->s.wts, S)) ||
       (rc = dev_alloc(ctx, &ctx->s.pos, S)) ||
       (rc = dev_alloc(ctx, &ctx->s.blk, nb * E)) ||
+      (rc = dev_alloc(ctx, &ctx->s.tb_done, nb)) ||
       (rc = dev_alloc(ctx, &ctx->s.slot_token, S)) ||
       (rc = dev_alloc(ctx, &ctx->s.inter, S * I)) ||
       (rc = dev_alloc(ctx, &ctx->s.sout, S * H))) {
@@ -167,7 +169,6 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
     delete ctx;
     return rc;
   }
-  ctx->gate4 = reinterpret_cast<float4 *>(gate_f);
   char *ctrl_mem = nullptr;
   const size_t ctrl_bytes = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
   if ((rc = dev_alloc(ctx, &ctrl_mem, ctrl_bytes))) {
@@ -178,6 +179,7 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
   ctx->s.ctrl = reinterpret_cast<Ctrl *>(ctrl_mem);
   ctx->s.dep = reinterpret_cast<int *>(ctrl_mem + sizeof(Ctrl));
   if (hipMemset(ctrl_mem, 0, ctrl_bytes) != hipSuccess ||
+      hipMemset(ctx->s.tb_done, 0, nb * sizeof(int)) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {
     free_all(ctx);
     delete ctx;
@@ -226,20 +228,7 @@ int moe_set_weights(moe_ctx *ctx, const float *gate, const float *bias,
     return code;
   };
   do {
-    // gate -> [H/4][E] float4
-    const float *gsrc = gate;
-    if (!src_on_device) {
-      if (hipMemcpyAsync(stage, gate, E * H * sizeof(float), kind, st) != hipSuccess) {
-        fail(MOE_ERR_HIP);
-        break;
-      }
-      gsrc = stage;
-    }
-    if (launch_pack_gate(ctx->gate4, gsrc, (int)E, (int)H, st) != hipSuccess) {
-      fail(MOE_ERR_HIP);
-      break;
-    }
-    if (!src_on_device && hipStreamSynchronize(st) != hipSuccess) {
+    if (hipMemcpyAsync(ctx->gate, gate, E * H * sizeof(float), kind, st) != hipSuccess) {
       fail(MOE_ERR_HIP);
       break;
     }
@@ -304,7 +293,7 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   RouterArgs a{};
   a.x = x;
   a.logits_in = logits;
-  a.w.gate4 = ctx->gate4;
+  a.w.gate = ctx->gate;
   a.w.bias = ctx->has_bias ? ctx->bias : nullptr;
   a.w.w13 = ctx->w13;
   a.w.w2 = ctx->w2;
@@ -349,7 +338,7 @@ int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
   a.x = x;
   a.y = y;
   a.residual = residual;
-  a.w.gate4 = ctx->gate4;
+  a.w.gate = ctx->gate;
   a.w.bias = ctx->has_bias ? ctx->bias : nullptr;
   a.w.w13 = ctx->w13;
   a.w.w2 = ctx->w2;
@@ -431,6 +420,7 @@ int moe_plan_tile_rows(const moe_ctx *ctx, int num_tokens) {
 int moe_force_tile_rows(moe_ctx *ctx, int rows) {
   if (!ctx) return MOE_ERR_INVALID_ARG;
   if (rows != -1 && plan_index(rows) < 0) return MOE_ERR_INVALID_ARG;
+  if (rows == 0 && !ctx->stream_ok) return MOE_ERR_UNSUPPORTED;
   ctx->tile_override = rows;
   return MOE_OK;
 }

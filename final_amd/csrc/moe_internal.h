@@ -10,12 +10,12 @@ namespace moe {
 
 constexpr int kExperts = 32;     // NUM_EXPERTS, reference include/config.h:14
 constexpr int kTopK = 4;         // NUM_EXPERTS_PER_TOK, config.h:15
-constexpr int kRouterTokens = 64;  // tokens per router block (one wave of lanes)
+constexpr int kMinRouterTokens = 8;  // smallest token block of the router
 constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
 constexpr int kCombineTokens = 8;  // tokens per combine task
 constexpr int kStreamRowsPerWave = 4;   // weight rows per wave, streaming kernel
 constexpr int kStreamRows = kStreamRowsPerWave * 4;  // rows per streaming task
-constexpr int kStreamTokens = 8;  // token rows per streaming pass (LDS staged)
+constexpr int kStreamTokens = 4;  // token rows per streaming pass (LDS staged)
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset
@@ -36,7 +36,7 @@ struct Ctrl {
   int p1_per_unit;  // W1W3 tasks per m-tile (MFMA) or per expert (streaming)
   int p2_per_unit;
   int n_active;     // experts with count > 0
-  int pad_;
+  int rtokens;      // tokens per router block (dispatch task size)
   int counts[kExperts];
   int offsets[kExperts + 1];
   int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)
@@ -45,7 +45,7 @@ struct Ctrl {
 };
 
 struct Weights {
-  const float4 *gate4;   // [H/4][E] float4: gate[e][4k..4k+3] at [k][e]
+  const float *gate;     // [E][H]
   const float *bias;     // [E] (may be null)
   const float *w13;      // [E][I/32][2][32][H]: 32 rows of W1 then 32 of W3
   const float *w2;       // [E][H][I]
@@ -56,7 +56,8 @@ struct Scratch {
   int *idx;              // [Tmax][4]
   float *wts;            // [Tmax][4]
   int *pos;              // [Tmax][4]: local rank, then slot
-  int *blk;              // [Tmax/64][E]: block counts, then block bases
+  int *blk;              // [Tmax/8][E]: block counts, then block bases
+  int *tb_done;          // [Tmax/8]: expert-split blocks finished per token block
   int *slot_token;       // [4 Tmax]
   float *inter;          // [4 Tmax][I]
   float *sout;           // [4 Tmax][H]
@@ -92,8 +93,10 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
                           hipStream_t st);
 hipError_t launch_pack_w13(float *dst, const float *w1, const float *w3, int H,
                            int I, hipStream_t st);
-hipError_t launch_pack_gate(float4 *dst, const float *gate, int E, int H,
-                            hipStream_t st);
+// Tokens per router block for a forward of T tokens.
+int router_tokens_per_block(int T);
+// Whether the weight-streaming kernel is compiled for (H, I).
+bool stream_supported(int H, int I);
 // Max resident blocks per CU of the expert kernel for a plan.
 int expert_blocks_per_cu(int tile_rows);
 // Columns of the B tile of the MFMA kernel for a plan.

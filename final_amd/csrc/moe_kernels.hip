@@ -29,35 +29,62 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 // Cross-block synchronisation (agent scope: coherent across the 8 XCD L2s)
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ int load_acquire(const int *p) {
-  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+// Coherent read without ordering: polling with acquire loads would invalidate
+// the L2 on every poll; the wait does one acquire fence after it succeeds.
+__device__ __forceinline__ int load_relaxed(const int *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ int fetch_add(int *p, int v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Task-queue claim: the index publishes no data, so no fence is needed.
+__device__ __forceinline__ int claim(int *p) {
+  return __hip_atomic_fetch_add(p, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Cross-block hand-off inside one kernel.  Data another block reads before the
+// kernel ends is written with agent-scope stores (write-through to the
+// device-coherent level, sc1), so publishing it needs no L2 writeback: a
+// release fence here would write back the whole XCD L2 per task, which costs
+// ~10x the HBM time of a weight-streaming task.  The signal waits for the
+// block's stores to complete and then counts; the consumer's single acquire
+// fence drops stale L2/L1 lines before it reads.
+__device__ __forceinline__ void st_agent(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent(int *p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_agent4(float *p, float4 v) {
+  st_agent(p + 0, v.x);
+  st_agent(p + 1, v.y);
+  st_agent(p + 2, v.z);
+  st_agent(p + 3, v.w);
 }
 
 // Block-wide: wait until *p >= target (thread 0 polls), then acquire.
 __device__ void block_wait(const int *p, int target, int limit, int *err) {
   if (threadIdx.x == 0) {
     int spins = 0;
-    while (load_acquire(p) < target) {
-      __builtin_amdgcn_s_sleep(2);
+    while (load_relaxed(p) < target) {
+      __builtin_amdgcn_s_sleep(8);
       if (++spins > limit) {
         __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }
     }
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
 }
 
-// Block-wide: release every thread's global writes, then count one.
+// Block-wide: once every thread's agent-scope stores have completed, count one.
 __device__ void block_signal(int *p) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (threadIdx.x == 0) fetch_add(p, 1);
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(p, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------
@@ -71,76 +98,152 @@ __device__ __forceinline__ float ref_sigmoid(float x) {
   return 1.0f / (1.0f + e);
 }
 
-// One block = 64 tokens.  Lane map for the gate chains: e = tid % 32,
-// tokens (tid / 32) * 8 + j, j < 8: each lane runs 8 independent FMA chains.
-template <bool FROM_LOGITS>
+// Router.  A block computes the gate logits of RT tokens x (32/ES) experts as
+// fp32 FMA chains over k ascending (the reference's per-output order,
+// layer.cu:109-127), staging x and gate through LDS in KC-wide k chunks with
+// the next chunk's global loads in flight during the current chunk's FMAs.
+// ES > 1 splits the experts over ES blocks so small T (decode) spreads the
+// gate over more CUs; the last of a token block's ES blocks then finishes it.
+// Finishing a token block: sigmoid with a double exp, score = p + bias,
+// top-4 insertion (layer.cu:439-499), weights, in-block ranks by 64-lane
+// ballots and per-block expert counts.  The last token block to finish scans
+// the counts and writes the expert kernel's plan.
+template <int RT, int ES, int KC> struct RouterCfg {
+  static constexpr int EPB = kExperts / ES;          // experts per block
+  static constexpr int NGRP = kThreads / EPB;        // lane groups
+  static constexpr int TPL = RT >= NGRP ? RT / NGRP : 1;  // tokens per lane
+  static constexpr int PITCH = KC + 4;
+  static constexpr int X_F4 = RT * KC / 4, G_F4 = EPB * KC / 4;
+  static constexpr int X_PER = (X_F4 + kThreads - 1) / kThreads;
+  static constexpr int G_PER = (G_F4 + kThreads - 1) / kThreads;
+  static_assert(RT <= 64, "ballot ranks need <= 64 tokens per block");
+  static_assert(KC % 4 == 0 && kThreads % (KC / 4) == 0, "chunk split");
+};
+
+template <bool FROM_LOGITS, int RT, int ES, int KC>
 __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
 #pragma clang fp contract(off)
-  __shared__ float s_score[kRouterTokens][kExperts + 1];
-  __shared__ float s_prob[kRouterTokens][kExperts + 1];
+  using C = RouterCfg<RT, ES, KC>;
+  constexpr int EPB = C::EPB, TPL = C::TPL, PITCH = C::PITCH;
+  __shared__ float xs[RT * PITCH];
+  __shared__ float gs[EPB * PITCH];
+  __shared__ float s_score[RT][kExperts + 1];
+  __shared__ float s_prob[RT][kExperts + 1];
   __shared__ int s_cnt[kExperts];
   __shared__ int s_part[8][kExperts];
   __shared__ int s_off[kExperts + 1];
-  __shared__ int s_last;
+  __shared__ int s_flag;
   __shared__ int s_units;
 
   const int tid = threadIdx.x;
-  const int b = blockIdx.x;
-  const int t0 = b * kRouterTokens;
-  const int T = a.T;
-  const int e = tid & (kExperts - 1);
-  const int g = tid >> 5;
+  const int tb = blockIdx.x / ES, es = blockIdx.x % ES;
+  const int t0 = tb * RT, e0 = es * EPB;
+  const int T = a.T, H = a.H;
+  const int el = tid % EPB, grp = tid / EPB;
+  const bool chain_lane = grp * TPL < RT;
   Ctrl *ctrl = a.s.ctrl;
 
-  float lg[8];
   if (!FROM_LOGITS) {
-    const int H4 = a.H >> 2;
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
-    const float4 *gp = a.w.gate4 + e;
-    const float4 *xr[8];
+    // staging map: thread -> (row, float4 column) of a KC-wide chunk
+    constexpr int KV = KC / 4, RPP = kThreads / KV;
+    const int srow = tid / KV, sc4 = (tid % KV) * 4;
+    float4 px[C::X_PER], pg[C::G_PER];
+    auto fetch = [&](int k0) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      int tok = t0 + g * 8 + j;
-      tok = tok < T ? tok : T - 1;  // rows past T compute a copy, never stored
-      xr[j] = x4 + (size_t)tok * H4;
-      lg[j] = 0.0f;
+      for (int i = 0; i < C::X_PER; ++i) {
+        const int r = srow + i * RPP;
+        if (r < RT) {
+          int tok = t0 + r;
+          tok = tok < T ? tok : T - 1;  // rows past T: a copy, never stored
+          px[i] = *reinterpret_cast<const float4 *>(a.x + (size_t)tok * H + k0 + sc4);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < C::G_PER; ++i) {
+        const int r = srow + i * RPP;
+        if (r < EPB)
+          pg[i] = *reinterpret_cast<const float4 *>(a.w.gate + (size_t)(e0 + r) * H + k0 + sc4);
+      }
+    };
+    float acc[TPL];
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) acc[j] = 0.0f;
+    fetch(0);
+    for (int k0 = 0; k0 < H; k0 += KC) {
+      __syncthreads();  // the previous chunk's readers are done
+#pragma unroll
+      for (int i = 0; i < C::X_PER; ++i) {
+        const int r = srow + i * RPP;
+        if (r < RT) *reinterpret_cast<float4 *>(xs + r * PITCH + sc4) = px[i];
+      }
+#pragma unroll
+      for (int i = 0; i < C::G_PER; ++i) {
+        const int r = srow + i * RPP;
+        if (r < EPB) *reinterpret_cast<float4 *>(gs + r * PITCH + sc4) = pg[i];
+      }
+      __syncthreads();
+      if (k0 + KC < H) fetch(k0 + KC);  // in flight during this chunk's FMAs
+      if (chain_lane) {
+        const float *gp = gs + el * PITCH;
+        const float *xp = xs + grp * TPL * PITCH;
+#pragma unroll 4
+        for (int k = 0; k < KC; k += 4) {
+          const float4 gv = *reinterpret_cast<const float4 *>(gp + k);
+#pragma unroll
+          for (int j = 0; j < TPL; ++j) {
+            const float4 xv = *reinterpret_cast<const float4 *>(xp + j * PITCH + k);
+            acc[j] = __builtin_fmaf(xv.x, gv.x, acc[j]);
+            acc[j] = __builtin_fmaf(xv.y, gv.y, acc[j]);
+            acc[j] = __builtin_fmaf(xv.z, gv.z, acc[j]);
+            acc[j] = __builtin_fmaf(xv.w, gv.w, acc[j]);
+          }
+        }
+      }
     }
-    // logits[t][e]: acc = fma(x[t][k], gate[e][k], acc), k = 0..H-1 ascending,
-    // the reference's per-output accumulation order (layer.cu:109-127).
-    for (int k4 = 0; k4 < H4; ++k4) {
-      const float4 gv = gp[(size_t)k4 * kExperts];
+    if (chain_lane) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float4 xv = xr[j][k4];
-        lg[j] = __builtin_fmaf(xv.x, gv.x, lg[j]);
-        lg[j] = __builtin_fmaf(xv.y, gv.y, lg[j]);
-        lg[j] = __builtin_fmaf(xv.z, gv.z, lg[j]);
-        lg[j] = __builtin_fmaf(xv.w, gv.w, lg[j]);
+      for (int j = 0; j < TPL; ++j) {
+        const int tl = grp * TPL + j;
+        if (t0 + tl < T) st_agent(&a.s.logits[(size_t)(t0 + tl) * kExperts + e0 + el], acc[j]);
       }
     }
   }
-  const float bias_e = a.w.bias ? a.w.bias[e] : 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int tl = g * 8 + j;
-    const int tok = t0 + tl;
-    float l;
-    if (FROM_LOGITS) {
-      l = tok < T ? a.logits_in[(size_t)tok * kExperts + e] : 0.0f;
-    } else {
-      l = lg[j];
+
+  // ---- the last of the token block's ES blocks finishes it ---------------
+  if (ES > 1 && !FROM_LOGITS) {
+    __builtin_amdgcn_s_waitcnt(0);  // this block's logits are stored
+    __syncthreads();
+    if (tid == 0) {
+      s_flag = fetch_add(&a.s.tb_done[tb], 1) == ES - 1;
+      if (s_flag) {
+        a.s.tb_done[tb] = 0;  // all ES blocks counted in: reset
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      }
     }
-    if (tok < T) a.s.logits[(size_t)tok * kExperts + e] = l;
+    __syncthreads();
+    if (!s_flag) return;
+  } else if (!FROM_LOGITS) {
+    __syncthreads();  // logits written by this block are read back below
+  }
+  const float *lsrc = FROM_LOGITS ? a.logits_in : a.s.logits;
+  for (int f = tid; f < RT * kExperts; f += kThreads) {
+    const int tl = f / kExperts, e = f % kExperts;
+    const int tok = t0 + tl;
+    float l = 0.0f;
+    if (tok < T) {
+      l = lsrc[(size_t)tok * kExperts + e];
+      if (FROM_LOGITS) a.s.logits[(size_t)tok * kExperts + e] = l;
+    }
     const float p = ref_sigmoid(l);
     s_prob[tl][e] = p;
-    s_score[tl][e] = p + bias_e;  // layer.cu:462
+    s_score[tl][e] = p + (a.w.bias ? a.w.bias[e] : 0.0f);  // layer.cu:462
   }
   __syncthreads();
 
-  if (tid < kRouterTokens) {  // wave 0: lane = token of the block
+  if (tid < 64) {  // wave 0: lane = token of the block
     const int tl = tid;
     const int tok = t0 + tl;
-    const bool valid = tok < T;
+    const bool valid = tl < RT && tok < T;
     float ms[kTopK], mp[kTopK];
     int mi[kTopK];
 #pragma unroll
@@ -149,35 +252,35 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
       mp[i] = 0.0f;
       mi[i] = -1;
     }
-    // Insertion with strict '>' (layer.cu:465-476): rank order is score
-    // descending, lower expert index first among equal scores.
-    for (int ee = 0; ee < kExperts; ++ee) {
-      const float score = s_score[tl][ee];
-      const float prob = s_prob[tl][ee];
-      if (score > ms[3]) {
-        if (score > ms[2]) {
-          ms[3] = ms[2]; mp[3] = mp[2]; mi[3] = mi[2];
-          if (score > ms[1]) {
-            ms[2] = ms[1]; mp[2] = mp[1]; mi[2] = mi[1];
-            if (score > ms[0]) {
-              ms[1] = ms[0]; mp[1] = mp[0]; mi[1] = mi[0];
-              ms[0] = score; mp[0] = prob; mi[0] = ee;
+    if (valid) {
+      // Insertion with strict '>' (layer.cu:465-476): rank order is score
+      // descending, lower expert index first among equal scores.
+      for (int ee = 0; ee < kExperts; ++ee) {
+        const float score = s_score[tl][ee];
+        const float prob = s_prob[tl][ee];
+        if (score > ms[3]) {
+          if (score > ms[2]) {
+            ms[3] = ms[2]; mp[3] = mp[2]; mi[3] = mi[2];
+            if (score > ms[1]) {
+              ms[2] = ms[1]; mp[2] = mp[1]; mi[2] = mi[1];
+              if (score > ms[0]) {
+                ms[1] = ms[0]; mp[1] = mp[0]; mi[1] = mi[0];
+                ms[0] = score; mp[0] = prob; mi[0] = ee;
+              } else {
+                ms[1] = score; mp[1] = prob; mi[1] = ee;
+              }
             } else {
-              ms[1] = score; mp[1] = prob; mi[1] = ee;
+              ms[2] = score; mp[2] = prob; mi[2] = ee;
             }
           } else {
-            ms[2] = score; mp[2] = prob; mi[2] = ee;
+            ms[3] = score; mp[3] = prob; mi[3] = ee;
           }
-        } else {
-          ms[3] = score; mp[3] = prob; mi[3] = ee;
         }
       }
-    }
-    float sum = 0.0f;  // layer.cu:480-482, rank order
+      float sum = 0.0f;  // layer.cu:480-482, rank order
 #pragma unroll
-    for (int i = 0; i < kTopK; ++i) sum += mp[i];
-    const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;  // layer.cu:484
-    if (valid) {
+      for (int i = 0; i < kTopK; ++i) sum += mp[i];
+      const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;  // layer.cu:484
 #pragma unroll
       for (int i = 0; i < kTopK; ++i) {
         a.s.idx[(size_t)tok * kTopK + i] = mi[i];
@@ -206,17 +309,20 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
     }
   }
   __syncthreads();
-  if (tid < kExperts) a.s.blk[b * kExperts + tid] = s_cnt[tid];
+  if (tid < kExperts) st_agent(&a.s.blk[tb * kExperts + tid], s_cnt[tid]);
 
-  // ---- last-block election: the block that finishes last builds the plan --
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  // ---- last-block election: the token block that finishes last plans -----
+  const int nb = gridDim.x / ES;
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
-  if (tid == 0) s_last = (fetch_add(&ctrl->router_done, 1) == (int)gridDim.x - 1);
+  if (tid == 0) {
+    s_flag = (fetch_add(&ctrl->router_done, 1) == nb - 1);
+    if (s_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
   __syncthreads();
-  if (!s_last) return;
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  if (!s_flag) return;
 
-  const int nb = gridDim.x;
+  const int e = tid & (kExperts - 1);
   const int part = tid >> 5;  // 8 parts x 32 experts
   const int per = (nb + 7) / 8;
   const int lo = part * per;
@@ -247,7 +353,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
   }
   __syncthreads();
   {
-    // block bases: offsets[e] + tokens of e in earlier router blocks
+    // block bases: offsets[e] + tokens of e in earlier token blocks
     int base = s_off[e] + s_part[part][e];
     for (int bb = lo; bb < hi; ++bb) {
       const int c = a.s.blk[bb * kExperts + e];
@@ -274,6 +380,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
     ctrl->p1_per_unit = p1u;
     ctrl->p2_per_unit = p2u;
     ctrl->n_rblocks = nb;
+    ctrl->rtokens = RT;
     ctrl->n_p1 = units * p1u;
     ctrl->n_p2 = units * p2u;
     ctrl->n_comb = (T + kCombineTokens - 1) / kCombineTokens;
@@ -288,7 +395,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
   __syncthreads();
   const int units = min(s_units, a.max_units);
   for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
-  if (tid == 0) ctrl->router_done = 0;  // every block has counted in
+  if (tid == 0) ctrl->router_done = 0;  // every token block has counted in
 }
 
 // ---------------------------------------------------------------------------
@@ -298,22 +405,22 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
 // Dispatch task q: slots of the 64 tokens of router block q (replaces
 // moe_scatter_kernel layer.cu:501-542: slot = block base + in-block rank, so
 // slots are stable by token; x itself is not copied, the GEMM gathers rows).
-__device__ void assign_task(const ExpertArgs &a, int q) {
+__device__ void assign_task(const ExpertArgs &a, int q, int rt) {
   const int tl = threadIdx.x >> 2, k = threadIdx.x & 3;
-  const int tok = q * kRouterTokens + tl;
-  if (tok < a.T) {
+  const int tok = q * rt + tl;
+  if (tl < rt && tok < a.T) {
     const int ee = a.s.idx[(size_t)tok * kTopK + k];
     if (ee >= 0 && ee < kExperts) {
       const int slot = a.s.blk[q * kExperts + ee] + a.s.pos[(size_t)tok * kTopK + k];
       if (slot >= 0 && slot < a.T * kTopK) {
-        a.s.pos[(size_t)tok * kTopK + k] = slot;
-        a.s.slot_token[slot] = tok;
+        st_agent(&a.s.pos[(size_t)tok * kTopK + k], slot);
+        st_agent(&a.s.slot_token[slot], tok);
       } else {  // inconsistent plan: flag it, never write out of range
-        a.s.pos[(size_t)tok * kTopK + k] = -1;
+        st_agent(&a.s.pos[(size_t)tok * kTopK + k], -1);
         __hip_atomic_store(&a.s.ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     } else {
-      a.s.pos[(size_t)tok * kTopK + k] = -1;
+      st_agent(&a.s.pos[(size_t)tok * kTopK + k], -1);
     }
   }
 }
@@ -547,8 +654,8 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
   for (int f = tid; f < BM * NC4; f += kThreads) {
     const int row = f / NC4, c4 = (f % NC4) * 4;
     if (row < rows_valid)
-      *reinterpret_cast<float4 *>(out + (size_t)row * ldo + col0 + c4) =
-          *reinterpret_cast<const float4 *>(Cs + row * CP + c4);
+      st_agent4(out + (size_t)row * ldo + col0 + c4,
+                *reinterpret_cast<const float4 *>(Cs + row * CP + c4));
   }
   __syncthreads();  // Cs aliases the slab buffers of the next tile
 }
@@ -573,14 +680,14 @@ void expert_mfma_kernel(ExpertArgs a) {
   const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
   const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
   const int H = a.H, I = a.I;
-  if (tid == 0) s_task = fetch_add(&c->head, 1);
+  if (tid == 0) s_task = claim(&c->head);
   __syncthreads();
   int task = s_task;
   while (task < ntot) {
     int next = 0;
-    if (tid == 0) next = fetch_add(&c->head, 1);  // claim ahead
+    if (tid == 0) next = claim(&c->head);  // claim ahead
     if (task < nb) {
-      assign_task(a, task);
+      assign_task(a, task, c->rtokens);
       block_signal(&c->assign_done);
     } else if (task < nb + n1) {
       const int q = task - nb;
@@ -623,84 +730,122 @@ void expert_mfma_kernel(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Weight-streaming kernel (small T): every weight byte is read once, as
-// coalesced 1 KiB wave loads; dot products on VALU against token rows staged
-// in LDS, then a wave butterfly reduction.
+// Weight-streaming kernel (small T).  Every weight byte is read once: a wave
+// owns 4 weight rows and loads each as 1 KiB coalesced float4 wave loads, all
+// issued up front and kept in registers while up to kStreamTokens token rows
+// at a time are staged in LDS and dotted against them on VALU.  The 64 lanes'
+// partial sums are combined by a butterfly transpose-reduction.
 // ---------------------------------------------------------------------------
 
-__device__ __forceinline__ float wave_sum(float v) {
+// Butterfly transpose-reduction of V values over the 64 lanes of a wave,
+// stopping when KEEP values remain per lane.  Afterwards every value is the
+// sum over all 64 lanes; lane l holds the group of KEEP consecutive values
+// starting at index KEEP * (l >> (6 - log2(V / KEEP))).
+template <int V, int KEEP>
+__device__ __forceinline__ void wave_transpose_sum(float (&v)[V]) {
+  const int lane = threadIdx.x & 63;
+  int off = 32;
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  for (int L = V; L > KEEP; L >>= 1, off >>= 1) {
+    const bool hi = (lane & off) != 0;
+#pragma unroll
+    for (int j = 0; j < L / 2; ++j) {
+      const float send = hi ? v[j] : v[L / 2 + j];
+      const float keep = hi ? v[L / 2 + j] : v[j];
+      v[j] = keep + __shfl_xor(send, off, 64);
+    }
+  }
+#pragma unroll
+  for (; off > 0; off >>= 1)
+#pragma unroll
+    for (int j = 0; j < KEEP; ++j) v[j] += __shfl_xor(v[j], off, 64);
 }
 
-// rows[r] (r < 4): this wave's weight rows, length K (K % 256 == 0).
-// xs: [ntok][K] staged token rows.  acc[r][m] = rows[r] . xs[m].
-__device__ __forceinline__ void stream_dots(const float *const rows[kStreamRowsPerWave],
-                                            const float *xs, int K, int ntok,
-                                            float acc[kStreamRowsPerWave][kStreamTokens]) {
+constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
+
+// Stage MT rows (length KCH*256, row m at base + off[m], off < 0 = zeros).
+template <int MT, int KCH>
+__device__ __forceinline__ void stage_tokens(float *xs, const float *base, const int *off) {
+  constexpr int K4 = KCH * 64;
+  constexpr int N = MT * K4;
+  constexpr int PER = (N + kThreads - 1) / kThreads;
+  float4 v[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int f = threadIdx.x + i * kThreads;
+    if (N % kThreads == 0 || f < N) {
+      const int m = f / K4, c4 = f % K4;
+      const int o = off[m];
+      v[i] = o >= 0 ? reinterpret_cast<const float4 *>(base + o)[c4]
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int f = threadIdx.x + i * kThreads;
+    if (N % kThreads == 0 || f < N) reinterpret_cast<float4 *>(xs)[f] = v[i];
+  }
+}
+
+// acc[r][m] = wv[r] . xs[m] (lane-partial: this lane's float4 of each chunk).
+template <int MT, int KCH>
+__device__ __forceinline__ void stream_dots(const float4 (&wv)[kStreamRowsPerWave][KCH],
+                                            const float *xs,
+                                            float (&acc)[kStreamRowsPerWave][MT]) {
+  constexpr int K = KCH * 256;
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int r = 0; r < kStreamRowsPerWave; ++r)
 #pragma unroll
-    for (int m = 0; m < kStreamTokens; ++m) acc[r][m] = 0.0f;
-  const int nch = K >> 8;
-  for (int c0 = 0; c0 < nch; c0 += 8) {
-    float4 wv[kStreamRowsPerWave][8];
+    for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+  for (int c = 0; c < KCH; ++c) {
 #pragma unroll
-      for (int r = 0; r < kStreamRowsPerWave; ++r)
-        if (c0 + c < nch)
-          wv[r][c] = *reinterpret_cast<const float4 *>(rows[r] + (c0 + c) * 256 + lane * 4);
+    for (int m = 0; m < MT; ++m) {
+      const float4 xv = *reinterpret_cast<const float4 *>(xs + m * K + c * 256 + lane * 4);
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      if (c0 + c >= nch) break;
-#pragma unroll
-      for (int m = 0; m < kStreamTokens; ++m) {
-        if (m >= ntok) break;
-        const float4 xv =
-            *reinterpret_cast<const float4 *>(xs + (size_t)m * K + (c0 + c) * 256 + lane * 4);
-#pragma unroll
-        for (int r = 0; r < kStreamRowsPerWave; ++r) {
-          acc[r][m] = __builtin_fmaf(wv[r][c].x, xv.x, acc[r][m]);
-          acc[r][m] = __builtin_fmaf(wv[r][c].y, xv.y, acc[r][m]);
-          acc[r][m] = __builtin_fmaf(wv[r][c].z, xv.z, acc[r][m]);
-          acc[r][m] = __builtin_fmaf(wv[r][c].w, xv.w, acc[r][m]);
-        }
+      for (int r = 0; r < kStreamRowsPerWave; ++r) {
+        acc[r][m] = __builtin_fmaf(wv[r][c].x, xv.x, acc[r][m]);
+        acc[r][m] = __builtin_fmaf(wv[r][c].y, xv.y, acc[r][m]);
+        acc[r][m] = __builtin_fmaf(wv[r][c].z, xv.z, acc[r][m]);
+        acc[r][m] = __builtin_fmaf(wv[r][c].w, xv.w, acc[r][m]);
       }
     }
   }
 }
 
-// Stage up to kStreamTokens rows (row_of[m], length K) into xs.
-__device__ __forceinline__ void stage_rows(float *xs, const float *const *row_of,
-                                           int ntok, int K) {
-  const int K4 = K >> 2;
-  float4 *d = reinterpret_cast<float4 *>(xs);
-  for (int f = threadIdx.x; f < ntok * K4; f += kThreads) {
-    const int m = f / K4, c4 = f % K4;
-    d[f] = reinterpret_cast<const float4 *>(row_of[m])[c4];
-  }
+template <int KCH>
+__device__ __forceinline__ void load_rows(const float *const (&rows)[kStreamRowsPerWave],
+                                          float4 (&wv)[kStreamRowsPerWave][KCH]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int c = 0; c < KCH; ++c)
+#pragma unroll
+    for (int r = 0; r < kStreamRowsPerWave; ++r)
+      wv[r][c] = *reinterpret_cast<const float4 *>(rows[r] + c * 256 + lane * 4);
 }
 
-__global__ __launch_bounds__(kThreads) void expert_stream_kernel(ExpertArgs a) {
-  extern __shared__ float xs[];  // [kStreamTokens][max(H, I)]
+// KCH1 = H / 256 (gate/up rows), KCH2 = I / 256 (down rows).
+template <int KCH1, int KCH2>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void expert_stream_kernel(ExpertArgs a) {
+  constexpr int MT = kStreamTokens, R = kStreamRowsPerWave;
+  extern __shared__ float xs[];  // [MT][max(H, I)]
   __shared__ int s_task;
-  __shared__ const float *s_row[kStreamTokens];
+  __shared__ int s_off[MT];
   Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
-  const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
+  const int p1u = c->p1_per_unit, p2u = c->p2_per_unit, rt = c->rtokens;
   const int H = a.H, I = a.I;
-  if (tid == 0) s_task = fetch_add(&c->head, 1);
+  if (tid == 0) s_task = claim(&c->head);
   __syncthreads();
   int task = s_task;
   while (task < ntot) {
     int next = 0;
-    if (tid == 0) next = fetch_add(&c->head, 1);
+    if (tid == 0) next = claim(&c->head);  // claim ahead
     if (task < nb) {
-      assign_task(a, task);
+      assign_task(a, task, rt);
       block_signal(&c->assign_done);
     } else if (task < nb + n1) {
       // gate/up: 8 consecutive n of one expert; wave w owns n0+2w, n0+2w+1
@@ -710,34 +855,34 @@ __global__ __launch_bounds__(kThreads) void expert_stream_kernel(ExpertArgs a) {
       const int cnt = c->counts[e], slot0 = c->offsets[e];
       const int n = ch * (kStreamRows / 2) + wave * 2;
       const float *wb = a.w.w13 + (size_t)e * 2 * I * H;
-      const float *rows[kStreamRowsPerWave];
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int nn = n + j;
-        const size_t prow = (size_t)(nn >> 5) * 64 + (nn & 31);
-        rows[j] = wb + prow * H;             // W1 row nn
-        rows[2 + j] = wb + (prow + 32) * H;  // W3 row nn
-      }
+      const size_t pa = (size_t)(n >> 5) * 64 + (n & 31);  // packed row of W1 n
+      const float *const rows[R] = {wb + pa * H, wb + (pa + 1) * H,
+                                    wb + (pa + 32) * H, wb + (pa + 33) * H};
+      float4 wv[R][KCH1];
+      load_rows<KCH1>(rows, wv);
       block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
-      for (int m0 = 0; m0 < cnt; m0 += kStreamTokens) {
-        const int nt = min(kStreamTokens, cnt - m0);
-        if (tid < nt) s_row[tid] = a.x + (size_t)slot_tok(a, slot0 + m0 + tid) * H;
+      for (int m0 = 0; m0 < cnt; m0 += MT) {
+        const int nt = min(MT, cnt - m0);
+        if (tid < MT) s_off[tid] = tid < nt ? slot_tok(a, slot0 + m0 + tid) * H : -1;
         __syncthreads();
-        stage_rows(xs, s_row, nt, H);
+        stage_tokens<MT, KCH1>(xs, a.x, s_off);
         __syncthreads();
-        float acc[kStreamRowsPerWave][kStreamTokens];
-        stream_dots(rows, xs, H, nt, acc);
+        float acc[R][MT];
+        stream_dots<MT, KCH1>(wv, xs, acc);
+        // value (j*MT + m)*2 + w: j = which n, w = 0 W1 / 1 W3 (row w*2 + j)
+        float v[2 * MT * 2];
 #pragma unroll
-        for (int m = 0; m < kStreamTokens; ++m) {
-          if (m >= nt) break;
-          const float h1a = wave_sum(acc[0][m]), h1b = wave_sum(acc[1][m]);
-          const float h3a = wave_sum(acc[2][m]), h3b = wave_sum(acc[3][m]);
-          if (lane == 0) {
-            float *irow = a.s.inter + (size_t)(slot0 + m0 + m) * I;
-            irow[n] = silu(h1a) * h3a;
-            irow[n + 1] = silu(h1b) * h3b;
-          }
-        }
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int m = 0; m < MT; ++m)
+#pragma unroll
+            for (int w = 0; w < 2; ++w) v[(j * MT + m) * 2 + w] = acc[w * 2 + j][m];
+        wave_transpose_sum<4 * MT, 2>(v);
+        constexpr int SH = 6 - log2i(2 * MT);
+        const int p = lane >> SH;  // pair index j*MT + m
+        const int j = p / MT, m = p % MT;
+        if ((lane & ((1 << SH) - 1)) == 0 && m < nt)
+          st_agent(&a.s.inter[(size_t)(slot0 + m0 + m) * I + n + j], silu(v[0]) * v[1]);
         __syncthreads();
       }
       block_signal(&a.s.dep[u]);
@@ -747,31 +892,31 @@ __global__ __launch_bounds__(kThreads) void expert_stream_kernel(ExpertArgs a) {
       const int u = q / p2u, ch = q % p2u;
       const int e = c->active[u];
       const int cnt = c->counts[e], slot0 = c->offsets[e];
-      const int h = ch * kStreamRows + wave * kStreamRowsPerWave;
-      const float *rows[kStreamRowsPerWave];
-#pragma unroll
-      for (int r = 0; r < kStreamRowsPerWave; ++r)
-        rows[r] = a.w.w2 + ((size_t)e * H + h + r) * I;
+      const int h = ch * kStreamRows + wave * R;
+      const float *wb = a.w.w2 + ((size_t)e * H + h) * I;
+      const float *const rows[R] = {wb, wb + I, wb + 2 * (size_t)I, wb + 3 * (size_t)I};
+      float4 wv[R][KCH2];
+      load_rows<KCH2>(rows, wv);
       block_wait(&a.s.dep[u], p1u, a.wait_limit, &c->err);
-      for (int m0 = 0; m0 < cnt; m0 += kStreamTokens) {
-        const int nt = min(kStreamTokens, cnt - m0);
-        if (tid < nt) s_row[tid] = a.s.inter + (size_t)(slot0 + m0 + tid) * I;
+      for (int m0 = 0; m0 < cnt; m0 += MT) {
+        const int nt = min(MT, cnt - m0);
+        if (tid < MT) s_off[tid] = tid < nt ? (slot0 + m0 + tid) * I : -1;
         __syncthreads();
-        stage_rows(xs, s_row, nt, I);
+        stage_tokens<MT, KCH2>(xs, a.s.inter, s_off);
         __syncthreads();
-        float acc[kStreamRowsPerWave][kStreamTokens];
-        stream_dots(rows, xs, I, nt, acc);
+        float acc[R][MT];
+        stream_dots<MT, KCH2>(wv, xs, acc);
+        float v[R * MT];  // value r*MT + m
 #pragma unroll
-        for (int m = 0; m < kStreamTokens; ++m) {
-          if (m >= nt) break;
-          float v[kStreamRowsPerWave];
+        for (int r = 0; r < R; ++r)
 #pragma unroll
-          for (int r = 0; r < kStreamRowsPerWave; ++r) v[r] = wave_sum(acc[r][m]);
-          if (lane == 0) {
-            float4 *o = reinterpret_cast<float4 *>(a.s.sout + (size_t)(slot0 + m0 + m) * H + h);
-            *o = make_float4(v[0], v[1], v[2], v[3]);
-          }
-        }
+          for (int m = 0; m < MT; ++m) v[r * MT + m] = acc[r][m];
+        wave_transpose_sum<R * MT, 1>(v);
+        constexpr int SH = 6 - log2i(R * MT);
+        const int i = lane >> SH;
+        const int r = i / MT, m = i % MT;
+        if ((lane & ((1 << SH) - 1)) == 0 && m < nt)
+          st_agent(&a.s.sout[(size_t)(slot0 + m0 + m) * H + h + r], v[0]);
         __syncthreads();
       }
       block_signal(&c->p2_done);
@@ -786,6 +931,9 @@ __global__ __launch_bounds__(kThreads) void expert_stream_kernel(ExpertArgs a) {
     task = s_task;
   }
 }
+
+// Streaming-kernel instantiations: (H/256, I/256) pairs it is compiled for.
+#define MOE_STREAM_SHAPES(X) X(8, 7)
 
 // ---------------------------------------------------------------------------
 // Weight packing (once per set_weights)
@@ -804,32 +952,51 @@ __global__ void pack_w13_kernel(float4 *dst, const float4 *w1, const float4 *w3,
   }
 }
 
-// dst[k4][e] = gate[e][4k4 .. 4k4+3]
-__global__ void pack_gate_kernel(float4 *dst, const float4 *gate, int E, int H4) {
-  const int n = E * H4;
-  for (int f = blockIdx.x * blockDim.x + threadIdx.x; f < n;
-       f += gridDim.x * blockDim.x) {
-    const int k4 = f / E, e = f % E;
-    dst[f] = gate[(size_t)e * H4 + k4];
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Launchers
 // ---------------------------------------------------------------------------
 
+// Router shapes: decode (T <= 64) spreads the gate over 4 expert splits of 8
+// tokens so more CUs share it and each lane runs one chain; larger T uses
+// 64-token blocks with all 32 experts and 8 chains per lane.
+constexpr int kSmallRT = 8, kSmallES = 4, kSmallKC = 256;
+constexpr int kLargeRT = 64, kLargeES = 1, kLargeKC = 64;
+
+int router_tokens_per_block(int T) { return T <= 64 ? kSmallRT : kLargeRT; }
+
 hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) {
-  const int nb = (a.T + kRouterTokens - 1) / kRouterTokens;
-  if (from_logits)
-    hipLaunchKernelGGL(router_kernel<true>, dim3(nb), dim3(kThreads), 0, st, a);
-  else
-    hipLaunchKernelGGL(router_kernel<false>, dim3(nb), dim3(kThreads), 0, st, a);
+  const bool small = a.T <= 64;
+  const int rt = small ? kSmallRT : kLargeRT;
+  const int nb = (a.T + rt - 1) / rt;
+  if (from_logits) {
+    // no gate GEMM: one block per token block finishes routing directly
+    if (small)
+      hipLaunchKernelGGL((router_kernel<true, kSmallRT, 1, kSmallKC>), dim3(nb), dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((router_kernel<true, kLargeRT, 1, kLargeKC>), dim3(nb), dim3(kThreads), 0, st, a);
+  } else if (small) {
+    hipLaunchKernelGGL((router_kernel<false, kSmallRT, kSmallES, kSmallKC>), dim3(nb * kSmallES),
+                       dim3(kThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((router_kernel<false, kLargeRT, kLargeES, kLargeKC>), dim3(nb * kLargeES),
+                       dim3(kThreads), 0, st, a);
+  }
   return hipGetLastError();
 }
 
 static size_t stream_lds_bytes(int H, int I) {
   return (size_t)kStreamTokens * (size_t)(H > I ? H : I) * sizeof(float);
 }
+
+static const void *stream_fn(int H, int I) {
+#define MOE_STREAM_CASE(K1, K2) \
+  if (H == (K1)*256 && I == (K2)*256) return reinterpret_cast<const void *>(&expert_stream_kernel<K1, K2>);
+  MOE_STREAM_SHAPES(MOE_STREAM_CASE)
+#undef MOE_STREAM_CASE
+  return nullptr;
+}
+
+bool stream_supported(int H, int I) { return stream_fn(H, I) != nullptr; }
 
 template <int BM> static void *mfma_fn() {
   return reinterpret_cast<void *>(&expert_mfma_kernel<BM>);
@@ -847,9 +1014,13 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
   switch (tile_rows) {
     case 0: {
       const size_t lds = stream_lds_bytes(a.H, a.I);
-      err = ensure_lds_attr(reinterpret_cast<const void *>(&expert_stream_kernel), lds);
+      const void *fn = stream_fn(a.H, a.I);
+      if (!fn) return hipErrorInvalidValue;
+      err = ensure_lds_attr(fn, lds);
       if (err != hipSuccess) return err;
-      hipLaunchKernelGGL(expert_stream_kernel, dim3(grid), dim3(kThreads), lds, st, a);
+      void *args[] = {const_cast<ExpertArgs *>(&a)};
+      err = hipLaunchKernel(fn, dim3(grid), dim3(kThreads), args, lds, st);
+      if (err != hipSuccess) return err;
       break;
     }
     case 32: {
@@ -892,11 +1063,13 @@ int expert_blocks_per_cu(int tile_rows) {
   int n = 0;
   hipError_t e = hipSuccess;
   switch (tile_rows) {
-    case 0:
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
-          &n, reinterpret_cast<const void *>(&expert_stream_kernel), kThreads,
-          stream_lds_bytes(2048, 2048));
+    case 0: {
+      const void *fn = stream_fn(2048, 1792);
+      if (!fn) return 1;
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads,
+                                                       stream_lds_bytes(2048, 1792));
       break;
+    }
     case 32:
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
           &n, mfma_fn<32>(), kThreads, Tile<32>::LDS_FLOATS * sizeof(float));
@@ -921,13 +1094,6 @@ hipError_t launch_pack_w13(float *dst, const float *w1, const float *w3, int H,
   hipLaunchKernelGGL(pack_w13_kernel, dim3(1024), dim3(256), 0, st,
                      reinterpret_cast<float4 *>(dst), reinterpret_cast<const float4 *>(w1),
                      reinterpret_cast<const float4 *>(w3), H / 4, I);
-  return hipGetLastError();
-}
-
-hipError_t launch_pack_gate(float4 *dst, const float *gate, int E, int H,
-                            hipStream_t st) {
-  hipLaunchKernelGGL(pack_gate_kernel, dim3(64), dim3(256), 0, st, dst,
-                     reinterpret_cast<const float4 *>(gate), E, H / 4);
   return hipGetLastError();
 }
 

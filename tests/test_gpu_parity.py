@@ -70,3 +70,52 @@ def test_every_kernel_plan(plan, block, real_weights, oracle_mod):
     ref = oracle_forward(oracle_mod, real_weights, x)
     check_routing(block.last_routing(), ref)
     np.testing.assert_allclose(y, ref["y"], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+def test_zipf_skew_t16384(block, real_weights, oracle_mod):
+    """Skewed routing: Zipf(1.2) expert frequencies, 3 empty experts, one expert
+    taking nearly every token.  Routing checked on all 16384 tokens; y on
+    every 16th token (the oracle's y rows are independent per token)."""
+    from final_amd import workloads as W
+    T = 16384
+    w = dict(real_weights)
+    w["bias"] = W.zipf_bias()
+    say(f"[zipf] T={T} plan={block.plan(T)}")
+    block.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+    try:
+        x = W.gen_x(T)
+        y = block.forward(x)
+        rt = block.last_routing()
+    finally:
+        rw = real_weights
+        block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
+    mask = np.zeros(T, np.uint8)
+    mask[::16] = 1
+    ref = oracle_forward(oracle_mod, w, x, token_mask=mask)
+    check_routing(rt, ref)
+    assert (rt["counts"] == 0).sum() >= 3
+    sel = mask.astype(bool)
+    np.testing.assert_allclose(y[sel], ref["y"][sel], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+def test_residual_fused_and_in_place(block, real_weights, oracle_mod):
+    """y = residual + MoE(x) (the decoder layer's add, layer.cu:1917), also
+    with y aliasing the residual buffer."""
+    from final_amd import hip
+    from final_amd import workloads as W
+    T = 300
+    x = W.gen_x(T, seed=7)
+    r = W.gen_x(T, seed=8)
+    ref = oracle_forward(oracle_mod, real_weights, x, residual=r)
+    dx = hip.DeviceArray.from_numpy(x)
+    dr = hip.DeviceArray.from_numpy(r)
+    dy = hip.DeviceArray((T, W.H))
+    block.forward_gpu(dx, dy, T, residual=dr)
+    hip.synchronize()
+    np.testing.assert_allclose(dy.download(), ref["y"], rtol=RTOL, atol=ATOL)
+    block.forward_gpu(dx, dr, T, residual=dr)  # in place
+    hip.synchronize()
+    block.check_device()
+    np.testing.assert_allclose(dr.download(), ref["y"], rtol=RTOL, atol=ATOL)
