@@ -1,0 +1,278 @@
+// C++ tests of the reference-shaped interface (include/layer.h, tensor.h,
+// model_loader.h) of the MoE block, driven the way the reference's engine
+// drives SparseMoeBlock (weights by tensor name through g_model_loader,
+// init_gpu, forward_gpu on device buffers).  Checks against the CPU oracle
+// (oracle/liboracle.so), which only tests link.
+//
+//   test_layer cpu   Tensor, model.bin loader, construction by name, errors
+//   test_layer gpu   SparseMoeBlock on the GPU vs the oracle
+#include <hip/hip_runtime_api.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <functional>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "layer.h"
+#include "model_loader.h"
+#include "tensor.h"
+
+extern "C" {
+#include "../../oracle/moe_oracle.h"
+}
+
+struct SparseMoeBlockTestAccess {
+  static void route(SparseMoeBlock &b, const Tensor &logits, std::vector<int> &idx,
+                    std::vector<float> &w) {
+    b.route_tokens(logits, idx, w);
+  }
+};
+
+namespace {
+
+int g_failed = 0, g_checks = 0;
+
+#define CHECK(cond)                                                        \
+  do {                                                                     \
+    ++g_checks;                                                            \
+    if (!(cond)) {                                                         \
+      ++g_failed;                                                          \
+      std::fprintf(stderr, "FAIL %s:%d: %s\n", __FILE__, __LINE__, #cond); \
+    }                                                                      \
+  } while (0)
+
+bool throws(const std::function<void()> &f) {
+  try {
+    f();
+  } catch (const std::exception &) {
+    return true;
+  }
+  return false;
+}
+
+struct Entry {
+  std::string name;
+  std::vector<uint32_t> shape;
+  std::vector<float> data;
+};
+
+// model.bin in the reference's format (src/model_loader.cpp:22-68).
+void write_model(const std::string &path, const std::vector<Entry> &es) {
+  uint64_t header = 12;
+  for (const auto &e : es) header += 4 + e.name.size() + 4 + 4 * e.shape.size() + 8;
+  std::ofstream f(path, std::ios::binary);
+  f.write("LFM2", 4);
+  const uint32_t version = 1, n = (uint32_t)es.size();
+  f.write((const char *)&version, 4);
+  f.write((const char *)&n, 4);
+  uint64_t off = header;
+  for (const auto &e : es) {
+    const uint32_t len = (uint32_t)e.name.size(), nd = (uint32_t)e.shape.size();
+    f.write((const char *)&len, 4);
+    f.write(e.name.data(), len);
+    f.write((const char *)&nd, 4);
+    f.write((const char *)e.shape.data(), 4 * nd);
+    f.write((const char *)&off, 8);
+    off += e.data.size() * 4;
+  }
+  for (const auto &e : es) f.write((const char *)e.data.data(), (std::streamsize)(e.data.size() * 4));
+}
+
+std::vector<float> normal(std::mt19937 &rng, size_t n, float sd) {
+  std::normal_distribution<float> d(0.0f, sd);
+  std::vector<float> v(n);
+  for (auto &x : v) x = d(rng);
+  return v;
+}
+
+constexpr int kH = 256, kI = 256, kE = 32, kLayer = 5;
+
+struct Weights {
+  std::vector<float> gate, bias, w1, w3, w2;  // w1/w3 [E][I][H], w2 [E][H][I]
+};
+
+Weights make_weights(unsigned seed) {
+  std::mt19937 rng(seed);
+  Weights w;
+  w.gate = normal(rng, (size_t)kE * kH, 0.1f);
+  w.bias = normal(rng, kE, 0.02f);
+  w.w1 = normal(rng, (size_t)kE * kI * kH, 0.05f);
+  w.w3 = normal(rng, (size_t)kE * kI * kH, 0.05f);
+  w.w2 = normal(rng, (size_t)kE * kH * kI, 0.05f);
+  return w;
+}
+
+std::string model_path() { return "test_layer_model.bin"; }
+
+void write_layer_model(const Weights &w) {
+  std::vector<Entry> es;
+  const std::string p = "layers." + std::to_string(kLayer) + ".feed_forward.";
+  es.push_back({p + "gate.weight", {kE, kH}, w.gate});
+  es.push_back({p + "expert_bias", {kE}, w.bias});
+  for (int e = 0; e < kE; ++e) {
+    const std::string q = p + "experts." + std::to_string(e) + ".";
+    es.push_back({q + "w1.weight", {kI, kH},
+                  std::vector<float>(w.w1.begin() + (size_t)e * kI * kH,
+                                     w.w1.begin() + (size_t)(e + 1) * kI * kH)});
+    es.push_back({q + "w2.weight", {kH, kI},
+                  std::vector<float>(w.w2.begin() + (size_t)e * kH * kI,
+                                     w.w2.begin() + (size_t)(e + 1) * kH * kI)});
+    es.push_back({q + "w3.weight", {kI, kH},
+                  std::vector<float>(w.w3.begin() + (size_t)e * kI * kH,
+                                     w.w3.begin() + (size_t)(e + 1) * kI * kH)});
+  }
+  write_model(model_path(), es);
+}
+
+void cpu_tests() {
+  // Tensor
+  Tensor t({2, 3});
+  CHECK(t.ndim() == 2 && t.size() == 6 && t.size(1) == 3 && t.size(-1) == 3);
+  for (size_t i = 0; i < 6; ++i) t[i] = (float)i;
+  CHECK(t.at(1, 2) == 5.0f);
+  Tensor c = t;  // deep copy
+  c[0] = 42.0f;
+  CHECK(t[0] == 0.0f);
+  Tensor v = t.view({3, 2});  // shares data
+  v[1] = 7.0f;
+  CHECK(t[1] == 7.0f);
+  CHECK(throws([&] { t.view({4, 2}); }));
+  CHECK(throws([&] { t.reshape({5}); }));
+  CHECK(throws([&] { t.size(2); }));
+  Tensor tt = t.transpose(0, 1);
+  CHECK(tt.shape()[0] == 3 && tt.at(2, 1) == t.at(1, 2));
+  Tensor s = t.slice(1, 1, 3);
+  CHECK(s.shape()[1] == 2 && s.at(1, 0) == t.at(1, 1));
+  Tensor m = std::move(c);
+  CHECK(m[0] == 42.0f && c.size() == 0);
+  t.save_to_file("test_layer_tensor.bin");
+  Tensor r = Tensor::load_from_file("test_layer_tensor.bin");
+  CHECK(r.shape() == t.shape() && std::memcmp(r.data(), t.data(), 24) == 0);
+  CHECK(throws([] { Tensor::load_from_file("no_such_file.bin"); }));
+
+  // model.bin loader and construction by name
+  Weights w = make_weights(1);
+  write_layer_model(w);
+  g_model_loader = std::make_unique<ModelLoader>(model_path());
+  const std::string p = "layers." + std::to_string(kLayer) + ".feed_forward.";
+  CHECK(g_model_loader->num_tensors() == 2 + 3 * kE);
+  CHECK(g_model_loader->has_tensor(p + "gate.weight"));
+  CHECK(g_model_loader->get_shape(p + "experts.3.w2.weight") == std::vector<size_t>({kH, kI}));
+  Tensor g = Tensor::load_from_file(p + "gate.weight");
+  CHECK(std::memcmp(g.data(), w.gate.data(), w.gate.size() * 4) == 0);
+  CHECK(throws([&] { g_model_loader->load_tensor("layers.0.missing"); }));
+  MLP mlp(p + "experts.7.w1.weight", p + "experts.7.w2.weight", p + "experts.7.w3.weight");
+  CHECK(std::memcmp(mlp.w3().data(), w.w3.data() + (size_t)7 * kI * kH, (size_t)kI * kH * 4) == 0);
+  CHECK(throws([&] { mlp.forward_gpu(nullptr, nullptr, 1, 1, kH, 0); }));
+  SparseMoeBlock blk(kLayer);
+  CHECK(blk.layer_idx() == kLayer && blk.context() == nullptr);
+  CHECK(throws([&] { blk.forward_gpu(nullptr, nullptr, 1, 1, kH, 0); }));  // before init_gpu
+  CHECK(throws([] { SparseMoeBlock bad(kLayer + 1); }));                  // tensors absent
+  {
+    std::ofstream f("test_layer_bad.bin", std::ios::binary);
+    f.write("XXXX", 4);
+  }
+  CHECK(throws([] { ModelLoader l("test_layer_bad.bin"); }));
+  CHECK(throws([] { ModelLoader l("no_such_model.bin"); }));
+  g_model_loader.reset();
+}
+
+bool close(float a, float b) { return std::fabs(a - b) <= 1e-4f + 1e-3f * std::fabs(b); }
+
+void gpu_tests() {
+  Weights w = make_weights(2);
+  write_layer_model(w);
+  g_model_loader = std::make_unique<ModelLoader>(model_path());
+  SparseMoeBlock blk(kLayer);  // by name, like DecoderLayer (layer.cu:1803-1804)
+  blk.set_max_tokens(512);
+  blk.init_gpu();
+  g_model_loader.reset();
+
+  for (int T : {1, 37, 300}) {
+    std::mt19937 rng(100 + T);
+    std::vector<float> x = normal(rng, (size_t)T * kH, 1.0f);
+    std::vector<float> res = normal(rng, (size_t)T * kH, 1.0f);
+    std::vector<float> yref((size_t)T * kH), yres((size_t)T * kH), lref((size_t)T * kE);
+    std::vector<int> iref((size_t)T * 4), cref(kE);
+    std::vector<float> wref((size_t)T * 4);
+    CHECK(orc_moe_forward(x.data(), w.gate.data(), w.bias.data(), w.w1.data(), w.w3.data(),
+                          w.w2.data(), nullptr, T, kH, kI, kE, nullptr, yref.data(), lref.data(),
+                          iref.data(), wref.data(), cref.data()) == 0);
+    CHECK(orc_moe_forward(x.data(), w.gate.data(), w.bias.data(), w.w1.data(), w.w3.data(),
+                          w.w2.data(), res.data(), T, kH, kI, kE, nullptr, yres.data(), nullptr,
+                          nullptr, nullptr, nullptr) == 0);
+    // device path: forward_gpu(x, y, batch, seq_len, hidden, stream)
+    float *dx = nullptr, *dy = nullptr, *dr = nullptr;
+    const size_t bytes = (size_t)T * kH * 4;
+    CHECK(hipMalloc(&dx, bytes) == hipSuccess && hipMalloc(&dy, bytes) == hipSuccess &&
+          hipMalloc(&dr, bytes) == hipSuccess);
+    hipStream_t st;
+    CHECK(hipStreamCreate(&st) == hipSuccess);
+    CHECK(hipMemcpy(dx, x.data(), bytes, hipMemcpyHostToDevice) == hipSuccess);
+    CHECK(hipMemcpy(dr, res.data(), bytes, hipMemcpyHostToDevice) == hipSuccess);
+    blk.forward_gpu(dx, dy, 1, T, kH, st);
+    std::vector<float> y((size_t)T * kH), yr((size_t)T * kH);
+    CHECK(hipStreamSynchronize(st) == hipSuccess);
+    CHECK(hipMemcpy(y.data(), dy, bytes, hipMemcpyDeviceToHost) == hipSuccess);
+    blk.forward_gpu(dx, dr, dr, 1, T, kH, st);  // residual fused, in place
+    CHECK(hipStreamSynchronize(st) == hipSuccess);
+    CHECK(hipMemcpy(yr.data(), dr, bytes, hipMemcpyDeviceToHost) == hipSuccess);
+    int bad = 0;
+    for (size_t i = 0; i < y.size(); ++i) bad += !close(y[i], yref[i]) + !close(yr[i], yres[i]);
+    CHECK(bad == 0);
+    // host path: forward(x, y, router_logits), logits bit-exact
+    Tensor tx({(size_t)T, (size_t)kH}, x.data(), true), ty, tl;
+    blk.forward(tx, ty, tl);
+    CHECK(std::memcmp(tl.data(), lref.data(), lref.size() * 4) == 0);
+    bad = 0;
+    for (size_t i = 0; i < y.size(); ++i) bad += !close(ty.data()[i], yref[i]);
+    CHECK(bad == 0);
+    // route_tokens on the oracle's logits: indices and weights bit-exact
+    std::vector<int> idx;
+    std::vector<float> wt;
+    SparseMoeBlockTestAccess::route(blk, tl, idx, wt);
+    CHECK(idx == iref);
+    CHECK(std::memcmp(wt.data(), wref.data(), wref.size() * 4) == 0);
+    (void)hipFree(dx);
+    (void)hipFree(dy);
+    (void)hipFree(dr);
+    (void)hipStreamDestroy(st);
+    std::printf("gpu T=%d ok\n", T);
+  }
+  // route_tokens on crafted logits (equal logits, large margins) vs the oracle
+  Tensor lt({3, (size_t)kE});
+  lt.zero();
+  for (int e : {30, 3, 17, 8}) lt.at(1, e) = 5.0f;
+  for (int e = 0; e < kE; ++e) lt.at(2, e) = (float)(e % 4) * 0.25f;
+  std::vector<int> idx, iref(12), cnt(kE);
+  std::vector<float> wt, wref(12);
+  SparseMoeBlockTestAccess::route(blk, lt, idx, wt);
+  orc_route(lt.data(), w.bias.data(), 3, kE, iref.data(), wref.data(), cnt.data());
+  CHECK(idx == iref);
+  CHECK(std::memcmp(wt.data(), wref.data(), wref.size() * 4) == 0);
+}
+
+}  // namespace
+
+int main(int argc, char **argv) {
+  const std::string mode = argc > 1 ? argv[1] : "cpu";
+  try {
+    if (mode == "cpu") cpu_tests();
+    else if (mode == "gpu") gpu_tests();
+    else {
+      std::fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
+      return 2;
+    }
+  } catch (const std::exception &e) {
+    std::fprintf(stderr, "FAIL exception: %s\n", e.what());
+    return 1;
+  }
+  std::printf("%s: %d checks, %d failed\n", mode.c_str(), g_checks, g_failed);
+  return g_failed ? 1 : 0;
+}
