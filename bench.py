@@ -46,6 +46,9 @@ def parse():
                         "exceed the 256 MB Infinity Cache for small T)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-threads", type=int, default=0)
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run device-to-device copies of MIB MiB (the runtime's copy "
+                        "kernel), as the known-size reference for HBM byte counters")
     return p.parse_args()
 
 
@@ -77,6 +80,15 @@ def main():
 
     from final_amd import SparseMoeBlock, hip
     from final_amd import workloads as W
+
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src, dst = hip.DeviceArray((n // 4,)), hip.DeviceArray((n // 4,))
+        for _ in range(3):
+            hip.copy_device(dst, src)
+        hip.synchronize()
+        print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
+        return
 
     wl = W.WORKLOADS[args.workload]
     T = wl.T

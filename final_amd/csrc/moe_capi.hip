@@ -151,6 +151,11 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
   const size_t Tm = d.max_tokens, S = Tm * kTopK;
   const size_t nb = (Tm + kMinRouterTokens - 1) / kMinRouterTokens;
   ctx->max_units = (int)(S / 32 + E + 1);
+  // inter and sout are addressed with 32-bit byte offsets
+  if (S * (H > I ? H : I) * sizeof(float) >= 0xFFFFFFF0ull) {
+    delete ctx;
+    return MOE_ERR_UNSUPPORTED;
+  }
   int rc = MOE_OK;
   if ((rc = dev_alloc(ctx, &ctx->gate, E * H)) ||
       (rc = dev_alloc(ctx, &ctx->bias, E)) ||
@@ -169,6 +174,8 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
     delete ctx;
     return rc;
   }
+  ctx->s.inter_bytes = (uint32_t)(S * I * sizeof(float));
+  ctx->s.sout_bytes = (uint32_t)(S * H * sizeof(float));
   char *ctrl_mem = nullptr;
   const size_t ctrl_bytes = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
   if ((rc = dev_alloc(ctx, &ctrl_mem, ctrl_bytes))) {

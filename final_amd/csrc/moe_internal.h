@@ -61,6 +61,8 @@ struct Scratch {
   int *slot_token;       // [4 Tmax]
   float *inter;          // [4 Tmax][I]
   float *sout;           // [4 Tmax][H]
+  uint32_t inter_bytes;  // allocation sizes (< 4 GiB: 32-bit buffer offsets)
+  uint32_t sout_bytes;
   Ctrl *ctrl;
   int *dep;              // [max_units]
 };

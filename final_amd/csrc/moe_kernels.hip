@@ -24,6 +24,18 @@
 namespace moe {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+// Native 4-wide vector for values held in registers across loop iterations
+// (HIP's float4 is a union-based struct that the optimiser may leave in
+// scratch memory when it is carried around a loop).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4 ld4(const float *p) { return *reinterpret_cast<const f32x4 *>(p); }
+__device__ __forceinline__ void st4(float *p, f32x4 v) { *reinterpret_cast<f32x4 *>(p) = v; }
+
+// Buffer-resource word 3 for raw (untyped) buffer access on CDNA, and the
+// cache-policy bit that makes a store agent-coherent (written through L2).
+constexpr int kBufferRsrcWord3 = 0x00020000;
+constexpr int kCachePolicySc1 = 16;
 
 // ---------------------------------------------------------------------------
 // Cross-block synchronisation (agent scope: coherent across the 8 XCD L2s)
@@ -57,12 +69,19 @@ __device__ __forceinline__ void st_agent(float *p, float v) {
 __device__ __forceinline__ void st_agent(int *p, int v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void st_agent4(float *p, float4 v) {
-  st_agent(p + 0, v.x);
-  st_agent(p + 1, v.y);
-  st_agent(p + 2, v.z);
-  st_agent(p + 3, v.w);
-}
+
+// 16-byte agent-scope stores through a buffer resource: one sc1 store per
+// float4 (a dword-wide atomic store per element would send 4 write
+// transactions per 16 bytes), and the descriptor's byte range drops any store
+// past the end of the buffer.
+struct AgentOut {
+  __amdgpu_buffer_rsrc_t rsrc;
+  __device__ AgentOut(float *base, uint32_t bytes)
+      : rsrc(__builtin_amdgcn_make_buffer_rsrc(base, 0, (int)bytes, kBufferRsrcWord3)) {}
+  __device__ void store(uint32_t byte_off, f32x4 v) const {
+    __builtin_amdgcn_raw_buffer_store_b128(v, rsrc, byte_off, 0, kCachePolicySc1);
+  }
+};
 
 // Block-wide: wait until *p >= target (thread 0 polls), then acquire.
 __device__ void block_wait(const int *p, int target, int limit, int *err) {
@@ -144,54 +163,54 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
   Ctrl *ctrl = a.s.ctrl;
 
   if (!FROM_LOGITS) {
-    // staging map: thread -> (row, float4 column) of a KC-wide chunk
+    // staging map: thread -> (row, float4 column) of a KC-wide chunk; the
+    // X_PER (G_PER) passes cover the RT (EPB) rows exactly
     constexpr int KV = KC / 4, RPP = kThreads / KV;
+    static_assert(C::X_PER * RPP == RT && C::G_PER * RPP == EPB, "exact staging passes");
     const int srow = tid / KV, sc4 = (tid % KV) * 4;
-    float4 px[C::X_PER], pg[C::G_PER];
-    auto fetch = [&](int k0) {
+    const float *xrow[C::X_PER];
 #pragma unroll
-      for (int i = 0; i < C::X_PER; ++i) {
-        const int r = srow + i * RPP;
-        if (r < RT) {
-          int tok = t0 + r;
-          tok = tok < T ? tok : T - 1;  // rows past T: a copy, never stored
-          px[i] = *reinterpret_cast<const float4 *>(a.x + (size_t)tok * H + k0 + sc4);
-        }
-      }
-#pragma unroll
-      for (int i = 0; i < C::G_PER; ++i) {
-        const int r = srow + i * RPP;
-        if (r < EPB)
-          pg[i] = *reinterpret_cast<const float4 *>(a.w.gate + (size_t)(e0 + r) * H + k0 + sc4);
-      }
-    };
+    for (int i = 0; i < C::X_PER; ++i) {
+      int tok = t0 + srow + i * RPP;
+      tok = tok < T ? tok : T - 1;  // rows past T: a copy, never stored
+      xrow[i] = a.x + (size_t)tok * H + sc4;
+    }
+    const float *grow = a.w.gate + (size_t)(e0 + srow) * H + sc4;
+    f32x4 px[C::X_PER], pg[C::G_PER];
     float acc[TPL];
 #pragma unroll
     for (int j = 0; j < TPL; ++j) acc[j] = 0.0f;
-    fetch(0);
+#pragma unroll
+    for (int i = 0; i < C::X_PER; ++i) px[i] = ld4(xrow[i]);
+#pragma unroll
+    for (int i = 0; i < C::G_PER; ++i)
+      pg[i] = ld4(grow + (size_t)i * RPP * H);
     for (int k0 = 0; k0 < H; k0 += KC) {
       __syncthreads();  // the previous chunk's readers are done
 #pragma unroll
-      for (int i = 0; i < C::X_PER; ++i) {
-        const int r = srow + i * RPP;
-        if (r < RT) *reinterpret_cast<float4 *>(xs + r * PITCH + sc4) = px[i];
-      }
+      for (int i = 0; i < C::X_PER; ++i)
+        st4(xs + (srow + i * RPP) * PITCH + sc4, px[i]);
 #pragma unroll
-      for (int i = 0; i < C::G_PER; ++i) {
-        const int r = srow + i * RPP;
-        if (r < EPB) *reinterpret_cast<float4 *>(gs + r * PITCH + sc4) = pg[i];
-      }
+      for (int i = 0; i < C::G_PER; ++i)
+        st4(gs + (srow + i * RPP) * PITCH + sc4, pg[i]);
       __syncthreads();
-      if (k0 + KC < H) fetch(k0 + KC);  // in flight during this chunk's FMAs
+      if (k0 + KC < H) {  // next chunk in flight during this chunk's FMAs
+#pragma unroll
+        for (int i = 0; i < C::X_PER; ++i)
+          px[i] = ld4(xrow[i] + k0 + KC);
+#pragma unroll
+        for (int i = 0; i < C::G_PER; ++i)
+          pg[i] = ld4(grow + (size_t)i * RPP * H + k0 + KC);
+      }
       if (chain_lane) {
         const float *gp = gs + el * PITCH;
         const float *xp = xs + grp * TPL * PITCH;
 #pragma unroll 4
         for (int k = 0; k < KC; k += 4) {
-          const float4 gv = *reinterpret_cast<const float4 *>(gp + k);
+          const f32x4 gv = ld4(gp + k);
 #pragma unroll
           for (int j = 0; j < TPL; ++j) {
-            const float4 xv = *reinterpret_cast<const float4 *>(xp + j * PITCH + k);
+            const f32x4 xv = ld4(xp + j * PITCH + k);
             acc[j] = __builtin_fmaf(xv.x, gv.x, acc[j]);
             acc[j] = __builtin_fmaf(xv.y, gv.y, acc[j]);
             acc[j] = __builtin_fmaf(xv.z, gv.z, acc[j]);
@@ -520,6 +539,34 @@ template <int BM> struct Tile {
   static_assert(BK % 8 == 0, "k groups of 8");
 };
 
+// Slab staging of the MFMA tile: global float4 loads into registers (A rows
+// gathered, a_src < 0 = zero row; B rows contiguous with stride K), then LDS
+// stores.  Fully unrolled with compile-time indices so the arrays stay in
+// registers while the loads are in flight.
+template <int A_PER, int B_PER, int RPP>
+__device__ __forceinline__ void slab_load(f32x4 (&ra)[A_PER], f32x4 (&rb)[B_PER],
+                                          const int (&a_src)[A_PER], const float *abase,
+                                          const float *bsrc, int K, int k0) {
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i) {
+    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+    ra[i] = a_src[i] >= 0 ? ld4(abase + a_src[i] + k0) : zero;
+  }
+#pragma unroll
+  for (int i = 0; i < B_PER; ++i) rb[i] = ld4(bsrc + (size_t)i * RPP * K + k0);
+}
+
+template <int BM, int A_PER, int B_PER, int RPP, int PITCH>
+__device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4 (&rb)[B_PER],
+                                           float *As, float *Bs, int lds_st, int lrow) {
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i)
+    if (A_PER * RPP <= BM || lrow + i * RPP < BM)  // rows past BM: threads of a partial pass
+      st4(As + lds_st + i * RPP * PITCH, ra[i]);
+#pragma unroll
+  for (int i = 0; i < B_PER; ++i) st4(Bs + lds_st + i * RPP * PITCH, rb[i]);
+}
+
 // One output tile of C[rows][cols] = A[rows][K] . B[cols][K]^T.
 // A rows are gathered: row r starts at abase + aoff[r] (aoff in LDS; rows at
 // or past rows_valid are zero).  B rows are contiguous with stride K from
@@ -531,8 +578,8 @@ template <int BM> struct Tile {
 template <int BM, bool GATED>
 __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
                                           const int *aoff, int rows_valid,
-                                          const float *brow0, int K, float *out,
-                                          int ldo, int col0) {
+                                          const float *brow0, int K, const AgentOut &out,
+                                          int row0, int ldo, int col0) {
   using TL = Tile<BM>;
   constexpr int WM = TL::WM, BK = TL::BK, PITCH = TL::PITCH, KV = TL::KV;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
@@ -554,25 +601,7 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
   const float *bsrc = brow0 + (size_t)lrow * K + lc4;
   const int lds_st = lrow * PITCH + lc4;
 
-  float4 ra[A_PER], rb[B_PER];
-#define MOE_LOAD_SLAB(k0)                                                      \
-  do {                                                                         \
-    _Pragma("unroll") for (int i = 0; i < A_PER; ++i) ra[i] =                  \
-        a_src[i] >= 0 ? *reinterpret_cast<const float4 *>(abase + a_src[i] + (k0)) \
-                      : make_float4(0.f, 0.f, 0.f, 0.f);                       \
-    _Pragma("unroll") for (int i = 0; i < B_PER; ++i) rb[i] =                  \
-        *reinterpret_cast<const float4 *>(bsrc + (size_t)i * ROWS_PER_PASS * K + (k0)); \
-  } while (0)
-#define MOE_STORE_SLAB(buf)                                                    \
-  do {                                                                         \
-    _Pragma("unroll") for (int i = 0; i < A_PER; ++i) if (lrow + i * ROWS_PER_PASS < BM) \
-        *reinterpret_cast<float4 *>(As + (buf) * BM * PITCH + lds_st +         \
-                                    i * ROWS_PER_PASS * PITCH) = ra[i];        \
-    _Pragma("unroll") for (int i = 0; i < B_PER; ++i)                          \
-        *reinterpret_cast<float4 *>(Bs + (buf) * TL::BN * PITCH + lds_st +     \
-                                    i * ROWS_PER_PASS * PITCH) = rb[i];        \
-  } while (0)
-
+  f32x4 ra[A_PER], rb[B_PER];
   floatx16 acc[WM][2];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
@@ -587,45 +616,43 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
   const int wrows = min(max(rows_valid - wrow0, 0), WM * 32);
 
   const int nslab = K / BK;
-  MOE_LOAD_SLAB(0);
-  MOE_STORE_SLAB(0);
+  slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra, rb, a_src, abase, bsrc, K, 0);
+  slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(ra, rb, As, Bs, lds_st, lrow);
   __syncthreads();
   const int lr = lane & 31, lh = (lane >> 5) * 4;
   const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
   const float *b_rd = Bs + (wn * 64 + lr) * PITCH + lh;
   for (int s = 0; s < nslab; ++s) {
     const int cur = s & 1;
-    if (s + 1 < nslab) MOE_LOAD_SLAB((s + 1) * BK);
+    if (s + 1 < nslab)
+      slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra, rb, a_src, abase, bsrc, K, (s + 1) * BK);
     const float *Ac = a_rd + cur * BM * PITCH;
     const float *Bc = b_rd + cur * TL::BN * PITCH;
     if (wrows > 0) {
 #pragma unroll
       for (int g8 = 0; g8 < BK / 8; ++g8) {
-        float4 af[WM], bf[2];
+        f32x4 af[WM], bf[2];
 #pragma unroll
-        for (int i = 0; i < WM; ++i)
-          af[i] = *reinterpret_cast<const float4 *>(Ac + i * 32 * PITCH + g8 * 8);
+        for (int i = 0; i < WM; ++i) af[i] = ld4(Ac + i * 32 * PITCH + g8 * 8);
 #pragma unroll
-        for (int c = 0; c < 2; ++c)
-          bf[c] = *reinterpret_cast<const float4 *>(Bc + c * 32 * PITCH + g8 * 8);
+        for (int c = 0; c < 2; ++c) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
 #pragma unroll
         for (int i = 0; i < WM; ++i) {
           if (i > 0 && wrows <= 32) break;
 #pragma unroll
           for (int c = 0; c < 2; ++c) {
-            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].x, bf[c].x, acc[i][c], 0, 0, 0);
-            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].y, bf[c].y, acc[i][c], 0, 0, 0);
-            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].z, bf[c].z, acc[i][c], 0, 0, 0);
-            acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i].w, bf[c].w, acc[i][c], 0, 0, 0);
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[c][q], acc[i][c], 0, 0, 0);
           }
         }
       }
     }
-    if (s + 1 < nslab) MOE_STORE_SLAB(cur ^ 1);
+    if (s + 1 < nslab)
+      slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(
+          ra, rb, As + (cur ^ 1) * BM * PITCH, Bs + (cur ^ 1) * TL::BN * PITCH, lds_st, lrow);
     __syncthreads();
   }
-#undef MOE_LOAD_SLAB
-#undef MOE_STORE_SLAB
 
   // Epilogue through LDS (the slab buffers are free after the last barrier):
   // results are written as a [BM][NC] tile, then stored as whole-row float4s.
@@ -654,8 +681,8 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
   for (int f = tid; f < BM * NC4; f += kThreads) {
     const int row = f / NC4, c4 = (f % NC4) * 4;
     if (row < rows_valid)
-      st_agent4(out + (size_t)row * ldo + col0 + c4,
-                *reinterpret_cast<const float4 *>(Cs + row * CP + c4));
+      out.store((uint32_t)(((size_t)(row0 + row) * ldo + col0 + c4) * sizeof(float)),
+                ld4(Cs + row * CP + c4));
   }
   __syncthreads();  // Cs aliases the slab buffers of the next tile
 }
@@ -680,6 +707,7 @@ void expert_mfma_kernel(ExpertArgs a) {
   const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
   const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
   const int H = a.H, I = a.I;
+  const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
   if (tid == 0) s_task = claim(&c->head);
   __syncthreads();
   int task = s_task;
@@ -700,8 +728,8 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
       __syncthreads();
       const float *brow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TL::BN) * H;
-      mfma_tile<BM, true>(lds, a.x, s_aoff, rows, brow0, H,
-                          a.s.inter + (size_t)slot0 * I, I, nt * (TL::BN / 2));
+      mfma_tile<BM, true>(lds, a.x, s_aoff, rows, brow0, H, inter_out, slot0, I,
+                          nt * (TL::BN / 2));
       block_signal(&a.s.dep[u]);
     } else if (task < nb + n1 + n2) {
       const int q = task - nb - n1;
@@ -715,7 +743,7 @@ void expert_mfma_kernel(ExpertArgs a) {
       __syncthreads();
       const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
       mfma_tile<BM, false>(lds, a.s.inter + (size_t)slot0 * I, s_aoff, rows, brow0, I,
-                           a.s.sout + (size_t)slot0 * H, H, ht * TL::BN);
+                           sout_out, slot0, H, ht * TL::BN);
       block_signal(&c->p2_done);
     } else {
       const int q = task - nb - n1 - n2;
@@ -750,8 +778,12 @@ __device__ __forceinline__ void wave_transpose_sum(float (&v)[V]) {
     const bool hi = (lane & off) != 0;
 #pragma unroll
     for (int j = 0; j < L / 2; ++j) {
-      const float send = hi ? v[j] : v[L / 2 + j];
-      const float keep = hi ? v[L / 2 + j] : v[j];
+      float lo_v = v[j], hi_v = v[L / 2 + j];
+      // keep both halves as register values: a select between two array
+      // elements would otherwise become a dynamically indexed (scratch) load
+      asm volatile("" : "+v"(lo_v), "+v"(hi_v));
+      const float send = hi ? lo_v : hi_v;
+      const float keep = hi ? hi_v : lo_v;
       v[j] = keep + __shfl_xor(send, off, 64);
     }
   }
@@ -769,27 +801,25 @@ __device__ __forceinline__ void stage_tokens(float *xs, const float *base, const
   constexpr int K4 = KCH * 64;
   constexpr int N = MT * K4;
   constexpr int PER = (N + kThreads - 1) / kThreads;
-  float4 v[PER];
+  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+  f32x4 v[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int f = threadIdx.x + i * kThreads;
-    if (N % kThreads == 0 || f < N) {
-      const int m = f / K4, c4 = f % K4;
-      const int o = off[m];
-      v[i] = o >= 0 ? reinterpret_cast<const float4 *>(base + o)[c4]
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
+    const int m = f / K4, c4 = f % K4;
+    const int o = (N % kThreads == 0 || f < N) ? off[m] : -1;
+    v[i] = o >= 0 ? ld4(base + o + c4 * 4) : zero;
   }
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int f = threadIdx.x + i * kThreads;
-    if (N % kThreads == 0 || f < N) reinterpret_cast<float4 *>(xs)[f] = v[i];
+    if (N % kThreads == 0 || f < N) st4(xs + f * 4, v[i]);
   }
 }
 
 // acc[r][m] = wv[r] . xs[m] (lane-partial: this lane's float4 of each chunk).
 template <int MT, int KCH>
-__device__ __forceinline__ void stream_dots(const float4 (&wv)[kStreamRowsPerWave][KCH],
+__device__ __forceinline__ void stream_dots(const f32x4 (&wv)[kStreamRowsPerWave][KCH],
                                             const float *xs,
                                             float (&acc)[kStreamRowsPerWave][MT]) {
   constexpr int K = KCH * 256;
@@ -802,27 +832,23 @@ __device__ __forceinline__ void stream_dots(const float4 (&wv)[kStreamRowsPerWav
   for (int c = 0; c < KCH; ++c) {
 #pragma unroll
     for (int m = 0; m < MT; ++m) {
-      const float4 xv = *reinterpret_cast<const float4 *>(xs + m * K + c * 256 + lane * 4);
+      const f32x4 xv = ld4(xs + m * K + c * 256 + lane * 4);
 #pragma unroll
-      for (int r = 0; r < kStreamRowsPerWave; ++r) {
-        acc[r][m] = __builtin_fmaf(wv[r][c].x, xv.x, acc[r][m]);
-        acc[r][m] = __builtin_fmaf(wv[r][c].y, xv.y, acc[r][m]);
-        acc[r][m] = __builtin_fmaf(wv[r][c].z, xv.z, acc[r][m]);
-        acc[r][m] = __builtin_fmaf(wv[r][c].w, xv.w, acc[r][m]);
-      }
+      for (int r = 0; r < kStreamRowsPerWave; ++r)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) acc[r][m] = __builtin_fmaf(wv[r][c][q], xv[q], acc[r][m]);
     }
   }
 }
 
 template <int KCH>
 __device__ __forceinline__ void load_rows(const float *const (&rows)[kStreamRowsPerWave],
-                                          float4 (&wv)[kStreamRowsPerWave][KCH]) {
+                                          f32x4 (&wv)[kStreamRowsPerWave][KCH]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int c = 0; c < KCH; ++c)
 #pragma unroll
-    for (int r = 0; r < kStreamRowsPerWave; ++r)
-      wv[r][c] = *reinterpret_cast<const float4 *>(rows[r] + c * 256 + lane * 4);
+    for (int r = 0; r < kStreamRowsPerWave; ++r) wv[r][c] = ld4(rows[r] + c * 256 + lane * 4);
 }
 
 // KCH1 = H / 256 (gate/up rows), KCH2 = I / 256 (down rows).
@@ -858,7 +884,7 @@ void expert_stream_kernel(ExpertArgs a) {
       const size_t pa = (size_t)(n >> 5) * 64 + (n & 31);  // packed row of W1 n
       const float *const rows[R] = {wb + pa * H, wb + (pa + 1) * H,
                                     wb + (pa + 32) * H, wb + (pa + 33) * H};
-      float4 wv[R][KCH1];
+      f32x4 wv[R][KCH1];
       load_rows<KCH1>(rows, wv);
       block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
       for (int m0 = 0; m0 < cnt; m0 += MT) {
@@ -895,7 +921,7 @@ void expert_stream_kernel(ExpertArgs a) {
       const int h = ch * kStreamRows + wave * R;
       const float *wb = a.w.w2 + ((size_t)e * H + h) * I;
       const float *const rows[R] = {wb, wb + I, wb + 2 * (size_t)I, wb + 3 * (size_t)I};
-      float4 wv[R][KCH2];
+      f32x4 wv[R][KCH2];
       load_rows<KCH2>(rows, wv);
       block_wait(&a.s.dep[u], p1u, a.wait_limit, &c->err);
       for (int m0 = 0; m0 < cnt; m0 += MT) {

@@ -62,6 +62,12 @@ def synchronize() -> None:
     _ck(rt().hipDeviceSynchronize(), "hipDeviceSynchronize")
 
 
+def copy_device(dst: "DeviceArray", src: "DeviceArray") -> None:
+    assert dst.nbytes == src.nbytes
+    _ck(rt().hipMemcpy(dst.handle, src.handle, dst.nbytes, hipMemcpyDeviceToDevice),
+        "hipMemcpy D2D")
+
+
 class Stream:
     def __init__(self):
         self.handle = _vp()
