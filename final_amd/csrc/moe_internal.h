@@ -15,7 +15,7 @@ constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
 constexpr int kCombineTokens = 8;  // tokens per combine task
 constexpr int kStreamRowsPerWave = 4;   // weight rows per wave, streaming kernel
 constexpr int kStreamRows = kStreamRowsPerWave * 4;  // rows per streaming task
-constexpr int kStreamTokens = 4;  // token rows per streaming pass (LDS staged)
+constexpr int kStreamTokens = 8;  // token rows per streaming pass (LDS staged)
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset

@@ -302,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
       const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;  // layer.cu:484
 #pragma unroll
       for (int i = 0; i < kTopK; ++i) {
-        a.s.idx[(size_t)tok * kTopK + i] = mi[i];
+        st_agent(&a.s.idx[(size_t)tok * kTopK + i], mi[i]);  // read by the planning block
         a.s.wts[(size_t)tok * kTopK + i] = mp[i] * scale * 1.0f;  // :489
       }
     }
@@ -324,7 +324,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
     }
     if (valid) {
 #pragma unroll
-      for (int i = 0; i < kTopK; ++i) a.s.pos[(size_t)tok * kTopK + i] = rank[i];
+      for (int i = 0; i < kTopK; ++i) st_agent(&a.s.pos[(size_t)tok * kTopK + i], rank[i]);
     }
   }
   __syncthreads();
@@ -398,12 +398,15 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
     const int p2u = tr > 0 ? a.H / a.bn : a.H / kStreamRows;
     ctrl->p1_per_unit = p1u;
     ctrl->p2_per_unit = p2u;
-    ctrl->n_rblocks = nb;
+    // The streaming plan (small T) gets its slots from this block below, so
+    // its expert kernel has no dispatch tasks to wait for.
+    const int ndisp = tr > 0 ? nb : 0;
+    ctrl->n_rblocks = ndisp;
     ctrl->rtokens = RT;
     ctrl->n_p1 = units * p1u;
     ctrl->n_p2 = units * p2u;
     ctrl->n_comb = (T + kCombineTokens - 1) / kCombineTokens;
-    ctrl->n_total = nb + units * p1u + units * p2u + ctrl->n_comb;
+    ctrl->n_total = ndisp + units * p1u + units * p2u + ctrl->n_comb;
     ctrl->num_tokens = T;
     ctrl->tile_rows = tr;
     ctrl->head = 0;
@@ -414,6 +417,21 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
   __syncthreads();
   const int units = min(s_units, a.max_units);
   for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
+  if (a.tile_rows == 0) {
+    // slot = token block base + in-block rank (stable by token), as the
+    // dispatch tasks of the tiled plans compute it
+    for (int f = tid; f < T * kTopK; f += kThreads) {
+      const int t = f / kTopK;
+      const int ee = a.s.idx[f];
+      int slot = -1;
+      if (ee >= 0 && ee < kExperts) {
+        slot = a.s.blk[(t / RT) * kExperts + ee] + a.s.pos[f];
+        if (slot >= 0 && slot < T * kTopK) a.s.slot_token[slot] = t;
+        else slot = -1;
+      }
+      a.s.pos[f] = slot;
+    }
+  }
   if (tid == 0) ctrl->router_done = 0;  // every token block has counted in
 }
 
@@ -796,30 +814,38 @@ __device__ __forceinline__ void wave_transpose_sum(float (&v)[V]) {
 constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
 
 // Stage MT rows (length KCH*256, row m at base + off[m], off < 0 = zeros).
+// Loads are issued in batches of at most 4 float4 per thread so staging does
+// not compete for registers with the weight rows held across tasks.
 template <int MT, int KCH>
 __device__ __forceinline__ void stage_tokens(float *xs, const float *base, const int *off) {
   constexpr int K4 = KCH * 64;
   constexpr int N = MT * K4;
   constexpr int PER = (N + kThreads - 1) / kThreads;
+  constexpr int BATCH = PER < 4 ? PER : 4;
   const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-  f32x4 v[PER];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int f = threadIdx.x + i * kThreads;
-    const int m = f / K4, c4 = f % K4;
-    const int o = (N % kThreads == 0 || f < N) ? off[m] : -1;
-    v[i] = o >= 0 ? ld4(base + o + c4 * 4) : zero;
-  }
+  for (int i0 = 0; i0 < PER; i0 += BATCH) {
+    f32x4 v[BATCH];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int f = threadIdx.x + i * kThreads;
-    if (N % kThreads == 0 || f < N) st4(xs + f * 4, v[i]);
+    for (int b = 0; b < BATCH; ++b) {
+      const int f = threadIdx.x + (i0 + b) * kThreads;
+      const int m = f / K4, c4 = f % K4;
+      const int o = (i0 + b < PER && (N % kThreads == 0 || f < N)) ? off[m] : -1;
+      v[b] = o >= 0 ? ld4(base + o + c4 * 4) : zero;
+    }
+#pragma unroll
+    for (int b = 0; b < BATCH; ++b) {
+      const int f = threadIdx.x + (i0 + b) * kThreads;
+      if (i0 + b < PER && (N % kThreads == 0 || f < N)) st4(xs + f * 4, v[b]);
+    }
   }
 }
 
-// acc[r][m] = wv[r] . xs[m] (lane-partial: this lane's float4 of each chunk).
+constexpr int kStreamMaxChunks = 8;  // weight row length <= 2048 floats
+
+// acc[r][m] = wv[r] . xs[m] over KCH chunks (this lane's float4 of each).
 template <int MT, int KCH>
-__device__ __forceinline__ void stream_dots(const f32x4 (&wv)[kStreamRowsPerWave][KCH],
+__device__ __forceinline__ void stream_dots(const f32x4 (&wv)[kStreamRowsPerWave][kStreamMaxChunks],
                                             const float *xs,
                                             float (&acc)[kStreamRowsPerWave][MT]) {
   constexpr int K = KCH * 256;
@@ -841,120 +867,189 @@ __device__ __forceinline__ void stream_dots(const f32x4 (&wv)[kStreamRowsPerWave
   }
 }
 
-template <int KCH>
-__device__ __forceinline__ void load_rows(const float *const (&rows)[kStreamRowsPerWave],
-                                          f32x4 (&wv)[kStreamRowsPerWave][KCH]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int c = 0; c < KCH; ++c)
-#pragma unroll
-    for (int r = 0; r < kStreamRowsPerWave; ++r) wv[r][c] = ld4(rows[r] + c * 256 + lane * 4);
+// A streaming-kernel task decoded: kind 0 dispatch, 1 gate/up rows, 2 down
+// rows, 3 combine, 4 none (past the end).  rows[] are this wave's 4 rows.
+struct StreamTask {
+  int kind, q, u, e, cnt, slot0, col;
+};
+
+__device__ __forceinline__ StreamTask stream_decode(const Ctrl *c, int task, int nb, int n1,
+                                                   int n2, int ntot, int p1u, int p2u,
+                                                   int wave) {
+  StreamTask t{4, 0, 0, 0, 0, 0, 0};
+  if (task >= ntot) return t;
+  if (task < nb) {
+    t.kind = 0;
+    t.q = task;
+  } else if (task < nb + n1) {
+    t.kind = 1;
+    t.q = task - nb;
+    t.u = t.q / p1u;
+    t.col = (t.q % p1u) * (kStreamRows / 2) + wave * 2;  // this wave's first n
+  } else if (task < nb + n1 + n2) {
+    t.kind = 2;
+    t.q = task - nb - n1;
+    t.u = t.q / p2u;
+    t.col = (t.q % p2u) * kStreamRows + wave * kStreamRowsPerWave;  // first h
+  } else {
+    t.kind = 3;
+    t.q = task - nb - n1 - n2;
+  }
+  if (t.kind == 1 || t.kind == 2) {
+    t.e = c->active[t.u];
+    t.cnt = c->counts[t.e];
+    t.slot0 = c->offsets[t.e];
+  }
+  return t;
 }
 
-// KCH1 = H / 256 (gate/up rows), KCH2 = I / 256 (down rows).
+// Issues the weight loads of a streaming task into wv (all chunks in flight),
+// unconditionally: tasks without weight rows (dispatch, combine, none) load
+// the first rows of W1/W3 as a harmless stand-in, so wv has one definition per
+// pass and stays in registers.  Gate/up: W1 rows n, n+1 and W3 rows n, n+1 of
+// the packed layout; down: W2 rows h .. h+3 (a row's last chunk is re-read
+// where I has fewer chunks than kStreamMaxChunks).
 template <int KCH1, int KCH2>
+__device__ __forceinline__ void stream_issue(const ExpertArgs &a, const StreamTask &t,
+                                             f32x4 (&wv)[kStreamRowsPerWave][kStreamMaxChunks]) {
+  const int lane = threadIdx.x & 63;
+  const int H = a.H, I = a.I;
+  const bool down = t.kind == 2;
+  const size_t pa = (size_t)(t.col >> 5) * 64 + (t.col & 31);  // packed row of W1 n
+  const float *w13 = a.w.w13 + (size_t)t.e * 2 * I * H;
+  const float *w2 = a.w.w2 + ((size_t)t.e * H + t.col) * I;
+  const bool rows13 = t.kind == 1;
+  const float *r0 = down ? w2 : (rows13 ? w13 + pa * H : a.w.w13);
+  const size_t step1 = down ? I : (rows13 ? H : H);        // row 1 - row 0
+  const size_t step2 = down ? 2 * (size_t)I : (rows13 ? 32 * (size_t)H : 2 * (size_t)H);
+  const size_t step3 = down ? 3 * (size_t)I : (rows13 ? 33 * (size_t)H : 3 * (size_t)H);
+  const int nch = down ? KCH2 : KCH1;
+  const float *rows[kStreamRowsPerWave] = {r0, r0 + step1, r0 + step2, r0 + step3};
+#pragma unroll
+  for (int c = 0; c < kStreamMaxChunks; ++c) {
+    const int cc = c < nch ? c : nch - 1;
+#pragma unroll
+    for (int r = 0; r < kStreamRowsPerWave; ++r) wv[r][c] = ld4(rows[r] + cc * 256 + lane * 4);
+  }
+}
+
+// Output half of a pass: reduce the lane partials of the wave's 4 rows x MT
+// tokens, gather the block's outputs in LDS, and write them as 16-byte stores
+// (8 floats per token for gate/up, 16 for down, contiguous in the row).
+template <int MT, bool GATED>
+__device__ __forceinline__ void stream_out(const ExpertArgs &a, const StreamTask &t, int m0,
+                                           int nt, float (&acc)[kStreamRowsPerWave][MT],
+                                           float (*s_res)[kStreamRows], const AgentOut &out) {
+  constexpr int R = kStreamRowsPerWave;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (GATED) {
+    // value (j*MT + m)*2 + w: j = which n, w = 0 W1 / 1 W3 (row w*2 + j)
+    float v[4 * MT];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int m = 0; m < MT; ++m)
+#pragma unroll
+        for (int w = 0; w < 2; ++w) v[(j * MT + m) * 2 + w] = acc[w * 2 + j][m];
+    wave_transpose_sum<4 * MT, 2>(v);
+    constexpr int SH = 6 - log2i(2 * MT);
+    const int p = lane >> SH;  // pair index j*MT + m
+    if ((lane & ((1 << SH) - 1)) == 0) s_res[p % MT][wave * 2 + p / MT] = silu(v[0]) * v[1];
+  } else {
+    float v[R * MT];  // value r*MT + m
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int m = 0; m < MT; ++m) v[r * MT + m] = acc[r][m];
+    wave_transpose_sum<R * MT, 1>(v);
+    constexpr int SH = 6 - log2i(R * MT);
+    const int i = lane >> SH;
+    if ((lane & ((1 << SH) - 1)) == 0) s_res[i % MT][wave * R + i / MT] = v[0];
+  }
+  __syncthreads();
+  constexpr int F4 = GATED ? 2 : 4;
+  if (tid < nt * F4) {
+    const int mm = tid / F4, q4 = tid % F4;
+    const int col0 = t.col - wave * (GATED ? 2 : R);
+    const int ld = GATED ? a.I : a.H;
+    out.store((uint32_t)(((size_t)(t.slot0 + m0 + mm) * ld + col0 + q4 * 4) * sizeof(float)),
+              ld4(&s_res[mm][q4 * 4]));
+  }
+  __syncthreads();
+}
+
+// KCH1 = H / 256 (gate/up rows), KCH2 = I / 256 (down rows), MT = token rows
+// per pass (LDS-staged; 2 for the smallest batches, else 8).  Every pass
+// issues the weight rows of what comes next (the next task after a task's last
+// pass, the same rows again otherwise) right after its dot products, so HBM
+// streams while the pass reduces, stores and signals, and a down task's
+// weights are already in flight while it waits for its expert's gate/up tasks.
+template <int KCH1, int KCH2, int MT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void expert_stream_kernel(ExpertArgs a) {
-  constexpr int MT = kStreamTokens, R = kStreamRowsPerWave;
+  static_assert(KCH1 <= kStreamMaxChunks && KCH2 <= kStreamMaxChunks, "row length");
+  constexpr int R = kStreamRowsPerWave;
   extern __shared__ float xs[];  // [MT][max(H, I)]
-  __shared__ int s_task;
+  __shared__ int s_task, s_next;
   __shared__ int s_off[MT];
+  __shared__ float s_res[MT][kStreamRows];
   Ctrl *c = a.s.ctrl;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, wave = tid >> 6;
   const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
   const int p1u = c->p1_per_unit, p2u = c->p2_per_unit, rt = c->rtokens;
-  const int H = a.H, I = a.I;
-  if (tid == 0) s_task = claim(&c->head);
+  const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
+  if (tid == 0) {
+    s_task = claim(&c->head);
+    s_next = claim(&c->head);
+  }
   __syncthreads();
   int task = s_task;
+  StreamTask cur = stream_decode(c, task, nb, n1, n2, ntot, p1u, p2u, wave);
+  f32x4 wv[R][kStreamMaxChunks];
+  stream_issue<KCH1, KCH2>(a, cur, wv);
   while (task < ntot) {
-    int next = 0;
-    if (tid == 0) next = claim(&c->head);  // claim ahead
-    if (task < nb) {
-      assign_task(a, task, rt);
+    const int next = s_next;
+    const StreamTask nxt = stream_decode(c, next, nb, n1, n2, ntot, p1u, p2u, wave);
+    const bool rows = cur.kind == 1 || cur.kind == 2;
+    if (cur.kind == 1 && nb > 0) block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
+    if (cur.kind == 2) block_wait(&a.s.dep[cur.u], p1u, a.wait_limit, &c->err);
+    const int npass = rows ? (cur.cnt + MT - 1) / MT : 1;
+    for (int ps = 0; ps < npass; ++ps) {
+      const int m0 = ps * MT;
+      const int nt = rows ? min(MT, cur.cnt - m0) : 0;
+      float acc[R][MT];
+      if (rows) {
+        if (tid < MT)
+          s_off[tid] = tid < nt ? (cur.kind == 1 ? slot_tok(a, cur.slot0 + m0 + tid) * a.H
+                                                 : (cur.slot0 + m0 + tid) * a.I)
+                                : -1;
+        __syncthreads();
+        if (cur.kind == 1) stage_tokens<MT, KCH1>(xs, a.x, s_off);
+        else stage_tokens<MT, KCH2>(xs, a.s.inter, s_off);
+        __syncthreads();
+        if (cur.kind == 1) stream_dots<MT, KCH1>(wv, xs, acc);
+        else stream_dots<MT, KCH2>(wv, xs, acc);
+      }
+      stream_issue<KCH1, KCH2>(a, ps + 1 < npass ? cur : nxt, wv);  // wv is dead: refill
+      if (cur.kind == 1) stream_out<MT, true>(a, cur, m0, nt, acc, s_res, inter_out);
+      else if (cur.kind == 2) stream_out<MT, false>(a, cur, m0, nt, acc, s_res, sout_out);
+    }
+    if (cur.kind == 0) {
+      assign_task(a, cur.q, rt);
       block_signal(&c->assign_done);
-    } else if (task < nb + n1) {
-      // gate/up: 8 consecutive n of one expert; wave w owns n0+2w, n0+2w+1
-      const int q = task - nb;
-      const int u = q / p1u, ch = q % p1u;
-      const int e = c->active[u];
-      const int cnt = c->counts[e], slot0 = c->offsets[e];
-      const int n = ch * (kStreamRows / 2) + wave * 2;
-      const float *wb = a.w.w13 + (size_t)e * 2 * I * H;
-      const size_t pa = (size_t)(n >> 5) * 64 + (n & 31);  // packed row of W1 n
-      const float *const rows[R] = {wb + pa * H, wb + (pa + 1) * H,
-                                    wb + (pa + 32) * H, wb + (pa + 33) * H};
-      f32x4 wv[R][KCH1];
-      load_rows<KCH1>(rows, wv);
-      block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
-      for (int m0 = 0; m0 < cnt; m0 += MT) {
-        const int nt = min(MT, cnt - m0);
-        if (tid < MT) s_off[tid] = tid < nt ? slot_tok(a, slot0 + m0 + tid) * H : -1;
-        __syncthreads();
-        stage_tokens<MT, KCH1>(xs, a.x, s_off);
-        __syncthreads();
-        float acc[R][MT];
-        stream_dots<MT, KCH1>(wv, xs, acc);
-        // value (j*MT + m)*2 + w: j = which n, w = 0 W1 / 1 W3 (row w*2 + j)
-        float v[2 * MT * 2];
-#pragma unroll
-        for (int j = 0; j < 2; ++j)
-#pragma unroll
-          for (int m = 0; m < MT; ++m)
-#pragma unroll
-            for (int w = 0; w < 2; ++w) v[(j * MT + m) * 2 + w] = acc[w * 2 + j][m];
-        wave_transpose_sum<4 * MT, 2>(v);
-        constexpr int SH = 6 - log2i(2 * MT);
-        const int p = lane >> SH;  // pair index j*MT + m
-        const int j = p / MT, m = p % MT;
-        if ((lane & ((1 << SH) - 1)) == 0 && m < nt)
-          st_agent(&a.s.inter[(size_t)(slot0 + m0 + m) * I + n + j], silu(v[0]) * v[1]);
-        __syncthreads();
-      }
-      block_signal(&a.s.dep[u]);
-    } else if (task < nb + n1 + n2) {
-      // down: 16 consecutive rows h of W2[e]; wave w owns h0+4w .. h0+4w+3
-      const int q = task - nb - n1;
-      const int u = q / p2u, ch = q % p2u;
-      const int e = c->active[u];
-      const int cnt = c->counts[e], slot0 = c->offsets[e];
-      const int h = ch * kStreamRows + wave * R;
-      const float *wb = a.w.w2 + ((size_t)e * H + h) * I;
-      const float *const rows[R] = {wb, wb + I, wb + 2 * (size_t)I, wb + 3 * (size_t)I};
-      f32x4 wv[R][KCH2];
-      load_rows<KCH2>(rows, wv);
-      block_wait(&a.s.dep[u], p1u, a.wait_limit, &c->err);
-      for (int m0 = 0; m0 < cnt; m0 += MT) {
-        const int nt = min(MT, cnt - m0);
-        if (tid < MT) s_off[tid] = tid < nt ? (slot0 + m0 + tid) * I : -1;
-        __syncthreads();
-        stage_tokens<MT, KCH2>(xs, a.s.inter, s_off);
-        __syncthreads();
-        float acc[R][MT];
-        stream_dots<MT, KCH2>(wv, xs, acc);
-        float v[R * MT];  // value r*MT + m
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-#pragma unroll
-          for (int m = 0; m < MT; ++m) v[r * MT + m] = acc[r][m];
-        wave_transpose_sum<R * MT, 1>(v);
-        constexpr int SH = 6 - log2i(R * MT);
-        const int i = lane >> SH;
-        const int r = i / MT, m = i % MT;
-        if ((lane & ((1 << SH) - 1)) == 0 && m < nt)
-          st_agent(&a.s.sout[(size_t)(slot0 + m0 + m) * H + h + r], v[0]);
-        __syncthreads();
-      }
+    } else if (cur.kind == 1) {
+      block_signal(&a.s.dep[cur.u]);
+    } else if (cur.kind == 2) {
       block_signal(&c->p2_done);
     } else {
-      const int q = task - nb - n1 - n2;
       block_wait(&c->p2_done, n2, a.wait_limit, &c->err);
-      combine_task(a, q);
+      combine_task(a, cur.q);
     }
+    __syncthreads();  // every thread has read s_next
+    if (tid == 0) s_next = claim(&c->head);
+    task = next;
+    cur = nxt;
     __syncthreads();
-    if (tid == 0) s_task = next;
-    __syncthreads();
-    task = s_task;
   }
 }
 
@@ -1014,15 +1109,20 @@ static size_t stream_lds_bytes(int H, int I) {
   return (size_t)kStreamTokens * (size_t)(H > I ? H : I) * sizeof(float);
 }
 
-static const void *stream_fn(int H, int I) {
-#define MOE_STREAM_CASE(K1, K2) \
-  if (H == (K1)*256 && I == (K2)*256) return reinterpret_cast<const void *>(&expert_stream_kernel<K1, K2>);
+// Token rows per streaming pass for a batch of T tokens.
+static int stream_mt(int T) { return T <= 2 ? 2 : kStreamTokens; }
+
+static const void *stream_fn(int H, int I, int mt) {
+#define MOE_STREAM_CASE(K1, K2)                                                              \
+  if (H == (K1)*256 && I == (K2)*256)                                                         \
+    return mt == 2 ? reinterpret_cast<const void *>(&expert_stream_kernel<K1, K2, 2>)         \
+                   : reinterpret_cast<const void *>(&expert_stream_kernel<K1, K2, kStreamTokens>);
   MOE_STREAM_SHAPES(MOE_STREAM_CASE)
 #undef MOE_STREAM_CASE
   return nullptr;
 }
 
-bool stream_supported(int H, int I) { return stream_fn(H, I) != nullptr; }
+bool stream_supported(int H, int I) { return stream_fn(H, I, kStreamTokens) != nullptr; }
 
 template <int BM> static void *mfma_fn() {
   return reinterpret_cast<void *>(&expert_mfma_kernel<BM>);
@@ -1040,7 +1140,7 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
   switch (tile_rows) {
     case 0: {
       const size_t lds = stream_lds_bytes(a.H, a.I);
-      const void *fn = stream_fn(a.H, a.I);
+      const void *fn = stream_fn(a.H, a.I, stream_mt(a.T));
       if (!fn) return hipErrorInvalidValue;
       err = ensure_lds_attr(fn, lds);
       if (err != hipSuccess) return err;
@@ -1090,7 +1190,7 @@ int expert_blocks_per_cu(int tile_rows) {
   hipError_t e = hipSuccess;
   switch (tile_rows) {
     case 0: {
-      const void *fn = stream_fn(2048, 1792);
+      const void *fn = stream_fn(2048, 1792, kStreamTokens);
       if (!fn) return 1;
       e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads,
                                                        stream_lds_bytes(2048, 1792));
