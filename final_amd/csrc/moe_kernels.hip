@@ -1057,6 +1057,512 @@ void expert_stream_kernel(ExpertArgs a) {
 #define MOE_STREAM_SHAPES(X) X(8, 7)
 
 // ---------------------------------------------------------------------------
+// Decoupled weight-streaming kernel (small T).
+//
+// A wave's vector-memory loads complete in issue order, so a wave that keeps
+// weight rows in flight cannot wait for any other load (a dependency counter,
+// a token row, a result store) without also waiting for those rows.  Each
+// block therefore splits the work by wave: eight streaming waves only load
+// weight rows into registers, one task ahead, and dot them with token rows
+// held in LDS; one control wave copies token rows into LDS with
+// direct-to-LDS loads, polls dependencies, reduces and stores results and
+// signals, issuing everything one step needs before a single wait.  The waves
+// hand over through LDS flags; there is no block barrier after start-up.
+//
+// Tasks are dealt round-robin (block b takes b, b + G, b + 2G, ... of the
+// task list, G = grid size), so both roles derive the block's sequence from
+// the plan without claiming.  Task = 16 weight rows of one active expert
+// (gate/up: W1 and W3 rows of 8 intermediate columns; down: W2 rows of 16
+// output columns) over all of the expert's tokens, in items of up to 8
+// tokens.  Streaming wave w holds rows 4*(w%4) .. +3 over the k half w/4.
+// Every task waits only on tasks of smaller index and each block runs its
+// tasks in increasing order, so the smallest unfinished task always runs.
+// ---------------------------------------------------------------------------
+
+constexpr int kPipeWaves = 8;                        // streaming waves
+constexpr int kPipeThreads = (kPipeWaves + 1) * 64;  // + the control wave
+constexpr int kPipeGroups = 4;                       // row groups of 4 rows
+constexpr int kPipeSplit = kPipeWaves / kPipeGroups; // k halves
+constexpr int kPipeChunks = 4;                       // 256-float chunks per wave
+constexpr int kPipeTokens = 8;                       // token rows per item
+constexpr int kPipeMaxBufs = 4;                      // token buffers (items in flight)
+static_assert(kPipeGroups * kStreamRowsPerWave == kStreamRows, "16 rows per task");
+static_assert(kPipeSplit * kPipeChunks * 256 >= 2048, "k halves cover rows of <= 2048");
+
+// kind: 1 gate/up rows, 2 down rows, 3 combine, 4 past the end.
+struct PipeTask {
+  int kind, q, u, e, cnt, slot0, col, npass;
+};
+
+struct PipeShared {
+  int active[kExperts], counts[kExperts], offsets[kExperts];
+  int xseq[kPipeMaxBufs];  // xseq[b] == i once item i's token rows are in buffer b
+  int done[kPipeMaxBufs];  // streaming waves finished with buffer b's item
+  int abort;
+  float res[kPipeMaxBufs][kPipeSplit][kPipeTokens][kStreamRows];
+};
+
+// Token buffers: an item holds at most min(T, 8) token rows, and the LDS
+// space of two 8-row buffers is split into as many buffers (2 to 4) as fit.
+__host__ __device__ constexpr int pipe_buf_tokens(int T) {
+  return T < 1 ? 1 : (T < kPipeTokens ? T : kPipeTokens);
+}
+__host__ __device__ constexpr int pipe_bufs(int T) {
+  return 2 * kPipeTokens / pipe_buf_tokens(T) < kPipeMaxBufs ? 2 * kPipeTokens / pipe_buf_tokens(T)
+                                                               : kPipeMaxBufs;
+}
+
+__device__ __forceinline__ int lds_load(const int *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void lds_store(int *p, int v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+// Orderings of LDS accesses between waves of the block; they wait only for
+// LDS operations (lgkmcnt), never for the wave's outstanding global loads.
+__device__ __forceinline__ void release_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+}
+__device__ __forceinline__ void acquire_lds() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// The plan values both roles need, wave-uniform.
+struct PipePlan {
+  int n1, n2, ntot, p1u, p2u, grid;
+};
+
+__device__ __forceinline__ PipeTask pipe_task(const PipeShared &sh, const PipePlan &pl, int j) {
+  const int task = (int)blockIdx.x + j * pl.grid;
+  PipeTask t{4, 0, 0, 0, 0, 0, 0, 1};
+  if (task >= pl.ntot) return t;
+  if (task < pl.n1) {
+    t.kind = 1;
+    t.q = task;
+    t.u = task / pl.p1u;
+    t.col = (task % pl.p1u) * (kStreamRows / 2);
+  } else if (task < pl.n1 + pl.n2) {
+    t.kind = 2;
+    t.q = task - pl.n1;
+    t.u = t.q / pl.p2u;
+    t.col = (t.q % pl.p2u) * kStreamRows;
+  } else {
+    t.kind = 3;
+    t.q = task - pl.n1 - pl.n2;
+  }
+  if (t.kind != 3) {
+    t.e = __builtin_amdgcn_readfirstlane(sh.active[t.u]);
+    t.cnt = __builtin_amdgcn_readfirstlane(sh.counts[t.e]);
+    t.slot0 = __builtin_amdgcn_readfirstlane(sh.offsets[t.e]);
+    t.npass = t.cnt > 0 ? (t.cnt + kPipeTokens - 1) / kPipeTokens : 1;
+  }
+  return t;
+}
+
+// Streaming side: wait until *p == want; false if the block aborts or the
+// control wave stops answering.
+__device__ __forceinline__ bool pipe_wait(const int *p, int want, const int *abort_flag,
+                                          int limit) {
+  int spins = 0;
+  while (__builtin_amdgcn_readfirstlane(lds_load(p)) != want) {
+    if (lds_load(abort_flag) || ++spins > limit) return false;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  acquire_lds();
+  return true;
+}
+
+// Raw buffer descriptors of the weight arrays: the streaming waves address a
+// row by a scalar byte offset and a lane by one shared vector offset, and a
+// descriptor with no records yields zeros without touching memory.
+struct PipeWeights {
+  __amdgpu_buffer_rsrc_t w13, w2, none;
+};
+
+__device__ __forceinline__ PipeWeights pipe_weights(const ExpertArgs &a) {
+  const size_t b13 = (size_t)kExperts * 2 * a.I * a.H * sizeof(float);
+  const size_t b2 = (size_t)kExperts * a.H * a.I * sizeof(float);
+  PipeWeights w;
+  w.w13 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.w.w13), 0, (int)b13, kBufferRsrcWord3);
+  w.w2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.w.w2), 0, (int)b2, kBufferRsrcWord3);
+  w.none = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.w.w2), 0, 0, kBufferRsrcWord3);
+  return w;
+}
+
+// Issue one task's weight loads for this wave (rows of group rg over k half
+// h).  Chunks past the end of a row and tasks without weight rows read
+// through the empty descriptor, so every register has one unconditional load.
+template <int KCH1, int KCH2>
+__device__ __forceinline__ void pipe_issue(const ExpertArgs &a, const PipeWeights &pw,
+                                           const PipeTask &t, int rg, int h,
+                                           f32x4 (&buf)[kStreamRowsPerWave][kPipeChunks]) {
+  const int lane = threadIdx.x & 63;
+  const int H = a.H, I = a.I;
+  __amdgpu_buffer_rsrc_t rs = pw.none;
+  uint32_t r0 = 0, s1 = 0, s2 = 0, s3 = 0;  // row byte offsets (row 0, then steps)
+  int nch = 0;
+  if (t.kind == 1) {
+    const int n = t.col + rg * 2;  // W1/W3 rows n, n+1 of the packed [I/32][2][32][H]
+    const uint32_t pa = (uint32_t)(n >> 5) * 64 + (n & 31);
+    r0 = ((uint32_t)t.e * 2 * I + pa) * (uint32_t)H * 4u;
+    s1 = H * 4u;
+    s2 = 32u * H * 4u;
+    s3 = 33u * H * 4u;
+    rs = pw.w13;
+    nch = KCH1 - h * kPipeChunks;
+  } else if (t.kind == 2) {
+    r0 = ((uint32_t)t.e * H + t.col + rg * kStreamRowsPerWave) * (uint32_t)I * 4u;
+    s1 = I * 4u;
+    s2 = 2u * I * 4u;
+    s3 = 3u * I * 4u;
+    rs = pw.w2;
+    nch = KCH2 - h * kPipeChunks;
+  }
+  const uint32_t soff[kStreamRowsPerWave] = {r0, r0 + s1, r0 + s2, r0 + s3};
+  const int voff = (h * kPipeChunks * 256 + lane * 4) * (int)sizeof(float);
+#pragma unroll
+  for (int c = 0; c < kPipeChunks; ++c) {
+    const __amdgpu_buffer_rsrc_t rc = c < nch ? rs : pw.none;
+#pragma unroll
+    for (int r = 0; r < kStreamRowsPerWave; ++r)
+      buf[r][c] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, voff + c * 1024, (int)soff[r], 0));
+  }
+}
+
+// acc[r][m] = this lane's part of row r . token row m (MS token rows at xb,
+// row stride KMAX), over the wave's nch chunks.
+template <int MS, int KMAX>
+__device__ __forceinline__ void pipe_dots(const f32x4 (&buf)[kStreamRowsPerWave][kPipeChunks],
+                                          const float *xb, int nch,
+                                          float (&acc)[kStreamRowsPerWave][MS]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int r = 0; r < kStreamRowsPerWave; ++r)
+#pragma unroll
+    for (int m = 0; m < MS; ++m) acc[r][m] = 0.0f;
+#pragma unroll
+  for (int c = 0; c < kPipeChunks; ++c) {
+    if (c < nch) {
+#pragma unroll
+      for (int m = 0; m < MS; ++m) {
+        const f32x4 xv = ld4(xb + m * KMAX + c * 256 + lane * 4);
+#pragma unroll
+        for (int r = 0; r < kStreamRowsPerWave; ++r)
+#pragma unroll
+          for (int q = 0; q < 4; ++q) acc[r][m] = __builtin_fmaf(buf[r][c][q], xv[q], acc[r][m]);
+      }
+    }
+  }
+}
+
+// Weighted top-4 sum of one token plus the residual, by one wave (the same
+// arithmetic as combine_task).
+__device__ void combine_token_wave(const ExpertArgs &a, int tok) {
+#pragma clang fp contract(off)
+  if (tok >= a.T) return;
+  const int lane = threadIdx.x & 63;
+  const int H4 = a.H >> 2;
+  const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
+  const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
+  float4 *y4 = reinterpret_cast<float4 *>(a.y);
+  int slot[kTopK];
+  float wk[kTopK];
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    slot[k] = a.s.pos[(size_t)tok * kTopK + k];
+    wk[k] = a.s.wts[(size_t)tok * kTopK + k];
+  }
+  for (int c4 = lane; c4 < H4; c4 += 64) {
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+      if (slot[k] >= 0 && slot[k] < a.T * kTopK) {
+        const float4 v = so[(size_t)slot[k] * H4 + c4];
+        acc.x = __builtin_fmaf(v.x, wk[k], acc.x);
+        acc.y = __builtin_fmaf(v.y, wk[k], acc.y);
+        acc.z = __builtin_fmaf(v.z, wk[k], acc.z);
+        acc.w = __builtin_fmaf(v.w, wk[k], acc.w);
+      }
+    }
+    if (r4) {
+      const float4 r = r4[(size_t)tok * H4 + c4];
+      acc.x = r.x + acc.x;
+      acc.y = r.y + acc.y;
+      acc.z = r.z + acc.z;
+      acc.w = r.w + acc.w;
+    }
+    y4[(size_t)tok * H4 + c4] = acc;
+  }
+}
+
+// One task on the streaming side: every item (pass of up to 8 tokens) waits
+// for its token rows, dots them in sub-passes of MS tokens, reduces over the
+// wave's lanes and leaves the sums in res[b][h][token][row].
+template <int KCH1, int KCH2, int MS>
+__device__ __forceinline__ bool pipe_process(const ExpertArgs &a, PipeShared &sh, const float *xs,
+                                             int nbuf, int bstride, const PipeTask &t,
+                                             const f32x4 (&buf)[kStreamRowsPerWave][kPipeChunks],
+                                             int &it, int &b, int rg, int h, int w, int limit) {
+  constexpr int KMAX = (KCH1 > KCH2 ? KCH1 : KCH2) * 256;
+  constexpr int V = kStreamRowsPerWave * MS;
+  constexpr int SH = 6 - log2i(V);
+  const int lane = threadIdx.x & 63;
+  if (t.kind == 3) {
+    if (!pipe_wait(&sh.xseq[b], it, &sh.abort, limit)) return false;
+    combine_token_wave(a, t.q * kCombineTokens + w);
+    // nothing of the combine stays in flight: the compiler's wait counts for
+    // the weight buffers then treat them as the only outstanding loads
+    __builtin_amdgcn_s_waitcnt(0);
+    release_lds();
+    if (lane == 0) __hip_atomic_fetch_add(&sh.done[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    ++it;
+    b = b + 1 == nbuf ? 0 : b + 1;
+    return true;
+  }
+  const int nch = (t.kind == 1 ? KCH1 : KCH2) - h * kPipeChunks;
+  for (int p = 0; p < t.npass; ++p, ++it, b = b + 1 == nbuf ? 0 : b + 1) {
+    if (!pipe_wait(&sh.xseq[b], it, &sh.abort, limit)) return false;
+    const int nt = min(kPipeTokens, t.cnt - p * kPipeTokens);
+    const float *xb = xs + (size_t)b * bstride + h * kPipeChunks * 256;
+    for (int s = 0; s < nt; s += MS) {
+      float acc[kStreamRowsPerWave][MS];
+      pipe_dots<MS, KMAX>(buf, xb + s * KMAX, nch, acc);
+      float v[V];  // value r*MS + m
+#pragma unroll
+      for (int r = 0; r < kStreamRowsPerWave; ++r)
+#pragma unroll
+        for (int m = 0; m < MS; ++m) v[r * MS + m] = acc[r][m];
+      wave_transpose_sum<V, 1>(v);
+      const int i = lane >> SH;
+      if ((lane & ((1 << SH) - 1)) == 0)
+        sh.res[b][h][s + i % MS][rg * kStreamRowsPerWave + i / MS] = v[0];
+    }
+    release_lds();
+    if (lane == 0) __hip_atomic_fetch_add(&sh.done[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  }
+  return true;
+}
+
+// Streaming side.  Two register buffers alternate: while one task's rows are
+// dotted, the next task's rows are in flight.  Every path through the loop
+// body issues both buffers in the same order and the loop has one exit, at
+// the end, so the compiler's wait counts see the current buffer as the older
+// of the two and never wait for the one in flight.
+template <int KCH1, int KCH2, int MS>
+__device__ void pipe_streamer(const ExpertArgs &a, PipeShared &sh, const PipePlan &pl,
+                              const float *xs, int nbuf, int bstride, int limit) {
+  // wave-uniform in scalar registers (descriptors and row offsets stay scalar)
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int rg = w % kPipeGroups, h = w / kPipeGroups;
+  const PipeWeights pw = pipe_weights(a);
+  f32x4 bufA[kStreamRowsPerWave][kPipeChunks], bufB[kStreamRowsPerWave][kPipeChunks];
+  int it = 0, ib = 0;  // item counter and its token buffer
+  bool ok = true;
+  PipeTask tA = pipe_task(sh, pl, 0);
+  pipe_issue<KCH1, KCH2>(a, pw, tA, rg, h, bufA);
+  PipeTask tB = pipe_task(sh, pl, 1);
+  pipe_issue<KCH1, KCH2>(a, pw, tB, rg, h, bufB);
+  for (int j = 0;; j += 2) {
+    if (tA.kind != 4)
+      ok = ok && pipe_process<KCH1, KCH2, MS>(a, sh, xs, nbuf, bstride, tA, bufA, it, ib, rg, h, w, limit);
+    tA = pipe_task(sh, pl, j + 2);
+    pipe_issue<KCH1, KCH2>(a, pw, tA, rg, h, bufA);
+    if (tB.kind != 4)
+      ok = ok && pipe_process<KCH1, KCH2, MS>(a, sh, xs, nbuf, bstride, tB, bufB, it, ib, rg, h, w, limit);
+    tB = pipe_task(sh, pl, j + 3);
+    pipe_issue<KCH1, KCH2>(a, pw, tB, rg, h, bufB);
+    if (!ok || tA.kind == 4) break;
+  }
+}
+
+// Control side: copy an item's token rows (x rows through slot_token for
+// gate/up, intermediate rows for down) into LDS buffer xb, 1 KiB per
+// direct-to-LDS load.  Returns without waiting.
+template <int KMAX>
+__device__ __forceinline__ void pipe_stage(const ExpertArgs &a, const PipeTask &t, int p,
+                                           float *xb) {
+  const int lane = threadIdx.x & 63;
+  const int nt = min(kPipeTokens, t.cnt - p * kPipeTokens);
+  const int slot0 = t.slot0 + p * kPipeTokens;
+  const int last = a.T * kTopK - 1;
+  const bool gate = t.kind == 1;
+  const int K = gate ? a.H : a.I;
+  const float *base = gate ? a.x : a.s.inter;
+  size_t roff = 0;
+  if (lane < nt) {
+    const int s = min(slot0 + lane, last);
+    roff = gate ? (size_t)slot_tok(a, s) * a.H : (size_t)s * a.I;
+  }
+  const int nch = K >> 8;
+  for (int m = 0; m < nt; ++m) {
+    const size_t ro = (size_t)__shfl((long long)roff, m, 64);
+    const float *src = base + ro + lane * 4;
+    for (int c = 0; c < nch; ++c)
+      __builtin_amdgcn_global_load_lds(
+          src + c * 256, (__attribute__((address_space(3))) void *)(xb + m * KMAX + c * 256), 16,
+          0, 0);
+  }
+}
+
+// Control side: sum the k halves and store an item's outputs with 16-byte
+// agent-scope stores (gate/up: silu(W1 x) * (W3 x) for 8 columns; down: 16).
+__device__ __forceinline__ void pipe_flush(const ExpertArgs &a, const PipeTask &t, int p, int b,
+                                           const PipeShared &sh, const AgentOut &inter_out,
+                                           const AgentOut &sout_out) {
+  const int lane = threadIdx.x & 63;
+  const int nt = min(kPipeTokens, t.cnt - p * kPipeTokens);
+  const int slot0 = t.slot0 + p * kPipeTokens;
+  if (t.kind == 1) {
+    if (lane < nt * 2) {
+      const int m = lane >> 1, q = lane & 1;
+      f32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int oc = q * 4 + j, rg = oc >> 1, jj = oc & 1;
+        const int rw = rg * kStreamRowsPerWave + jj;
+        const float g = sh.res[b][0][m][rw] + sh.res[b][1][m][rw];
+        const float u = sh.res[b][0][m][rw + 2] + sh.res[b][1][m][rw + 2];
+        o[j] = silu(g) * u;
+      }
+      inter_out.store((uint32_t)(((size_t)(slot0 + m) * a.I + t.col + q * 4) * sizeof(float)), o);
+    }
+  } else {
+    if (lane < nt * 4) {
+      const int m = lane >> 2, q = lane & 3;
+      f32x4 o;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] = sh.res[b][0][m][q * 4 + j] + sh.res[b][1][m][q * 4 + j];
+      sout_out.store((uint32_t)(((size_t)(slot0 + m) * a.H + t.col + q * 4) * sizeof(float)), o);
+    }
+  }
+}
+
+// Control side.  Each step issues the stores of every finished item, the
+// token copies of every item that has a free buffer and satisfied inputs, and
+// dependency polls, then waits once; the completed tasks' counters are bumped
+// and the staged items published after that wait.
+template <int KCH1, int KCH2>
+__device__ void pipe_control(const ExpertArgs &a, PipeShared &sh, const PipePlan &pl, float *xs,
+                             int nbuf, int bstride) {
+  constexpr int KMAX = (KCH1 > KCH2 ? KCH1 : KCH2) * 256;
+  Ctrl *c = a.s.ctrl;
+  const int lane = threadIdx.x & 63;
+  const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
+  const int limit = a.wait_limit * 4;
+  int j_fl = 0, p_fl = 0, it_fl = 0, b_fl = 0;  // next item to flush (task, pass, item, buffer)
+  int j_st = 0, p_st = 0, it_st = 0, b_st = 0;  // next item to stage
+  uint32_t dep_ok = 0;                // units whose gate/up tasks are all done
+  bool p2_ok = false;                 // every down task done
+  int idle = 0;
+  int sig = 0;  // lane u < 32: finished gate/up tasks of unit u; lane 32: down tasks
+  while (true) {
+    int flushed = 0, staged = 0;
+    // 1. results of finished items
+    while (it_fl < it_st) {
+      const int b = b_fl;
+      if (__builtin_amdgcn_readfirstlane(lds_load(&sh.done[b])) != kPipeWaves) break;
+      acquire_lds();
+      const PipeTask t = pipe_task(sh, pl, j_fl);
+      if (t.kind == 1 || t.kind == 2) pipe_flush(a, t, p_fl, b, sh, inter_out, sout_out);
+      lds_store(&sh.done[b], 0);
+      b_fl = b + 1 == nbuf ? 0 : b + 1;
+      if (++p_fl >= t.npass) {
+        if ((t.kind == 1 && lane == t.u) || (t.kind == 2 && lane == kExperts)) ++sig;
+        p_fl = 0;
+        ++j_fl;
+      }
+      ++it_fl;
+      ++flushed;
+    }
+    // 2. token rows of the next items, while buffers are free
+    while (it_st < it_fl + nbuf) {
+      const PipeTask t = pipe_task(sh, pl, j_st);
+      if (t.kind == 4) break;
+      if (t.kind == 2 && !((dep_ok >> t.u) & 1u)) {
+        if (__builtin_amdgcn_readfirstlane(load_relaxed(&a.s.dep[t.u])) < pl.p1u) break;
+        dep_ok |= 1u << t.u;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      }
+      if (t.kind == 3 && !p2_ok) {
+        if (__builtin_amdgcn_readfirstlane(load_relaxed(&c->p2_done)) < pl.n2) break;
+        p2_ok = true;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      }
+      if (t.kind != 3) pipe_stage<KMAX>(a, t, p_st, xs + (size_t)b_st * bstride);
+      b_st = b_st + 1 == nbuf ? 0 : b_st + 1;
+      ++staged;
+      ++it_st;
+      if (++p_st >= t.npass) {
+        p_st = 0;
+        ++j_st;
+      }
+    }
+    if (staged > 0 || flushed > 0) {
+      __builtin_amdgcn_s_waitcnt(0);  // stores complete, token rows in LDS
+      if (sig) fetch_add(lane < kExperts ? &a.s.dep[lane] : &c->p2_done, sig);
+      sig = 0;
+      release_lds();
+      if (lane == 0) {
+        int bb = b_st;  // walk back over the buffers staged in this step
+        for (int i = it_st - 1; i >= it_st - staged; --i) {
+          bb = bb == 0 ? nbuf - 1 : bb - 1;
+          lds_store(&sh.xseq[bb], i);
+        }
+      }
+      idle = 0;
+    } else {
+      if (it_fl == it_st && pipe_task(sh, pl, j_st).kind == 4) break;  // all flushed
+      if (++idle > limit) {
+        if (lane == 0) {
+          st_agent(&c->err, 1);
+          lds_store(&sh.abort, 1);
+        }
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+  }
+}
+
+template <int KCH1, int KCH2, int MS>
+__global__ __launch_bounds__(kPipeThreads) void expert_pipe_kernel(ExpertArgs a) {
+  static_assert(KCH1 <= kPipeSplit * kPipeChunks && KCH2 <= kPipeSplit * kPipeChunks, "row length");
+  constexpr int KMAX = (KCH1 > KCH2 ? KCH1 : KCH2) * 256;
+  extern __shared__ float xs[];  // [nbuf][min(T, 8)][max(H, I)]
+  __shared__ PipeShared sh;
+  const Ctrl *c = a.s.ctrl;
+  const int tid = threadIdx.x;
+  if (tid < kExperts) {
+    sh.active[tid] = c->active[tid];
+    sh.counts[tid] = c->counts[tid];
+    sh.offsets[tid] = c->offsets[tid];
+  }
+  if (tid < kPipeMaxBufs) {
+    sh.xseq[tid] = -1;
+    sh.done[tid] = 0;
+  }
+  if (tid == 0) sh.abort = 0;
+  PipePlan pl;
+  pl.n1 = c->n_p1;
+  pl.n2 = c->n_p2;
+  pl.ntot = c->n_total;
+  pl.p1u = c->p1_per_unit;
+  pl.p2u = c->p2_per_unit;
+  pl.grid = gridDim.x;
+  const int nbuf = pipe_bufs(a.T);
+  const int bstride = pipe_buf_tokens(a.T) * KMAX;
+  if (c->n_rblocks != 0) {  // plans for this kernel take their slots from the router
+    if (tid == 0) st_agent(&a.s.ctrl->err, 2);
+    return;
+  }
+  __syncthreads();
+  if (__builtin_amdgcn_readfirstlane(tid >> 6) == kPipeWaves)  // uniform branch per wave
+    pipe_control<KCH1, KCH2>(a, sh, pl, xs, nbuf, bstride);
+  else pipe_streamer<KCH1, KCH2, MS>(a, sh, pl, xs, nbuf, bstride, a.wait_limit * 16);
+}
+
+// ---------------------------------------------------------------------------
 // Weight packing (once per set_weights)
 // ---------------------------------------------------------------------------
 
@@ -1106,23 +1612,25 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
 }
 
 static size_t stream_lds_bytes(int H, int I) {
-  return (size_t)kStreamTokens * (size_t)(H > I ? H : I) * sizeof(float);
+  return (size_t)2 * kPipeTokens * (size_t)(H > I ? H : I) * sizeof(float);
 }
 
-// Token rows per streaming pass for a batch of T tokens.
-static int stream_mt(int T) { return T <= 2 ? 2 : kStreamTokens; }
+// Tokens per dot-product sub-pass for a batch of T tokens (an expert sees
+// about 4T/32 of them).
+static int stream_ms(int T) { return T <= 2 ? 1 : (T <= 16 ? 2 : 4); }
 
-static const void *stream_fn(int H, int I, int mt) {
-#define MOE_STREAM_CASE(K1, K2)                                                              \
-  if (H == (K1)*256 && I == (K2)*256)                                                         \
-    return mt == 2 ? reinterpret_cast<const void *>(&expert_stream_kernel<K1, K2, 2>)         \
-                   : reinterpret_cast<const void *>(&expert_stream_kernel<K1, K2, kStreamTokens>);
+static const void *stream_fn(int H, int I, int ms) {
+#define MOE_STREAM_CASE(K1, K2)                                                          \
+  if (H == (K1)*256 && I == (K2)*256)                                                     \
+    return ms == 1 ? reinterpret_cast<const void *>(&expert_pipe_kernel<K1, K2, 1>)       \
+         : ms == 2 ? reinterpret_cast<const void *>(&expert_pipe_kernel<K1, K2, 2>)       \
+                   : reinterpret_cast<const void *>(&expert_pipe_kernel<K1, K2, 4>);
   MOE_STREAM_SHAPES(MOE_STREAM_CASE)
 #undef MOE_STREAM_CASE
   return nullptr;
 }
 
-bool stream_supported(int H, int I) { return stream_fn(H, I, kStreamTokens) != nullptr; }
+bool stream_supported(int H, int I) { return stream_fn(H, I, 4) != nullptr; }
 
 template <int BM> static void *mfma_fn() {
   return reinterpret_cast<void *>(&expert_mfma_kernel<BM>);
@@ -1140,12 +1648,12 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
   switch (tile_rows) {
     case 0: {
       const size_t lds = stream_lds_bytes(a.H, a.I);
-      const void *fn = stream_fn(a.H, a.I, stream_mt(a.T));
+      const void *fn = stream_fn(a.H, a.I, stream_ms(a.T));
       if (!fn) return hipErrorInvalidValue;
       err = ensure_lds_attr(fn, lds);
       if (err != hipSuccess) return err;
       void *args[] = {const_cast<ExpertArgs *>(&a)};
-      err = hipLaunchKernel(fn, dim3(grid), dim3(kThreads), args, lds, st);
+      err = hipLaunchKernel(fn, dim3(grid), dim3(kPipeThreads), args, lds, st);
       if (err != hipSuccess) return err;
       break;
     }
@@ -1190,9 +1698,9 @@ int expert_blocks_per_cu(int tile_rows) {
   hipError_t e = hipSuccess;
   switch (tile_rows) {
     case 0: {
-      const void *fn = stream_fn(2048, 1792, kStreamTokens);
+      const void *fn = stream_fn(2048, 1792, 4);
       if (!fn) return 1;
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kThreads,
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kPipeThreads,
                                                        stream_lds_bytes(2048, 1792));
       break;
     }
