@@ -84,7 +84,9 @@ static int auto_plan(int T, bool stream_ok) {
 }
 
 static int ctx_plan(const moe_ctx *ctx, int T) {
-  return ctx->tile_override >= 0 ? ctx->tile_override : auto_plan(T, ctx->stream_ok);
+  const int p = ctx->tile_override >= 0 ? ctx->tile_override : auto_plan(T, ctx->stream_ok);
+  // the streaming plan keeps the batch's slot -> token map in LDS
+  return p == 0 && T > stream_max_tokens() ? 32 : p;
 }
 
 template <typename T>

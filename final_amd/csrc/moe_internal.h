@@ -99,6 +99,8 @@ hipError_t launch_pack_w13(float *dst, const float *w1, const float *w3, int H,
 int router_tokens_per_block(int T);
 // Whether the weight-streaming kernel is compiled for (H, I).
 bool stream_supported(int H, int I);
+// Largest batch the streaming plan handles (its slot -> token map is in LDS).
+int stream_max_tokens();
 // Max resident blocks per CU of the expert kernel for a plan.
 int expert_blocks_per_cu(int tile_rows);
 // Columns of the B tile of the MFMA kernel for a plan.

@@ -1057,60 +1057,48 @@ void expert_stream_kernel(ExpertArgs a) {
 #define MOE_STREAM_SHAPES(X) X(8, 7)
 
 // ---------------------------------------------------------------------------
-// Decoupled weight-streaming kernel (small T).
+// Weight-streaming kernel for small T (expert_ring_kernel).
 //
-// A wave's vector-memory loads complete in issue order, so a wave that keeps
-// weight rows in flight cannot wait for any other load (a dependency counter,
-// a token row, a result store) without also waiting for those rows.  Each
-// block therefore splits the work by wave: eight streaming waves only load
-// weight rows into registers, one task ahead, and dot them with token rows
-// held in LDS; one control wave copies token rows into LDS with
-// direct-to-LDS loads, polls dependencies, reduces and stores results and
-// signals, issuing everything one step needs before a single wait.  The waves
-// hand over through LDS flags; there is no block barrier after start-up.
+// HBM saturates with ~32 KiB of loads in flight per CU, and every round trip
+// a CU makes queues behind whatever it already has in flight, so this kernel
+// keeps each wave only a few KiB ahead and never puts a control round trip
+// between a wave and its weights.  Each block has eight streaming waves and
+// one control wave.  Streaming wave w owns the k slice [256w, 256w + 256) of
+// a task's 16 weight rows and walks it in 16 steps of 16 floats; a step loads
+// one f32x4 of weights per lane (lane l: row l%16, k offset 4*(l/16)) and one
+// f32x4 of token rows per pass of 16 tokens in the same shape, and feeds both
+// to v_mfma_f32_16x16x4f32 (16 rows x 16 tokens, k permuted consistently in
+// the A and B operands).  Loads run kRingDepth steps ahead in a register ring
+// that crosses task boundaries.  The control wave polls the dependency
+// counters, sums the eight k-slice partials a task leaves in LDS, stores the
+// results (SwiGLU applied for gate/up), and signals.
 //
-// Tasks are dealt round-robin (block b takes b, b + G, b + 2G, ... of the
-// task list, G = grid size), so both roles derive the block's sequence from
-// the plan without claiming.  Task = 16 weight rows of one active expert
-// (gate/up: W1 and W3 rows of 8 intermediate columns; down: W2 rows of 16
-// output columns) over all of the expert's tokens, in items of up to 8
-// tokens.  Streaming wave w holds rows 4*(w%4) .. +3 over the k half w/4.
-// Every task waits only on tasks of smaller index and each block runs its
-// tasks in increasing order, so the smallest unfinished task always runs.
+// Tasks are dealt round-robin (block b runs tasks b, b + G, ...; G = grid) in
+// the plan's order: gate/up row blocks expert by expert, then down row
+// blocks, then the combine.  A task waits only on tasks of smaller index and
+// each block runs its tasks in increasing order, so the smallest unfinished
+// task always runs.
 // ---------------------------------------------------------------------------
 
-constexpr int kPipeWaves = 8;                        // streaming waves
-constexpr int kPipeThreads = (kPipeWaves + 1) * 64;  // + the control wave
-constexpr int kPipeGroups = 4;                       // row groups of 4 rows
-constexpr int kPipeSplit = kPipeWaves / kPipeGroups; // k halves
-constexpr int kPipeChunks = 4;                       // 256-float chunks per wave
-constexpr int kPipeTokens = 8;                       // token rows per item
-constexpr int kPipeMaxBufs = 4;                      // token buffers (items in flight)
-static_assert(kPipeGroups * kStreamRowsPerWave == kStreamRows, "16 rows per task");
-static_assert(kPipeSplit * kPipeChunks * 256 >= 2048, "k halves cover rows of <= 2048");
+constexpr int kRingWaves = 8;                       // k-slice streaming waves
+constexpr int kRingThreads = (kRingWaves + 1) * 64; // + the control wave
+constexpr int kRingSteps = 16;                      // 16-float k steps per wave per task
+constexpr int kRingDepth = 4;                       // steps in flight ahead of the MFMAs
+constexpr int kRingTokens = 16;                     // tokens per MFMA pass
+constexpr int kRingSlice = kRingSteps * 16;         // floats of k per wave (256)
+constexpr int kRingMaxSlots = 4096;                 // slot -> token map kept in LDS
+static_assert(kRingWaves * kRingSlice == 2048, "k slices cover rows of <= 2048 floats");
+static_assert(kRingSteps % kRingDepth == 0, "ring rotation realigns at task boundaries");
 
-// kind: 1 gate/up rows, 2 down rows, 3 combine, 4 past the end.
-struct PipeTask {
-  int kind, q, u, e, cnt, slot0, col, npass;
-};
-
-struct PipeShared {
+struct RingShared {
   int active[kExperts], counts[kExperts], offsets[kExperts];
-  int xseq[kPipeMaxBufs];  // xseq[b] == i once item i's token rows are in buffer b
-  int done[kPipeMaxBufs];  // streaming waves finished with buffer b's item
+  int tok[kRingMaxSlots];  // slot -> token
+  int dep_ok;              // bit u: every gate/up task of unit u is done
+  int p2_ok;               // every down task is done
+  int flushed;             // items whose partials the control wave has consumed
+  int done[2];             // streaming waves that wrote item i's partials into buffer i & 1
   int abort;
-  float res[kPipeMaxBufs][kPipeSplit][kPipeTokens][kStreamRows];
 };
-
-// Token buffers: an item holds at most min(T, 8) token rows, and the LDS
-// space of two 8-row buffers is split into as many buffers (2 to 4) as fit.
-__host__ __device__ constexpr int pipe_buf_tokens(int T) {
-  return T < 1 ? 1 : (T < kPipeTokens ? T : kPipeTokens);
-}
-__host__ __device__ constexpr int pipe_bufs(int T) {
-  return 2 * kPipeTokens / pipe_buf_tokens(T) < kPipeMaxBufs ? 2 * kPipeTokens / pipe_buf_tokens(T)
-                                                               : kPipeMaxBufs;
-}
 
 __device__ __forceinline__ int lds_load(const int *p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1127,14 +1115,50 @@ __device__ __forceinline__ void acquire_lds() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// The plan values both roles need, wave-uniform.
-struct PipePlan {
+// 100 MHz constant clock: waits are bounded in time, not in polls.
+__device__ __forceinline__ long long ring_now() { return __builtin_amdgcn_s_memrealtime(); }
+constexpr long long kRingTicksPerLimit = 20;  // wait_limit x 200 ns
+
+// Streaming side: wait until cond(*p) holds.  False if the block aborts; a
+// wait longer than `ticks` reports a device timeout and aborts the block.
+template <typename Cond>
+__device__ __forceinline__ bool ring_wait(const int *p, Cond cond, int *abort_flag, int *err,
+                                          long long ticks) {
+  if (cond(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
+    acquire_lds();
+    return true;
+  }
+  const long long t0 = ring_now();
+  while (!cond(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
+    if (lds_load(abort_flag)) return false;
+    if (ring_now() - t0 > ticks) {
+      if ((threadIdx.x & 63) == 0) {
+        st_agent(err, 1);
+        lds_store(abort_flag, 1);
+      }
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  acquire_lds();
+  return true;
+}
+
+struct RingPlan {
   int n1, n2, ntot, p1u, p2u, grid;
 };
 
-__device__ __forceinline__ PipeTask pipe_task(const PipeShared &sh, const PipePlan &pl, int j) {
+// A task of the block's sequence, wave-uniform.  kind: 1 gate/up rows, 2
+// down rows, 3 combine, 4 past the end.  A row task runs in groups of up to
+// 16 * P tokens (one pass of the ring per group).
+struct RingTask {
+  int kind, q, u, e, cnt, slot0, col, ngroups;
+};
+
+template <int P>
+__device__ __forceinline__ RingTask ring_task(const RingShared &sh, const RingPlan &pl, int j) {
   const int task = (int)blockIdx.x + j * pl.grid;
-  PipeTask t{4, 0, 0, 0, 0, 0, 0, 1};
+  RingTask t{4, 0, 0, 0, 0, 0, 0, 1};
   if (task >= pl.ntot) return t;
   if (task < pl.n1) {
     t.kind = 1;
@@ -1154,106 +1178,102 @@ __device__ __forceinline__ PipeTask pipe_task(const PipeShared &sh, const PipePl
     t.e = __builtin_amdgcn_readfirstlane(sh.active[t.u]);
     t.cnt = __builtin_amdgcn_readfirstlane(sh.counts[t.e]);
     t.slot0 = __builtin_amdgcn_readfirstlane(sh.offsets[t.e]);
-    t.npass = t.cnt > 0 ? (t.cnt + kPipeTokens - 1) / kPipeTokens : 1;
+    t.ngroups = t.cnt > 0 ? (t.cnt + kRingTokens * P - 1) / (kRingTokens * P) : 1;
   }
   return t;
 }
 
-// Streaming side: wait until *p == want; false if the block aborts or the
-// control wave stops answering.
-__device__ __forceinline__ bool pipe_wait(const int *p, int want, const int *abort_flag,
-                                          int limit) {
-  int spins = 0;
-  while (__builtin_amdgcn_readfirstlane(lds_load(p)) != want) {
-    if (lds_load(abort_flag) || ++spins > limit) return false;
-    __builtin_amdgcn_s_sleep(1);
-  }
-  acquire_lds();
-  return true;
-}
-
-// Raw buffer descriptors of the weight arrays: the streaming waves address a
-// row by a scalar byte offset and a lane by one shared vector offset, and a
-// descriptor with no records yields zeros without touching memory.
-struct PipeWeights {
-  __amdgpu_buffer_rsrc_t w13, w2, none;
+// Buffer descriptors: weights, token rows, intermediate rows, and an empty
+// one whose loads return zeros without touching memory.
+struct RingRsrc {
+  __amdgpu_buffer_rsrc_t w13, w2, x, inter, none;
 };
 
-__device__ __forceinline__ PipeWeights pipe_weights(const ExpertArgs &a) {
+__device__ __forceinline__ RingRsrc ring_rsrc(const ExpertArgs &a) {
+  RingRsrc r;
   const size_t b13 = (size_t)kExperts * 2 * a.I * a.H * sizeof(float);
   const size_t b2 = (size_t)kExperts * a.H * a.I * sizeof(float);
-  PipeWeights w;
-  w.w13 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.w.w13), 0, (int)b13, kBufferRsrcWord3);
-  w.w2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.w.w2), 0, (int)b2, kBufferRsrcWord3);
-  w.none = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.w.w2), 0, 0, kBufferRsrcWord3);
-  return w;
+  const size_t bx = (size_t)a.T * a.H * sizeof(float);
+  r.w13 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.w.w13), 0, (int)b13, kBufferRsrcWord3);
+  r.w2 = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.w.w2), 0, (int)b2, kBufferRsrcWord3);
+  r.x = __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(a.x), 0, (int)bx, kBufferRsrcWord3);
+  r.inter = __builtin_amdgcn_make_buffer_rsrc(a.s.inter, 0, (int)a.s.inter_bytes, kBufferRsrcWord3);
+  r.none = __builtin_amdgcn_make_buffer_rsrc(a.s.inter, 0, 0, kBufferRsrcWord3);
+  return r;
 }
 
-// Issue one task's weight loads for this wave (rows of group rg over k half
-// h).  Chunks past the end of a row and tasks without weight rows read
-// through the empty descriptor, so every register has one unconditional load.
-template <int KCH1, int KCH2>
-__device__ __forceinline__ void pipe_issue(const ExpertArgs &a, const PipeWeights &pw,
-                                           const PipeTask &t, int rg, int h,
-                                           f32x4 (&buf)[kStreamRowsPerWave][kPipeChunks]) {
-  const int lane = threadIdx.x & 63;
-  const int H = a.H, I = a.I;
-  __amdgpu_buffer_rsrc_t rs = pw.none;
-  uint32_t r0 = 0, s1 = 0, s2 = 0, s3 = 0;  // row byte offsets (row 0, then steps)
-  int nch = 0;
+constexpr uint32_t kRingOff = 0xFFFF0000u;  // lane offset past any buffer: loads read 0
+
+// What one streaming lane loads for a group of a task: the weight row byte
+// offset (with this wave's k slice) and a token-row byte offset per pass.
+template <int P>
+struct RingWork {
+  __amdgpu_buffer_rsrc_t wr, xr;
+  uint32_t woff;
+  uint32_t xoff[P];
+  int npass;
+};
+
+template <int P>
+__device__ __forceinline__ RingWork<P> ring_work(const ExpertArgs &a, const RingShared &sh,
+                                                 const RingPlan &pl, const RingRsrc &rr,
+                                                 const RingTask &t, int g, int w) {
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  RingWork<P> r;
+  r.wr = rr.none;
+  r.xr = rr.none;
+  r.woff = kRingOff;
+  r.npass = 0;
+#pragma unroll
+  for (int p = 0; p < P; ++p) r.xoff[p] = kRingOff;
+  if (t.kind != 1 && t.kind != 2) return r;
+  const int m0 = g * kRingTokens * P;
+  // every wave writes partials for every pass of the group (zeros from a
+  // slice past the end of the rows), so the control wave sums all eight
+  r.npass = min(P, (t.cnt - m0 + kRingTokens - 1) / kRingTokens);
+  const int K = t.kind == 1 ? a.H : a.I;
+  const int k0 = w * kRingSlice;
+  if (k0 >= K) return r;  // this wave's slice is past the end of the rows
+  const int kl = k0 + 4 * lg;
   if (t.kind == 1) {
-    const int n = t.col + rg * 2;  // W1/W3 rows n, n+1 of the packed [I/32][2][32][H]
-    const uint32_t pa = (uint32_t)(n >> 5) * 64 + (n & 31);
-    r0 = ((uint32_t)t.e * 2 * I + pa) * (uint32_t)H * 4u;
-    s1 = H * 4u;
-    s2 = 32u * H * 4u;
-    s3 = 33u * H * 4u;
-    rs = pw.w13;
-    nch = KCH1 - h * kPipeChunks;
-  } else if (t.kind == 2) {
-    r0 = ((uint32_t)t.e * H + t.col + rg * kStreamRowsPerWave) * (uint32_t)I * 4u;
-    s1 = I * 4u;
-    s2 = 2u * I * 4u;
-    s3 = 3u * I * 4u;
-    rs = pw.w2;
-    nch = KCH2 - h * kPipeChunks;
-  }
-  const uint32_t soff[kStreamRowsPerWave] = {r0, r0 + s1, r0 + s2, r0 + s3};
-  const int voff = (h * kPipeChunks * 256 + lane * 4) * (int)sizeof(float);
+    // MFMA row li: W1 row col + li (li < 8) or W3 row col + li - 8, packed
+    // [I/32][2][32][H] so that the two are 32 rows apart
+    const int n = t.col + (li & 7);
+    const uint32_t prow = (uint32_t)(n >> 5) * 64 + (li >= 8 ? 32 : 0) + (n & 31);
+    r.wr = rr.w13;
+    r.woff = (((uint32_t)t.e * 2 * a.I + prow) * (uint32_t)a.H + kl) * 4u;
+    r.xr = rr.x;
 #pragma unroll
-  for (int c = 0; c < kPipeChunks; ++c) {
-    const __amdgpu_buffer_rsrc_t rc = c < nch ? rs : pw.none;
-#pragma unroll
-    for (int r = 0; r < kStreamRowsPerWave; ++r)
-      buf[r][c] = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rc, voff + c * 1024, (int)soff[r], 0));
-  }
-}
-
-// acc[r][m] = this lane's part of row r . token row m (MS token rows at xb,
-// row stride KMAX), over the wave's nch chunks.
-template <int MS, int KMAX>
-__device__ __forceinline__ void pipe_dots(const f32x4 (&buf)[kStreamRowsPerWave][kPipeChunks],
-                                          const float *xb, int nch,
-                                          float (&acc)[kStreamRowsPerWave][MS]) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int r = 0; r < kStreamRowsPerWave; ++r)
-#pragma unroll
-    for (int m = 0; m < MS; ++m) acc[r][m] = 0.0f;
-#pragma unroll
-  for (int c = 0; c < kPipeChunks; ++c) {
-    if (c < nch) {
-#pragma unroll
-      for (int m = 0; m < MS; ++m) {
-        const f32x4 xv = ld4(xb + m * KMAX + c * 256 + lane * 4);
-#pragma unroll
-        for (int r = 0; r < kStreamRowsPerWave; ++r)
-#pragma unroll
-          for (int q = 0; q < 4; ++q) acc[r][m] = __builtin_fmaf(buf[r][c][q], xv[q], acc[r][m]);
+    for (int p = 0; p < P; ++p) {
+      const int m = m0 + p * kRingTokens + li;
+      if (m < t.cnt) {
+        const int s = min(t.slot0 + m, kRingMaxSlots - 1);  // plans here have T * 4 <= kRingMaxSlots
+        int tk = sh.tok[s];
+        tk = tk < 0 ? 0 : (tk >= a.T ? a.T - 1 : tk);
+        r.xoff[p] = ((uint32_t)tk * a.H + kl) * 4u;
       }
     }
+  } else {
+    r.wr = rr.w2;
+    r.woff = (((uint32_t)t.e * a.H + t.col + li) * (uint32_t)a.I + kl) * 4u;
+    r.xr = rr.inter;
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      const int m = m0 + p * kRingTokens + li;
+      if (m < t.cnt) r.xoff[p] = ((uint32_t)(t.slot0 + m) * a.I + kl) * 4u;
+    }
   }
+  return r;
+}
+
+// One ring step's loads (weights + every pass's token rows) into one slot.
+template <int P>
+__device__ __forceinline__ void ring_issue(const RingWork<P> &r, int s, f32x4 &wt,
+                                           f32x4 (&xv)[P]) {
+  wt = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.wr, r.woff + s * 64, 0, 0));
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+    xv[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + s * 64, 0, 0));
 }
 
 // Weighted top-4 sum of one token plus the residual, by one wave (the same
@@ -1296,241 +1316,261 @@ __device__ void combine_token_wave(const ExpertArgs &a, int tok) {
   }
 }
 
-// One task on the streaming side: every item (pass of up to 8 tokens) waits
-// for its token rows, dots them in sub-passes of MS tokens, reduces over the
-// wave's lanes and leaves the sums in res[b][h][token][row].
-template <int KCH1, int KCH2, int MS>
-__device__ __forceinline__ bool pipe_process(const ExpertArgs &a, PipeShared &sh, const float *xs,
-                                             int nbuf, int bstride, const PipeTask &t,
-                                             const f32x4 (&buf)[kStreamRowsPerWave][kPipeChunks],
-                                             int &it, int &b, int rg, int h, int w, int limit) {
-  constexpr int KMAX = (KCH1 > KCH2 ? KCH1 : KCH2) * 256;
-  constexpr int V = kStreamRowsPerWave * MS;
-  constexpr int SH = 6 - log2i(V);
-  const int lane = threadIdx.x & 63;
-  if (t.kind == 3) {
-    if (!pipe_wait(&sh.xseq[b], it, &sh.abort, limit)) return false;
-    combine_token_wave(a, t.q * kCombineTokens + w);
-    // nothing of the combine stays in flight: the compiler's wait counts for
-    // the weight buffers then treat them as the only outstanding loads
-    __builtin_amdgcn_s_waitcnt(0);
-    release_lds();
-    if (lane == 0) __hip_atomic_fetch_add(&sh.done[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    ++it;
-    b = b + 1 == nbuf ? 0 : b + 1;
-    return true;
-  }
-  const int nch = (t.kind == 1 ? KCH1 : KCH2) - h * kPipeChunks;
-  for (int p = 0; p < t.npass; ++p, ++it, b = b + 1 == nbuf ? 0 : b + 1) {
-    if (!pipe_wait(&sh.xseq[b], it, &sh.abort, limit)) return false;
-    const int nt = min(kPipeTokens, t.cnt - p * kPipeTokens);
-    const float *xb = xs + (size_t)b * bstride + h * kPipeChunks * 256;
-    for (int s = 0; s < nt; s += MS) {
-      float acc[kStreamRowsPerWave][MS];
-      pipe_dots<MS, KMAX>(buf, xb + s * KMAX, nch, acc);
-      float v[V];  // value r*MS + m
-#pragma unroll
-      for (int r = 0; r < kStreamRowsPerWave; ++r)
-#pragma unroll
-        for (int m = 0; m < MS; ++m) v[r * MS + m] = acc[r][m];
-      wave_transpose_sum<V, 1>(v);
-      const int i = lane >> SH;
-      if ((lane & ((1 << SH) - 1)) == 0)
-        sh.res[b][h][s + i % MS][rg * kStreamRowsPerWave + i / MS] = v[0];
-    }
-    release_lds();
-    if (lane == 0) __hip_atomic_fetch_add(&sh.done[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  }
-  return true;
+// Partials of item i: res[i & 1][wave][pass][row][token], 16 x 16 per pass.
+template <int P>
+__device__ __forceinline__ float *ring_res(float *res, int b, int w, int p) {
+  return res + ((((size_t)b * kRingWaves + w) * P + p) * kRingTokens * kRingTokens);
 }
 
-// Streaming side.  Two register buffers alternate: while one task's rows are
-// dotted, the next task's rows are in flight.  Every path through the loop
-// body issues both buffers in the same order and the loop has one exit, at
-// the end, so the compiler's wait counts see the current buffer as the older
-// of the two and never wait for the one in flight.
-template <int KCH1, int KCH2, int MS>
-__device__ void pipe_streamer(const ExpertArgs &a, PipeShared &sh, const PipePlan &pl,
-                              const float *xs, int nbuf, int bstride, int limit) {
-  // wave-uniform in scalar registers (descriptors and row offsets stay scalar)
+template <int P>
+__device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, const RingPlan &pl,
+                              long long ticks) {
+  int *err = &a.s.ctrl->err;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rg = w % kPipeGroups, h = w / kPipeGroups;
-  const PipeWeights pw = pipe_weights(a);
-  f32x4 bufA[kStreamRowsPerWave][kPipeChunks], bufB[kStreamRowsPerWave][kPipeChunks];
-  int it = 0, ib = 0;  // item counter and its token buffer
+  const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
+  const RingRsrc rr = ring_rsrc(a);
+  f32x4 wt[kRingDepth];
+  f32x4 xv[kRingDepth][P];
+  int j = 0, g = 0, it = 0;  // task, group within it, item (group) counter
+  RingTask t = ring_task<P>(sh, pl, 0);
+  RingWork<P> cur = ring_work<P>(a, sh, pl, rr, t, 0, w);
   bool ok = true;
-  PipeTask tA = pipe_task(sh, pl, 0);
-  pipe_issue<KCH1, KCH2>(a, pw, tA, rg, h, bufA);
-  PipeTask tB = pipe_task(sh, pl, 1);
-  pipe_issue<KCH1, KCH2>(a, pw, tB, rg, h, bufB);
-  for (int j = 0;; j += 2) {
-    if (tA.kind != 4)
-      ok = ok && pipe_process<KCH1, KCH2, MS>(a, sh, xs, nbuf, bstride, tA, bufA, it, ib, rg, h, w, limit);
-    tA = pipe_task(sh, pl, j + 2);
-    pipe_issue<KCH1, KCH2>(a, pw, tA, rg, h, bufA);
-    if (tB.kind != 4)
-      ok = ok && pipe_process<KCH1, KCH2, MS>(a, sh, xs, nbuf, bstride, tB, bufB, it, ib, rg, h, w, limit);
-    tB = pipe_task(sh, pl, j + 3);
-    pipe_issue<KCH1, KCH2>(a, pw, tB, rg, h, bufB);
-    if (!ok || tA.kind == 4) break;
+  if (t.kind == 2)
+    ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> t.u) & 1; }, &sh.abort, err, ticks);
+  if (!ok) cur = ring_work<P>(a, sh, pl, rr, RingTask{4, 0, 0, 0, 0, 0, 0, 1}, 0, w);
+#pragma unroll
+  for (int s = 0; s < kRingDepth; ++s) ring_issue<P>(cur, s, wt[s], xv[s]);
+  while (true) {
+    // the next group: another group of this task or the first of the next
+    int jn = j, gn = g + 1;
+    RingTask tn = t;
+    if (gn >= t.ngroups) {
+      jn = j + 1;
+      gn = 0;
+      tn = ring_task<P>(sh, pl, jn);
+    }
+    const bool rows = t.kind == 1 || t.kind == 2;
+    RingWork<P> nxt;
+    f32x4 acc[P][2];
+#pragma unroll
+    for (int p = 0; p < P; ++p) acc[p][0] = acc[p][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < kRingSteps; ++s) {
+      const int sl = s % kRingDepth;
+      if (rows) {
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          if (p < cur.npass) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              acc[p][q & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(wt[sl][q], xv[sl][p][q],
+                                                                   acc[p][q & 1], 0, 0, 0);
+          }
+        }
+      }
+      if (s == kRingSteps - kRingDepth - 1) {
+        // the next group's rows are about to be issued: a down task needs
+        // every gate/up task of its unit done before its rows are read
+        if (ok && tn.kind == 2 && gn == 0)
+          ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> tn.u) & 1; }, &sh.abort, err, ticks);
+        nxt = ring_work<P>(a, sh, pl, rr, ok ? tn : RingTask{4, 0, 0, 0, 0, 0, 0, 1}, gn, w);
+      }
+      if (s + kRingDepth < kRingSteps) ring_issue<P>(cur, s + kRingDepth, wt[sl], xv[sl]);
+      else ring_issue<P>(nxt, s + kRingDepth - kRingSteps, wt[sl], xv[sl]);
+    }
+    if (rows && ok) {
+      // partials of item it into buffer it & 1, once item it - 2 is consumed
+      ok = ring_wait(&sh.flushed, [&](int v) { return v >= it - 1; }, &sh.abort, err, ticks);
+      if (ok) {
+        const int b = it & 1;
+#pragma unroll
+        for (int p = 0; p < P; ++p) {
+          if (p < cur.npass) {
+            float *r = ring_res<P>(res, b, w, p);
+            const f32x4 v = acc[p][0] + acc[p][1];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) r[(4 * lg + i) * kRingTokens + li] = v[i];
+          }
+        }
+        release_lds();
+        if (lane == 0) __hip_atomic_fetch_add(&sh.done[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      }
+      ++it;
+    } else if (t.kind == 3 && ok) {
+      ok = ring_wait(&sh.p2_ok, [&](int v) { return v != 0; }, &sh.abort, err, ticks);
+      if (ok) combine_token_wave(a, t.q * kCombineTokens + w);
+      // nothing of the combine stays in flight (the ring's compiler waits
+      // then count only ring loads)
+      __builtin_amdgcn_s_waitcnt(0);
+    }
+    if (!ok || t.kind == 4) break;
+    j = jn;
+    g = gn;
+    t = tn;
+    cur = nxt;
   }
 }
 
-// Control side: copy an item's token rows (x rows through slot_token for
-// gate/up, intermediate rows for down) into LDS buffer xb, 1 KiB per
-// direct-to-LDS load.  Returns without waiting.
-template <int KMAX>
-__device__ __forceinline__ void pipe_stage(const ExpertArgs &a, const PipeTask &t, int p,
-                                           float *xb) {
-  const int lane = threadIdx.x & 63;
-  const int nt = min(kPipeTokens, t.cnt - p * kPipeTokens);
-  const int slot0 = t.slot0 + p * kPipeTokens;
-  const int last = a.T * kTopK - 1;
-  const bool gate = t.kind == 1;
-  const int K = gate ? a.H : a.I;
-  const float *base = gate ? a.x : a.s.inter;
-  size_t roff = 0;
-  if (lane < nt) {
-    const int s = min(slot0 + lane, last);
-    roff = gate ? (size_t)slot_tok(a, s) * a.H : (size_t)s * a.I;
-  }
-  const int nch = K >> 8;
-  for (int m = 0; m < nt; ++m) {
-    const size_t ro = (size_t)__shfl((long long)roff, m, 64);
-    const float *src = base + ro + lane * 4;
-    for (int c = 0; c < nch; ++c)
-      __builtin_amdgcn_global_load_lds(
-          src + c * 256, (__attribute__((address_space(3))) void *)(xb + m * KMAX + c * 256), 16,
-          0, 0);
-  }
-}
-
-// Control side: sum the k halves and store an item's outputs with 16-byte
-// agent-scope stores (gate/up: silu(W1 x) * (W3 x) for 8 columns; down: 16).
-__device__ __forceinline__ void pipe_flush(const ExpertArgs &a, const PipeTask &t, int p, int b,
-                                           const PipeShared &sh, const AgentOut &inter_out,
+// Control side: sums the 8 k-slice partials of item (t, g) and stores the
+// outputs with 16-byte agent-scope stores (gate/up: silu(W1 x) * (W3 x) for
+// 8 columns; down: 16 columns).
+template <int P>
+__device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &t, int g,
+                                           const float *res, int b, const AgentOut &inter_out,
                                            const AgentOut &sout_out) {
   const int lane = threadIdx.x & 63;
-  const int nt = min(kPipeTokens, t.cnt - p * kPipeTokens);
-  const int slot0 = t.slot0 + p * kPipeTokens;
-  if (t.kind == 1) {
-    if (lane < nt * 2) {
-      const int m = lane >> 1, q = lane & 1;
-      f32x4 o;
+  const int m0 = g * kRingTokens * P;
+  const int nt = min(kRingTokens * P, t.cnt - m0);
+  // gate/up: lane -> (token, 4 columns): 2 lanes per token; down: 4 lanes
+  const int per = t.kind == 1 ? 2 : 4;
+  for (int f = lane; f < nt * per; f += 64) {
+    const int m = f / per, q = f % per;
+    const int p = m / kRingTokens, mt = m % kRingTokens;
+    f32x4 o;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int oc = q * 4 + j, rg = oc >> 1, jj = oc & 1;
-        const int rw = rg * kStreamRowsPerWave + jj;
-        const float g = sh.res[b][0][m][rw] + sh.res[b][1][m][rw];
-        const float u = sh.res[b][0][m][rw + 2] + sh.res[b][1][m][rw + 2];
-        o[j] = silu(g) * u;
+    for (int jj = 0; jj < 4; ++jj) {
+      const int c = q * 4 + jj;
+      if (t.kind == 1) {
+        float gs = 0.f, us = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRingWaves; ++w) {
+          const float *r = ring_res<P>(const_cast<float *>(res), b, w, p);
+          gs += r[c * kRingTokens + mt];
+          us += r[(8 + c) * kRingTokens + mt];
+        }
+        o[jj] = silu(gs) * us;
+      } else {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < kRingWaves; ++w) s += ring_res<P>(const_cast<float *>(res), b, w, p)[c * kRingTokens + mt];
+        o[jj] = s;
       }
-      inter_out.store((uint32_t)(((size_t)(slot0 + m) * a.I + t.col + q * 4) * sizeof(float)), o);
     }
-  } else {
-    if (lane < nt * 4) {
-      const int m = lane >> 2, q = lane & 3;
-      f32x4 o;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) o[j] = sh.res[b][0][m][q * 4 + j] + sh.res[b][1][m][q * 4 + j];
-      sout_out.store((uint32_t)(((size_t)(slot0 + m) * a.H + t.col + q * 4) * sizeof(float)), o);
-    }
+    const int slot = t.slot0 + m0 + m;
+    if (t.kind == 1)
+      inter_out.store((uint32_t)(((size_t)slot * a.I + t.col + q * 4) * sizeof(float)), o);
+    else
+      sout_out.store((uint32_t)(((size_t)slot * a.H + t.col + q * 4) * sizeof(float)), o);
   }
 }
 
-// Control side.  Each step issues the stores of every finished item, the
-// token copies of every item that has a free buffer and satisfied inputs, and
-// dependency polls, then waits once; the completed tasks' counters are bumped
-// and the staged items published after that wait.
-template <int KCH1, int KCH2>
-__device__ void pipe_control(const ExpertArgs &a, PipeShared &sh, const PipePlan &pl, float *xs,
-                             int nbuf, int bstride) {
-  constexpr int KMAX = (KCH1 > KCH2 ? KCH1 : KCH2) * 256;
+// Control side.  A step issues the stores of every item whose partials are
+// complete and, when one of the next tasks the streaming waves will reach
+// needs it, one dependency poll; then it waits once, publishes what the poll
+// found and signals the completed tasks.  Polls are few and rate-limited: the
+// counters sit in one memory channel that every wave's weight stream also
+// crosses.
+// The streaming waves write item i's partials only after item i - 2 is
+// flushed, and while finishing task k they need task k + 1's inputs, so they
+// are never more than 3 tasks past the control wave's flush position.
+constexpr int kRingHorizon = 4;            // tasks (from the flush position) polled for
+constexpr long long kRingPollTicks = 50;   // at most one poll per 500 ns
+
+template <int P>
+__device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *res,
+                             const RingPlan &pl) {
   Ctrl *c = a.s.ctrl;
   const int lane = threadIdx.x & 63;
   const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
-  const int limit = a.wait_limit * 4;
-  int j_fl = 0, p_fl = 0, it_fl = 0, b_fl = 0;  // next item to flush (task, pass, item, buffer)
-  int j_st = 0, p_st = 0, it_st = 0, b_st = 0;  // next item to stage
-  uint32_t dep_ok = 0;                // units whose gate/up tasks are all done
-  bool p2_ok = false;                 // every down task done
-  int idle = 0;
-  int sig = 0;  // lane u < 32: finished gate/up tasks of unit u; lane 32: down tasks
+  const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
+  uint32_t dep_ok = 0;  // units whose gate/up tasks are all done
+  bool p2_ok = false;   // every down task done
+  int j = 0, g = 0, it = 0;  // next item to flush
+  RingTask t = ring_task<P>(sh, pl, 0);
+  int sig = 0;
+  long long last = ring_now(), last_poll = 0;
   while (true) {
-    int flushed = 0, staged = 0;
-    // 1. results of finished items
-    while (it_fl < it_st) {
-      const int b = b_fl;
-      if (__builtin_amdgcn_readfirstlane(lds_load(&sh.done[b])) != kPipeWaves) break;
+    // inputs one of the next tasks needs and nobody has seen yet
+    int pu = -1;
+    bool pp2 = false;
+    for (int d = 0; d < kRingHorizon; ++d) {
+      const RingTask tt = d == 0 ? t : ring_task<P>(sh, pl, j + d);
+      if (tt.kind == 4) break;
+      if (tt.kind == 2 && !((dep_ok >> tt.u) & 1u)) {
+        pu = tt.u;
+        break;
+      }
+      if (tt.kind == 3 && !p2_ok) {
+        pp2 = true;
+        break;
+      }
+    }
+    // every row task flushed (only combine tasks or the end remain) and no
+    // input left to poll for: done
+    if (t.kind != 1 && t.kind != 2 && pu < 0 && !pp2) break;
+    bool prog = false;
+    const long long now = ring_now();
+    const bool poll = (pu >= 0 || pp2) && now - last_poll >= kRingPollTicks;
+    int pv = 0;
+    if (poll) {
+      last_poll = now;
+      if (lane == 0) pv = load_relaxed(pu >= 0 ? &a.s.dep[pu] : &c->p2_done);
+    }
+    // flush every complete item (in order)
+    int flushed_now = 0;
+    while (t.kind == 1 || t.kind == 2) {
+      const int b = it & 1;
+      if (__builtin_amdgcn_readfirstlane(lds_load(&sh.done[b])) != kRingWaves) break;
       acquire_lds();
-      const PipeTask t = pipe_task(sh, pl, j_fl);
-      if (t.kind == 1 || t.kind == 2) pipe_flush(a, t, p_fl, b, sh, inter_out, sout_out);
+      ring_flush<P>(a, t, g, res, b, inter_out, sout_out);
       lds_store(&sh.done[b], 0);
-      b_fl = b + 1 == nbuf ? 0 : b + 1;
-      if (++p_fl >= t.npass) {
-        if ((t.kind == 1 && lane == t.u) || (t.kind == 2 && lane == kExperts)) ++sig;
-        p_fl = 0;
-        ++j_fl;
+      ++it;
+      ++flushed_now;
+      if (++g >= t.ngroups) {
+        if ((t.kind == 1 && lane == t.u) || (t.kind == 2 && lane == 32)) ++sig;
+        g = 0;
+        ++j;
+        t = ring_task<P>(sh, pl, j);
       }
-      ++it_fl;
-      ++flushed;
+      if (flushed_now == 2) break;
     }
-    // 2. token rows of the next items, while buffers are free
-    while (it_st < it_fl + nbuf) {
-      const PipeTask t = pipe_task(sh, pl, j_st);
-      if (t.kind == 4) break;
-      if (t.kind == 2 && !((dep_ok >> t.u) & 1u)) {
-        if (__builtin_amdgcn_readfirstlane(load_relaxed(&a.s.dep[t.u])) < pl.p1u) break;
-        dep_ok |= 1u << t.u;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      }
-      if (t.kind == 3 && !p2_ok) {
-        if (__builtin_amdgcn_readfirstlane(load_relaxed(&c->p2_done)) < pl.n2) break;
-        p2_ok = true;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      }
-      if (t.kind != 3) pipe_stage<KMAX>(a, t, p_st, xs + (size_t)b_st * bstride);
-      b_st = b_st + 1 == nbuf ? 0 : b_st + 1;
-      ++staged;
-      ++it_st;
-      if (++p_st >= t.npass) {
-        p_st = 0;
-        ++j_st;
-      }
+    if (flushed_now) {
+      // partials are read: the streaming waves may reuse the buffers
+      release_lds();
+      if (lane == 0) lds_store(&sh.flushed, it);
+      prog = true;
     }
-    if (staged > 0 || flushed > 0) {
-      __builtin_amdgcn_s_waitcnt(0);  // stores complete, token rows in LDS
+    if (poll || flushed_now) {
+      __builtin_amdgcn_s_waitcnt(0);  // poll returned, stores complete
       if (sig) fetch_add(lane < kExperts ? &a.s.dep[lane] : &c->p2_done, sig);
       sig = 0;
-      release_lds();
-      if (lane == 0) {
-        int bb = b_st;  // walk back over the buffers staged in this step
-        for (int i = it_st - 1; i >= it_st - staged; --i) {
-          bb = bb == 0 ? nbuf - 1 : bb - 1;
-          lds_store(&sh.xseq[bb], i);
+      if (poll) {
+        pv = __builtin_amdgcn_readfirstlane(pv);
+        const bool ready = pu >= 0 ? pv >= pl.p1u : pv >= pl.n2;
+        if (ready) {
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // inputs that counter publishes
+          if (pu >= 0) dep_ok |= 1u << pu;
+          else p2_ok = true;
+          if (lane == 0) {
+            if (pu >= 0) lds_store(&sh.dep_ok, (int)dep_ok);
+            else lds_store(&sh.p2_ok, 1);
+          }
+          prog = true;
         }
       }
-      idle = 0;
+    }
+    if (prog) {
+      last = ring_now();
     } else {
-      if (it_fl == it_st && pipe_task(sh, pl, j_st).kind == 4) break;  // all flushed
-      if (++idle > limit) {
+      if (lds_load(&sh.abort)) break;
+      if (ring_now() - last > ticks) {
         if (lane == 0) {
           st_agent(&c->err, 1);
           lds_store(&sh.abort, 1);
         }
         break;
       }
-      __builtin_amdgcn_s_sleep(1);
+      __builtin_amdgcn_s_sleep(2);
     }
   }
 }
 
-template <int KCH1, int KCH2, int MS>
-__global__ __launch_bounds__(kPipeThreads) void expert_pipe_kernel(ExpertArgs a) {
-  static_assert(KCH1 <= kPipeSplit * kPipeChunks && KCH2 <= kPipeSplit * kPipeChunks, "row length");
-  constexpr int KMAX = (KCH1 > KCH2 ? KCH1 : KCH2) * 256;
-  extern __shared__ float xs[];  // [nbuf][min(T, 8)][max(H, I)]
-  __shared__ PipeShared sh;
+template <int KCH1, int KCH2, int P>
+__global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a) {
+  static_assert(KCH1 * 256 <= kRingWaves * kRingSlice && KCH2 * 256 <= kRingWaves * kRingSlice,
+                "row length");
+  extern __shared__ float res[];  // [2][kRingWaves][P][16][16]
+  __shared__ RingShared sh;
   const Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
   if (tid < kExperts) {
@@ -1538,28 +1578,31 @@ __global__ __launch_bounds__(kPipeThreads) void expert_pipe_kernel(ExpertArgs a)
     sh.counts[tid] = c->counts[tid];
     sh.offsets[tid] = c->offsets[tid];
   }
-  if (tid < kPipeMaxBufs) {
-    sh.xseq[tid] = -1;
-    sh.done[tid] = 0;
+  const int nslots = min(a.T * kTopK, kRingMaxSlots);
+  for (int i = tid; i < nslots; i += kRingThreads) sh.tok[i] = a.s.slot_token[i];
+  if (tid < 2) sh.done[tid] = 0;
+  if (tid == 0) {
+    sh.dep_ok = 0;
+    sh.p2_ok = 0;
+    sh.flushed = 0;
+    sh.abort = 0;
   }
-  if (tid == 0) sh.abort = 0;
-  PipePlan pl;
+  RingPlan pl;
   pl.n1 = c->n_p1;
   pl.n2 = c->n_p2;
   pl.ntot = c->n_total;
   pl.p1u = c->p1_per_unit;
   pl.p2u = c->p2_per_unit;
   pl.grid = gridDim.x;
-  const int nbuf = pipe_bufs(a.T);
-  const int bstride = pipe_buf_tokens(a.T) * KMAX;
   if (c->n_rblocks != 0) {  // plans for this kernel take their slots from the router
     if (tid == 0) st_agent(&a.s.ctrl->err, 2);
     return;
   }
   __syncthreads();
-  if (__builtin_amdgcn_readfirstlane(tid >> 6) == kPipeWaves)  // uniform branch per wave
-    pipe_control<KCH1, KCH2>(a, sh, pl, xs, nbuf, bstride);
-  else pipe_streamer<KCH1, KCH2, MS>(a, sh, pl, xs, nbuf, bstride, a.wait_limit * 16);
+  if (__builtin_amdgcn_readfirstlane(tid >> 6) == kRingWaves)  // uniform branch per wave
+    ring_control<P>(a, sh, res, pl);
+  else
+    ring_streamer<P>(a, sh, res, pl, 2 * (long long)a.wait_limit * kRingTicksPerLimit);
 }
 
 // ---------------------------------------------------------------------------
@@ -1611,26 +1654,28 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
   return hipGetLastError();
 }
 
-static size_t stream_lds_bytes(int H, int I) {
-  return (size_t)2 * kPipeTokens * (size_t)(H > I ? H : I) * sizeof(float);
+// Ring passes of 16 tokens kept per group for a batch of T tokens (an expert
+// sees at most T of them).
+static int ring_passes(int T) { return T <= 16 ? 1 : (T <= 32 ? 2 : 4); }
+
+static size_t stream_lds_bytes(int P) {
+  return (size_t)2 * kRingWaves * P * kRingTokens * kRingTokens * sizeof(float);
 }
 
-// Tokens per dot-product sub-pass for a batch of T tokens (an expert sees
-// about 4T/32 of them).
-static int stream_ms(int T) { return T <= 2 ? 1 : (T <= 16 ? 2 : 4); }
-
-static const void *stream_fn(int H, int I, int ms) {
+static const void *stream_fn(int H, int I, int P) {
 #define MOE_STREAM_CASE(K1, K2)                                                          \
   if (H == (K1)*256 && I == (K2)*256)                                                     \
-    return ms == 1 ? reinterpret_cast<const void *>(&expert_pipe_kernel<K1, K2, 1>)       \
-         : ms == 2 ? reinterpret_cast<const void *>(&expert_pipe_kernel<K1, K2, 2>)       \
-                   : reinterpret_cast<const void *>(&expert_pipe_kernel<K1, K2, 4>);
+    return P == 1 ? reinterpret_cast<const void *>(&expert_ring_kernel<K1, K2, 1>)        \
+         : P == 2 ? reinterpret_cast<const void *>(&expert_ring_kernel<K1, K2, 2>)        \
+                  : reinterpret_cast<const void *>(&expert_ring_kernel<K1, K2, 4>);
   MOE_STREAM_SHAPES(MOE_STREAM_CASE)
 #undef MOE_STREAM_CASE
   return nullptr;
 }
 
 bool stream_supported(int H, int I) { return stream_fn(H, I, 4) != nullptr; }
+
+int stream_max_tokens() { return kRingMaxSlots / kTopK; }
 
 template <int BM> static void *mfma_fn() {
   return reinterpret_cast<void *>(&expert_mfma_kernel<BM>);
@@ -1647,13 +1692,14 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
   hipError_t err = hipSuccess;
   switch (tile_rows) {
     case 0: {
-      const size_t lds = stream_lds_bytes(a.H, a.I);
-      const void *fn = stream_fn(a.H, a.I, stream_ms(a.T));
+      const int P = ring_passes(a.T);
+      const size_t lds = stream_lds_bytes(P);
+      const void *fn = stream_fn(a.H, a.I, P);
       if (!fn) return hipErrorInvalidValue;
       err = ensure_lds_attr(fn, lds);
       if (err != hipSuccess) return err;
       void *args[] = {const_cast<ExpertArgs *>(&a)};
-      err = hipLaunchKernel(fn, dim3(grid), dim3(kPipeThreads), args, lds, st);
+      err = hipLaunchKernel(fn, dim3(grid), dim3(kRingThreads), args, lds, st);
       if (err != hipSuccess) return err;
       break;
     }
@@ -1700,8 +1746,7 @@ int expert_blocks_per_cu(int tile_rows) {
     case 0: {
       const void *fn = stream_fn(2048, 1792, 4);
       if (!fn) return 1;
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kPipeThreads,
-                                                       stream_lds_bytes(2048, 1792));
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kRingThreads, stream_lds_bytes(4));
       break;
     }
     case 32:

@@ -120,7 +120,8 @@ int moe_device_status(moe_ctx *ctx, moe_stream_t stream);
  * (small T), 32/64/128 = MFMA grouped GEMM with that many rows per tile. */
 int moe_plan_tile_rows(const moe_ctx *ctx, int num_tokens);
 
-/* Overrides the plan (tests): rows = -1 automatic, 0 streaming, 32/64/128. */
+/* Overrides the plan (tests): rows = -1 automatic, 0 streaming, 32/64/128.
+ * Streaming covers batches of up to 1024 tokens; larger ones use 32. */
 int moe_force_tile_rows(moe_ctx *ctx, int rows);
 
 /* Test hook: scales the kernels' bounded-wait limit (1 = default, >1 shorter).
