@@ -1053,9 +1053,6 @@ void expert_stream_kernel(ExpertArgs a) {
   }
 }
 
-// Streaming-kernel instantiations: (H/256, I/256) pairs it is compiled for.
-#define MOE_STREAM_SHAPES(X) X(8, 7)
-
 // ---------------------------------------------------------------------------
 // Weight-streaming kernel for small T (expert_ring_kernel).
 //
@@ -1565,11 +1562,17 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
   }
 }
 
-template <int KCH1, int KCH2, int P>
+// Token passes per ring step: the fewest that cover the largest expert's
+// tokens (up to 4 passes; larger experts run in several groups).  A pass that
+// holds no tokens would still move 1 KiB per wave per step through the CU's
+// load-return path, so the kernel picks the count from the plan at run time.
+constexpr int kRingMaxPasses = 4;
+
+template <int KCH1, int KCH2>
 __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a) {
   static_assert(KCH1 * 256 <= kRingWaves * kRingSlice && KCH2 * 256 <= kRingWaves * kRingSlice,
                 "row length");
-  extern __shared__ float res[];  // [2][kRingWaves][P][16][16]
+  extern __shared__ float res[];  // [2][kRingWaves][passes][16][16]
   __shared__ RingShared sh;
   const Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
@@ -1599,11 +1602,24 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     return;
   }
   __syncthreads();
-  if (__builtin_amdgcn_readfirstlane(tid >> 6) == kRingWaves)  // uniform branch per wave
-    ring_control<P>(a, sh, res, pl);
-  else
-    ring_streamer<P>(a, sh, res, pl, 2 * (long long)a.wait_limit * kRingTicksPerLimit);
+  int maxcnt = 0;
+  for (int e = 0; e < kExperts; ++e) maxcnt = max(maxcnt, sh.counts[e]);
+  maxcnt = __builtin_amdgcn_readfirstlane(maxcnt);
+  const int passes = maxcnt <= kRingTokens ? 1 : (maxcnt <= 2 * kRingTokens ? 2 : kRingMaxPasses);
+  const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
+  if (__builtin_amdgcn_readfirstlane(tid >> 6) == kRingWaves) {  // uniform branch per wave
+    if (passes == 1) ring_control<1>(a, sh, res, pl);
+    else if (passes == 2) ring_control<2>(a, sh, res, pl);
+    else ring_control<kRingMaxPasses>(a, sh, res, pl);
+  } else {
+    if (passes == 1) ring_streamer<1>(a, sh, res, pl, 2 * ticks);
+    else if (passes == 2) ring_streamer<2>(a, sh, res, pl, 2 * ticks);
+    else ring_streamer<kRingMaxPasses>(a, sh, res, pl, 2 * ticks);
+  }
 }
+
+// Streaming-kernel instantiations: (H/256, I/256) pairs it is compiled for.
+#define MOE_STREAM_SHAPES(X) X(8, 7)
 
 // ---------------------------------------------------------------------------
 // Weight packing (once per set_weights)
@@ -1654,26 +1670,19 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
   return hipGetLastError();
 }
 
-// Ring passes of 16 tokens kept per group for a batch of T tokens (an expert
-// sees at most T of them).
-static int ring_passes(int T) { return T <= 16 ? 1 : (T <= 32 ? 2 : 4); }
-
-static size_t stream_lds_bytes(int P) {
-  return (size_t)2 * kRingWaves * P * kRingTokens * kRingTokens * sizeof(float);
+static size_t stream_lds_bytes() {
+  return (size_t)2 * kRingWaves * kRingMaxPasses * kRingTokens * kRingTokens * sizeof(float);
 }
 
-static const void *stream_fn(int H, int I, int P) {
-#define MOE_STREAM_CASE(K1, K2)                                                          \
-  if (H == (K1)*256 && I == (K2)*256)                                                     \
-    return P == 1 ? reinterpret_cast<const void *>(&expert_ring_kernel<K1, K2, 1>)        \
-         : P == 2 ? reinterpret_cast<const void *>(&expert_ring_kernel<K1, K2, 2>)        \
-                  : reinterpret_cast<const void *>(&expert_ring_kernel<K1, K2, 4>);
+static const void *stream_fn(int H, int I) {
+#define MOE_STREAM_CASE(K1, K2) \
+  if (H == (K1)*256 && I == (K2)*256) return reinterpret_cast<const void *>(&expert_ring_kernel<K1, K2>);
   MOE_STREAM_SHAPES(MOE_STREAM_CASE)
 #undef MOE_STREAM_CASE
   return nullptr;
 }
 
-bool stream_supported(int H, int I) { return stream_fn(H, I, 4) != nullptr; }
+bool stream_supported(int H, int I) { return stream_fn(H, I) != nullptr; }
 
 int stream_max_tokens() { return kRingMaxSlots / kTopK; }
 
@@ -1692,9 +1701,8 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
   hipError_t err = hipSuccess;
   switch (tile_rows) {
     case 0: {
-      const int P = ring_passes(a.T);
-      const size_t lds = stream_lds_bytes(P);
-      const void *fn = stream_fn(a.H, a.I, P);
+      const size_t lds = stream_lds_bytes();
+      const void *fn = stream_fn(a.H, a.I);
       if (!fn) return hipErrorInvalidValue;
       err = ensure_lds_attr(fn, lds);
       if (err != hipSuccess) return err;
@@ -1744,9 +1752,9 @@ int expert_blocks_per_cu(int tile_rows) {
   hipError_t e = hipSuccess;
   switch (tile_rows) {
     case 0: {
-      const void *fn = stream_fn(2048, 1792, 4);
+      const void *fn = stream_fn(2048, 1792);
       if (!fn) return 1;
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kRingThreads, stream_lds_bytes(4));
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, fn, kRingThreads, stream_lds_bytes());
       break;
     }
     case 32:
