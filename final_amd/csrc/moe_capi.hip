@@ -179,7 +179,10 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
   ctx->s.inter_bytes = (uint32_t)(S * I * sizeof(float));
   ctx->s.sout_bytes = (uint32_t)(S * H * sizeof(float));
   char *ctrl_mem = nullptr;
-  const size_t ctrl_bytes = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
+  // Ctrl, dep[max_units], then the ready lines on a 128-byte boundary
+  const size_t dep_end = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
+  const size_t ready_off = (dep_end + 127) / 128 * 128;
+  const size_t ctrl_bytes = ready_off + sizeof(int) * (size_t)kReadyLines * kReadyStride;
   if ((rc = dev_alloc(ctx, &ctrl_mem, ctrl_bytes))) {
     free_all(ctx);
     delete ctx;
@@ -187,6 +190,7 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
   }
   ctx->s.ctrl = reinterpret_cast<Ctrl *>(ctrl_mem);
   ctx->s.dep = reinterpret_cast<int *>(ctrl_mem + sizeof(Ctrl));
+  ctx->s.ready = reinterpret_cast<int *>(ctrl_mem + ready_off);
   if (hipMemset(ctrl_mem, 0, ctrl_bytes) != hipSuccess ||
       hipMemset(ctx->s.tb_done, 0, nb * sizeof(int)) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {

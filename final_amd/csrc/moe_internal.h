@@ -16,6 +16,10 @@ constexpr int kCombineTokens = 8;  // tokens per combine task
 constexpr int kStreamRowsPerWave = 4;   // weight rows per wave, streaming kernel
 constexpr int kStreamRows = kStreamRowsPerWave * 4;  // rows per streaming task
 constexpr int kStreamTokens = 8;  // token rows per streaming pass (LDS staged)
+// Streaming-plan blocks each get a private 128-byte line of ready bits (word
+// 0: units whose gate/up tasks are done, word 1: all down tasks done).
+constexpr int kReadyLines = 1024;
+constexpr int kReadyStride = 32;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset
@@ -65,6 +69,7 @@ struct Scratch {
   uint32_t sout_bytes;
   Ctrl *ctrl;
   int *dep;              // [max_units]
+  int *ready;            // [kReadyLines][32]: per-block ready bits, one 128-byte line each
 };
 
 struct RouterArgs {

@@ -418,6 +418,10 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
   const int units = min(s_units, a.max_units);
   for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
   if (a.tile_rows == 0) {
+    for (int i = tid; i < kReadyLines; i += kThreads) {
+      a.s.ready[i * kReadyStride] = 0;
+      a.s.ready[i * kReadyStride + 1] = 0;
+    }
     // slot = token block base + in-block rank (stable by token), as the
     // dispatch tasks of the tiled plans compute it
     for (int f = tid; f < T * kTopK; f += kThreads) {
@@ -1453,15 +1457,16 @@ __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &
 
 // Control side.  A step issues the stores of every item whose partials are
 // complete and, when one of the next tasks the streaming waves will reach
-// needs it, one dependency poll; then it waits once, publishes what the poll
-// found and signals the completed tasks.  Polls are few and rate-limited: the
-// counters sit in one memory channel that every wave's weight stream also
-// crosses.
+// needs an input not yet seen, a poll of the block's own ready line; then it
+// waits once, signals the completed tasks and publishes what the poll found.
+// The block whose signal completes a unit's gate/up tasks (or the down
+// tasks) sets that bit in every block's ready line, so each block polls a
+// line nobody else reads instead of all blocks polling the shared counters.
 // The streaming waves write item i's partials only after item i - 2 is
 // flushed, and while finishing task k they need task k + 1's inputs, so they
 // are never more than 3 tasks past the control wave's flush position.
 constexpr int kRingHorizon = 4;            // tasks (from the flush position) polled for
-constexpr long long kRingPollTicks = 50;   // at most one poll per 500 ns
+constexpr long long kRingPollTicks = 20;   // at most one poll per 200 ns
 
 template <int P>
 __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *res,
@@ -1501,7 +1506,7 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
     int pv = 0;
     if (poll) {
       last_poll = now;
-      if (lane == 0) pv = load_relaxed(pu >= 0 ? &a.s.dep[pu] : &c->p2_done);
+      if (lane < 2) pv = load_relaxed(&a.s.ready[(int)blockIdx.x * kReadyStride + lane]);
     }
     // flush every complete item (in order)
     int flushed_now = 0;
@@ -1529,18 +1534,36 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
     }
     if (poll || flushed_now) {
       __builtin_amdgcn_s_waitcnt(0);  // poll returned, stores complete
-      if (sig) fetch_add(lane < kExperts ? &a.s.dep[lane] : &c->p2_done, sig);
+      bool crossed = false;
+      if (sig) {
+        const int target = lane < kExperts ? pl.p1u : pl.n2;
+        const int old = fetch_add(lane < kExperts ? &a.s.dep[lane] : &c->p2_done, sig);
+        crossed = old < target && old + sig >= target;
+      }
       sig = 0;
+      const uint64_t cm = __builtin_amdgcn_ballot_w64(crossed);
+      if (cm) {
+        // this block completed units (bits 0..31) and/or the down tasks
+        // (bit 32): tell every block
+        const int ubits = (int)(uint32_t)cm;
+        const bool p2 = (cm >> 32) & 1;
+        for (int bb = lane; bb < pl.grid; bb += 64) {
+          if (ubits) __hip_atomic_fetch_or(&a.s.ready[bb * kReadyStride], ubits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (p2) __hip_atomic_fetch_or(&a.s.ready[bb * kReadyStride + 1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
       if (poll) {
-        pv = __builtin_amdgcn_readfirstlane(pv);
-        const bool ready = pu >= 0 ? pv >= pl.p1u : pv >= pl.n2;
-        if (ready) {
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // inputs that counter publishes
-          if (pu >= 0) dep_ok |= 1u << pu;
-          else p2_ok = true;
+        const uint32_t ub = (uint32_t)__builtin_amdgcn_readlane(pv, 0);
+        const bool p2r = __builtin_amdgcn_readlane(pv, 1) != 0;
+        const uint32_t nd = dep_ok | ub;
+        const bool np2 = p2_ok || p2r;
+        if (nd != dep_ok || np2 != p2_ok) {
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // inputs those bits publish
+          dep_ok = nd;
+          p2_ok = np2;
           if (lane == 0) {
-            if (pu >= 0) lds_store(&sh.dep_ok, (int)dep_ok);
-            else lds_store(&sh.p2_ok, 1);
+            lds_store(&sh.dep_ok, (int)dep_ok);
+            if (p2_ok) lds_store(&sh.p2_ok, 1);
           }
           prog = true;
         }
@@ -1597,7 +1620,9 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   pl.p1u = c->p1_per_unit;
   pl.p2u = c->p2_per_unit;
   pl.grid = gridDim.x;
-  if (c->n_rblocks != 0) {  // plans for this kernel take their slots from the router
+  // plans for this kernel take their slots from the router, and every block
+  // needs a ready line
+  if (c->n_rblocks != 0 || (int)gridDim.x > kReadyLines) {
     if (tid == 0) st_agent(&a.s.ctrl->err, 2);
     return;
   }
