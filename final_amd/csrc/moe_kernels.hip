@@ -1277,43 +1277,58 @@ __device__ __forceinline__ void ring_issue(const RingWork<P> &r, int s, f32x4 &w
     xv[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + s * 64, 0, 0));
 }
 
-// Weighted top-4 sum of one token plus the residual, by one wave (the same
-// arithmetic as combine_task).
-__device__ void combine_token_wave(const ExpertArgs &a, int tok) {
+// Combine task q (tokens 8q .. 8q + 7) by the 512 threads of the streaming
+// waves: thread ts takes column quads ts, ts + 512, ... of every token, two
+// tokens at a time so that 10 loads are in flight per thread.  Same
+// arithmetic as combine_task: FMA chain over k ascending, then the residual.
+__device__ void ring_combine(const ExpertArgs &a, int q, int ts) {
 #pragma clang fp contract(off)
-  if (tok >= a.T) return;
-  const int lane = threadIdx.x & 63;
+  constexpr int TB = 2;  // tokens per batch
   const int H4 = a.H >> 2;
   const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
   const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
   float4 *y4 = reinterpret_cast<float4 *>(a.y);
-  int slot[kTopK];
-  float wk[kTopK];
+  const int t0 = q * kCombineTokens;
+  const int nt = min(kCombineTokens, a.T - t0);
+  for (int k0 = 0; k0 < nt; k0 += TB) {
+    for (int c4 = ts; c4 < H4; c4 += kRingWaves * 64) {
+      float4 v[TB][kTopK], rv[TB];
+      float wk[TB][kTopK];
 #pragma unroll
-  for (int k = 0; k < kTopK; ++k) {
-    slot[k] = a.s.pos[(size_t)tok * kTopK + k];
-    wk[k] = a.s.wts[(size_t)tok * kTopK + k];
-  }
-  for (int c4 = lane; c4 < H4; c4 += 64) {
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int i = 0; i < TB; ++i) {
+        const int tok = t0 + min(k0 + i, nt - 1);
 #pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-      if (slot[k] >= 0 && slot[k] < a.T * kTopK) {
-        const float4 v = so[(size_t)slot[k] * H4 + c4];
-        acc.x = __builtin_fmaf(v.x, wk[k], acc.x);
-        acc.y = __builtin_fmaf(v.y, wk[k], acc.y);
-        acc.z = __builtin_fmaf(v.z, wk[k], acc.z);
-        acc.w = __builtin_fmaf(v.w, wk[k], acc.w);
+        for (int k = 0; k < kTopK; ++k) {
+          int slot = a.s.pos[(size_t)tok * kTopK + k];
+          wk[i][k] = a.s.wts[(size_t)tok * kTopK + k];
+          if (slot < 0 || slot >= a.T * kTopK) {
+            slot = 0;
+            wk[i][k] = 0.0f;
+          }
+          v[i][k] = so[(size_t)slot * H4 + c4];
+        }
+        rv[i] = r4 ? r4[(size_t)tok * H4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int i = 0; i < TB; ++i) {
+        if (k0 + i >= nt) break;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) {
+          acc.x = __builtin_fmaf(v[i][k].x, wk[i][k], acc.x);
+          acc.y = __builtin_fmaf(v[i][k].y, wk[i][k], acc.y);
+          acc.z = __builtin_fmaf(v[i][k].z, wk[i][k], acc.z);
+          acc.w = __builtin_fmaf(v[i][k].w, wk[i][k], acc.w);
+        }
+        if (r4) {
+          acc.x = rv[i].x + acc.x;
+          acc.y = rv[i].y + acc.y;
+          acc.z = rv[i].z + acc.z;
+          acc.w = rv[i].w + acc.w;
+        }
+        y4[(size_t)(t0 + k0 + i) * H4 + c4] = acc;
       }
     }
-    if (r4) {
-      const float4 r = r4[(size_t)tok * H4 + c4];
-      acc.x = r.x + acc.x;
-      acc.y = r.y + acc.y;
-      acc.z = r.z + acc.z;
-      acc.w = r.w + acc.w;
-    }
-    y4[(size_t)tok * H4 + c4] = acc;
   }
 }
 
@@ -1341,7 +1356,9 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
   if (!ok) cur = ring_work<P>(a, sh, pl, rr, RingTask{4, 0, 0, 0, 0, 0, 0, 1}, 0, w);
 #pragma unroll
   for (int s = 0; s < kRingDepth; ++s) ring_issue<P>(cur, s, wt[s], xv[s]);
-  while (true) {
+  // Row tasks run through the ring; the combine tasks, which come after
+  // every row task, run after it with the ring's registers free.
+  while (ok && (t.kind == 1 || t.kind == 2)) {
     // the next group: another group of this task or the first of the next
     int jn = j, gn = g + 1;
     RingTask tn = t;
@@ -1350,7 +1367,6 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
       gn = 0;
       tn = ring_task<P>(sh, pl, jn);
     }
-    const bool rows = t.kind == 1 || t.kind == 2;
     RingWork<P> nxt;
     f32x4 acc[P][2];
 #pragma unroll
@@ -1358,15 +1374,13 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
 #pragma unroll
     for (int s = 0; s < kRingSteps; ++s) {
       const int sl = s % kRingDepth;
-      if (rows) {
 #pragma unroll
-        for (int p = 0; p < P; ++p) {
-          if (p < cur.npass) {
+      for (int p = 0; p < P; ++p) {
+        if (p < cur.npass) {
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              acc[p][q & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(wt[sl][q], xv[sl][p][q],
-                                                                   acc[p][q & 1], 0, 0, 0);
-          }
+          for (int q = 0; q < 4; ++q)
+            acc[p][q & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(wt[sl][q], xv[sl][p][q],
+                                                                 acc[p][q & 1], 0, 0, 0);
         }
       }
       if (s == kRingSteps - kRingDepth - 1) {
@@ -1379,7 +1393,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
       if (s + kRingDepth < kRingSteps) ring_issue<P>(cur, s + kRingDepth, wt[sl], xv[sl]);
       else ring_issue<P>(nxt, s + kRingDepth - kRingSteps, wt[sl], xv[sl]);
     }
-    if (rows && ok) {
+    if (ok) {
       // partials of item it into buffer it & 1, once item it - 2 is consumed
       ok = ring_wait(&sh.flushed, [&](int v) { return v >= it - 1; }, &sh.abort, err, ticks);
       if (ok) {
@@ -1397,18 +1411,15 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
         if (lane == 0) __hip_atomic_fetch_add(&sh.done[b], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
       ++it;
-    } else if (t.kind == 3 && ok) {
-      ok = ring_wait(&sh.p2_ok, [&](int v) { return v != 0; }, &sh.abort, err, ticks);
-      if (ok) combine_token_wave(a, t.q * kCombineTokens + w);
-      // nothing of the combine stays in flight (the ring's compiler waits
-      // then count only ring loads)
-      __builtin_amdgcn_s_waitcnt(0);
     }
-    if (!ok || t.kind == 4) break;
     j = jn;
     g = gn;
     t = tn;
     cur = nxt;
+  }
+  for (; ok && t.kind == 3; t = ring_task<P>(sh, pl, ++j)) {
+    ok = ring_wait(&sh.p2_ok, [&](int v) { return v != 0; }, &sh.abort, err, ticks);
+    if (ok) ring_combine(a, t.q, (int)threadIdx.x);
   }
 }
 
