@@ -117,6 +117,195 @@ __device__ __forceinline__ float ref_sigmoid(float x) {
   return 1.0f / (1.0f + e);
 }
 
+// acc = FMA chain over k = 0 .. K-1 of x[k] * g[k] (LDS rows xp, gp), k
+// ascending (layer.cu:109-127).  The chain is latency-bound, so the operands
+// of the next 16 k are read while this 16 k's FMAs run; the loop body has no
+// branch so both operand sets stay in fixed registers.  K % 32 == 0.
+__device__ __forceinline__ float chain_dot(const float *gp, const float *xp, int K) {
+#pragma clang fp contract(off)
+  constexpr int U = 4;  // float4 per half step: 16 k
+  f32x4 ga[U], xa[U], gb[U], xb[U];
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    ga[u] = ld4(gp + 4 * u);
+    xa[u] = ld4(xp + 4 * u);
+  }
+  int k = 0;
+  for (; k < K - 8 * U; k += 8 * U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      gb[u] = ld4(gp + k + 4 * (U + u));
+      xb[u] = ld4(xp + k + 4 * (U + u));
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      acc = __builtin_fmaf(xa[u].x, ga[u].x, acc);
+      acc = __builtin_fmaf(xa[u].y, ga[u].y, acc);
+      acc = __builtin_fmaf(xa[u].z, ga[u].z, acc);
+      acc = __builtin_fmaf(xa[u].w, ga[u].w, acc);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ga[u] = ld4(gp + k + 8 * U + 4 * u);
+      xa[u] = ld4(xp + k + 8 * U + 4 * u);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      acc = __builtin_fmaf(xb[u].x, gb[u].x, acc);
+      acc = __builtin_fmaf(xb[u].y, gb[u].y, acc);
+      acc = __builtin_fmaf(xb[u].z, gb[u].z, acc);
+      acc = __builtin_fmaf(xb[u].w, gb[u].w, acc);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    gb[u] = ld4(gp + k + 4 * (U + u));
+    xb[u] = ld4(xp + k + 4 * (U + u));
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    acc = __builtin_fmaf(xa[u].x, ga[u].x, acc);
+    acc = __builtin_fmaf(xa[u].y, ga[u].y, acc);
+    acc = __builtin_fmaf(xa[u].z, ga[u].z, acc);
+    acc = __builtin_fmaf(xa[u].w, ga[u].w, acc);
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    acc = __builtin_fmaf(xb[u].x, gb[u].x, acc);
+    acc = __builtin_fmaf(xb[u].y, gb[u].y, acc);
+    acc = __builtin_fmaf(xb[u].z, gb[u].z, acc);
+    acc = __builtin_fmaf(xb[u].w, gb[u].w, acc);
+  }
+  return acc;
+}
+
+// Planning, by the last token block of the router (256 threads): expert
+// counts and offsets (the exclusive scan of layer.cu:737-760), each token
+// block's base within every expert, the units (tiles, or one per active
+// expert for the streaming plan), the expert kernel's task plan, and for the
+// streaming plan each slot's token (slot = block base + in-block rank).
+struct PlanShared {
+  int part[8][kExperts];
+  int off[kExperts + 1];
+  int cnt[kExperts];
+  int units;
+};
+
+// Exclusive prefix sum over lanes 0..31 of a wave (lanes >= 32 idle).
+__device__ __forceinline__ int lane_scan32(int v, int lane, int *total) {
+  int inc = v;
+#pragma unroll
+  for (int d = 1; d < 32; d <<= 1) {
+    const int u = __shfl_up(inc, d, 32);
+    if (lane >= d) inc += u;
+  }
+  *total = __shfl(inc, 31, 32);
+  return inc - v;
+}
+
+template <int RT>
+__device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) {
+  Ctrl *ctrl = a.s.ctrl;
+  const int tid = threadIdx.x;
+  const int e = tid & (kExperts - 1);
+  const int part = tid >> 5;  // 8 parts x 32 experts
+  const int per = (nb + 7) / 8;
+  const int lo = part * per;
+  const int hi = min(nb, lo + per);
+  {
+    int sum = 0;
+    for (int bb = lo; bb < hi; ++bb) sum += a.s.blk[bb * kExperts + e];
+    ps.part[part][e] = sum;
+  }
+  __syncthreads();
+  if (tid < kExperts) {
+    const int lane = tid;
+    int run = 0;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int v = ps.part[p][lane];
+      ps.part[p][lane] = run;
+      run += v;
+    }
+    const int cnt = run;
+    int total = 0, utotal = 0;
+    const int off = lane_scan32(cnt, lane, &total);
+    const int tr = a.tile_rows;
+    const int units_e = tr > 0 ? (cnt + tr - 1) / tr : (cnt > 0 ? 1 : 0);
+    const int uoff = lane_scan32(units_e, lane, &utotal);
+    const unsigned long long act = __ballot(cnt > 0);
+    const int nact = __popcll(act);
+    const int aidx = __popcll(act & ((1ull << lane) - 1ull));
+    ps.cnt[lane] = cnt;
+    ps.off[lane] = off;
+    ctrl->counts[lane] = cnt;
+    ctrl->offsets[lane] = off;
+    ctrl->unit_off[lane] = uoff;
+    if (cnt > 0) ctrl->active[aidx] = lane;
+    if (lane >= nact) ctrl->active[lane] = -1;
+    if (lane == 0) {
+      ps.off[kExperts] = total;
+      ctrl->offsets[kExperts] = total;
+      ctrl->unit_off[kExperts] = utotal;
+      ctrl->n_active = nact;
+      const int units = utotal;
+      const int p1u = tr > 0 ? a.inter / (a.bn / 2) : a.inter / (kStreamRows / 2);
+      const int p2u = tr > 0 ? a.H / a.bn : a.H / kStreamRows;
+      ctrl->p1_per_unit = p1u;
+      ctrl->p2_per_unit = p2u;
+      // The streaming plan (small T) gets its slots from this block below, so
+      // its expert kernel has no dispatch tasks to wait for.
+      const int ndisp = tr > 0 ? nb : 0;
+      ctrl->n_rblocks = ndisp;
+      ctrl->rtokens = RT;
+      ctrl->n_p1 = units * p1u;
+      ctrl->n_p2 = units * p2u;
+      ctrl->n_comb = (T + kCombineTokens - 1) / kCombineTokens;
+      ctrl->n_total = ndisp + units * p1u + units * p2u + ctrl->n_comb;
+      ctrl->num_tokens = T;
+      ctrl->tile_rows = tr;
+      ctrl->head = 0;
+      ctrl->assign_done = 0;
+      ctrl->p2_done = 0;
+      ps.units = units;
+    }
+  }
+  __syncthreads();
+  {
+    // block bases: offsets[e] + tokens of e in earlier token blocks
+    int base = ps.off[e] + ps.part[part][e];
+    for (int bb = lo; bb < hi; ++bb) {
+      const int c = a.s.blk[bb * kExperts + e];
+      a.s.blk[bb * kExperts + e] = base;
+      base += c;
+    }
+  }
+  const int units = min(ps.units, a.max_units);
+  for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
+  if (a.tile_rows == 0) {
+    for (int i = tid; i < kReadyLines; i += kThreads) {
+      a.s.ready[i * kReadyStride] = 0;
+      a.s.ready[i * kReadyStride + 1] = 0;
+    }
+    __syncthreads();  // the block bases above are read back below
+    // slot = token block base + in-block rank (stable by token), as the
+    // dispatch tasks of the tiled plans compute it
+    for (int f = tid; f < T * kTopK; f += kThreads) {
+      const int t = f / kTopK;
+      const int ee = a.s.idx[f];
+      int slot = -1;
+      if (ee >= 0 && ee < kExperts) {
+        slot = a.s.blk[(t / RT) * kExperts + ee] + a.s.pos[f];
+        if (slot >= 0 && slot < T * kTopK) a.s.slot_token[slot] = t;
+        else slot = -1;
+      }
+      a.s.pos[f] = slot;
+    }
+  }
+  if (tid == 0) ctrl->router_done = 0;  // every token block has counted in
+}
+
 // Router.  A block computes the gate logits of RT tokens x (32/ES) experts as
 // fp32 FMA chains over k ascending (the reference's per-output order,
 // layer.cu:109-127), staging x and gate through LDS in KC-wide k chunks with
@@ -139,8 +328,12 @@ template <int RT, int ES, int KC> struct RouterCfg {
   static_assert(KC % 4 == 0 && kThreads % (KC / 4) == 0, "chunk split");
 };
 
+// At most a few blocks per CU run (T/64 blocks), so the kernel is compiled for
+// instruction-level parallelism (all of a chunk's LDS reads in flight), not
+// occupancy.
 template <bool FROM_LOGITS, int RT, int ES, int KC>
-__global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void router_kernel(RouterArgs a) {
 #pragma clang fp contract(off)
   using C = RouterCfg<RT, ES, KC>;
   constexpr int EPB = C::EPB, TPL = C::TPL, PITCH = C::PITCH;
@@ -149,10 +342,8 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
   __shared__ float s_score[RT][kExperts + 1];
   __shared__ float s_prob[RT][kExperts + 1];
   __shared__ int s_cnt[kExperts];
-  __shared__ int s_part[8][kExperts];
-  __shared__ int s_off[kExperts + 1];
+  __shared__ PlanShared ps;
   __shared__ int s_flag;
-  __shared__ int s_units;
 
   const int tid = threadIdx.x;
   const int tb = blockIdx.x / ES, es = blockIdx.x % ES;
@@ -224,6 +415,7 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
       for (int j = 0; j < TPL; ++j) {
         const int tl = grp * TPL + j;
         if (t0 + tl < T) st_agent(&a.s.logits[(size_t)(t0 + tl) * kExperts + e0 + el], acc[j]);
+        if (ES == 1) s_prob[tl][el] = acc[j];  // the block has every expert: logits stay in LDS
       }
     }
   }
@@ -250,8 +442,12 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
     const int tok = t0 + tl;
     float l = 0.0f;
     if (tok < T) {
-      l = lsrc[(size_t)tok * kExperts + e];
-      if (FROM_LOGITS) a.s.logits[(size_t)tok * kExperts + e] = l;
+      if (!FROM_LOGITS && ES == 1) {
+        l = s_prob[tl][e];
+      } else {
+        l = lsrc[(size_t)tok * kExperts + e];
+        if (FROM_LOGITS) a.s.logits[(size_t)tok * kExperts + e] = l;
+      }
     }
     const float p = ref_sigmoid(l);
     s_prob[tl][e] = p;
@@ -335,108 +531,149 @@ __global__ __launch_bounds__(kThreads) void router_kernel(RouterArgs a) {
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
-    s_flag = (fetch_add(&ctrl->router_done, 1) == nb - 1);
+    // a single token block is the last one by construction
+    s_flag = nb == 1 || (fetch_add(&ctrl->router_done, 1) == nb - 1);
     if (s_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
   __syncthreads();
   if (!s_flag) return;
 
-  const int e = tid & (kExperts - 1);
-  const int part = tid >> 5;  // 8 parts x 32 experts
-  const int per = (nb + 7) / 8;
-  const int lo = part * per;
-  const int hi = min(nb, lo + per);
+  router_plan<RT>(a, nb, T, ps);
+}
+
+// Decode router (T <= 64).  A token block is 8 tokens; its 32 experts are
+// split over 8 blocks of 4, so 8x more CUs share the gate.  Each block copies
+// its 4 gate rows and the token rows whole into LDS with direct-to-LDS loads
+// (no chunk loop) and runs one FMA chain per (token, expert) lane (the
+// reference's order, layer.cu:109-127).  The last of a token block's blocks
+// finishes it with one thread per (token, expert): probability, score, and
+// the top-4 as a rank - the strict-'>' insertion of layer.cu:465-476 keeps an
+// expert exactly when fewer than 4 experts have a higher score or an equal
+// score and a lower index - then weights in rank order, in-block ranks and
+// counts.  The last token block plans.
+constexpr int kDecRT = 8, kDecEPB = 4, kDecES = kExperts / kDecEPB;
+
+__host__ __device__ constexpr size_t router_decode_lds(int H) {
+  return (size_t)(kDecEPB + kDecRT) * (size_t)(H + 4) * sizeof(float);
+}
+
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void router_decode_kernel(RouterArgs a) {
+#pragma clang fp contract(off)
+  extern __shared__ float lds[];  // gate rows [4][H + 4], then token rows [8][H + 4]
+  __shared__ float s_score[kDecRT][kExperts + 1];
+  __shared__ float s_prob[kDecRT][kExperts + 1];
+  __shared__ int s_sel[kDecRT][kExperts];  // rank in the token's top-4, or -1
+  __shared__ int s_ti[kDecRT][kTopK];
+  __shared__ float s_tp[kDecRT][kTopK];
+  __shared__ PlanShared ps;
+  __shared__ int s_flag;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int tb = blockIdx.x / kDecES, es = blockIdx.x % kDecES;
+  const int t0 = tb * kDecRT, e0 = es * kDecEPB;
+  const int T = a.T, H = a.H, P = H + 4;
+  const int nt = min(kDecRT, T - t0);
+  float *gs = lds, *xs = lds + kDecEPB * P;
+
+  // 1. gate rows e0..e0+3 and token rows t0..t0+nt-1, 1 KiB per load
   {
-    int sum = 0;
-    for (int bb = lo; bb < hi; ++bb) sum += a.s.blk[bb * kExperts + e];
-    s_part[part][e] = sum;
-  }
-  __syncthreads();
-  if (tid < kExperts) {
-    int run = 0;
-    for (int p = 0; p < 8; ++p) {
-      const int v = s_part[p][tid];
-      s_part[p][tid] = run;
-      run += v;
+    const int nch = H >> 8;
+    const int items = (kDecEPB + nt) * nch;
+    for (int i = wave; i < items; i += kThreads / 64) {
+      const int r = i / nch, c = i % nch;
+      const float *src = (r < kDecEPB ? a.w.gate + (size_t)(e0 + r) * H
+                                      : a.x + (size_t)(t0 + r - kDecEPB) * H) +
+                         c * 256 + lane * 4;
+      float *dst = (r < kDecEPB ? gs + r * P : xs + (r - kDecEPB) * P) + c * 256;
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
-    s_cnt[tid] = run;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
   }
+  // 2. chains: wave 0, lane = (token l / 4, expert l % 4)
+  if (wave == 0) {
+    const int tl = lane >> 2, el = lane & 3;
+    const float *gp = gs + el * P;
+    const float *xp = xs + min(tl, nt - 1) * P;
+    const float acc = chain_dot(gp, xp, H);
+    if (tl < nt) st_agent(&a.s.logits[(size_t)(t0 + tl) * kExperts + e0 + el], acc);
+  }
+  // 3. the last of the token block's 8 blocks finishes it
+  __builtin_amdgcn_s_waitcnt(0);  // this block's logits are stored
   __syncthreads();
-  if (tid == 0) {  // exclusive scan over experts (layer.cu:737-760)
-    int run = 0;
-    for (int ee = 0; ee < kExperts; ++ee) {
-      s_off[ee] = run;
-      run += s_cnt[ee];
-    }
-    s_off[kExperts] = run;
-  }
-  __syncthreads();
-  {
-    // block bases: offsets[e] + tokens of e in earlier token blocks
-    int base = s_off[e] + s_part[part][e];
-    for (int bb = lo; bb < hi; ++bb) {
-      const int c = a.s.blk[bb * kExperts + e];
-      a.s.blk[bb * kExperts + e] = base;
-      base += c;
-    }
-  }
-  if (tid < kExperts) ctrl->counts[tid] = s_cnt[tid];
-  if (tid <= kExperts) ctrl->offsets[tid] = s_off[tid];
   if (tid == 0) {
-    const int tr = a.tile_rows;
-    int units = 0, nact = 0;
-    for (int ee = 0; ee < kExperts; ++ee) {
-      ctrl->unit_off[ee] = units;
-      const int c = s_cnt[ee];
-      if (c > 0) ctrl->active[nact++] = ee;
-      units += tr > 0 ? (c + tr - 1) / tr : (c > 0 ? 1 : 0);
+    s_flag = fetch_add(&a.s.tb_done[tb], 1) == kDecES - 1;
+    if (s_flag) {
+      a.s.tb_done[tb] = 0;  // all blocks counted in: reset
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
-    ctrl->unit_off[kExperts] = units;
-    for (int i = nact; i < kExperts; ++i) ctrl->active[i] = -1;
-    ctrl->n_active = nact;
-    const int p1u = tr > 0 ? a.inter / (a.bn / 2) : a.inter / (kStreamRows / 2);
-    const int p2u = tr > 0 ? a.H / a.bn : a.H / kStreamRows;
-    ctrl->p1_per_unit = p1u;
-    ctrl->p2_per_unit = p2u;
-    // The streaming plan (small T) gets its slots from this block below, so
-    // its expert kernel has no dispatch tasks to wait for.
-    const int ndisp = tr > 0 ? nb : 0;
-    ctrl->n_rblocks = ndisp;
-    ctrl->rtokens = RT;
-    ctrl->n_p1 = units * p1u;
-    ctrl->n_p2 = units * p2u;
-    ctrl->n_comb = (T + kCombineTokens - 1) / kCombineTokens;
-    ctrl->n_total = ndisp + units * p1u + units * p2u + ctrl->n_comb;
-    ctrl->num_tokens = T;
-    ctrl->tile_rows = tr;
-    ctrl->head = 0;
-    ctrl->assign_done = 0;
-    ctrl->p2_done = 0;
-    s_units = units;
   }
   __syncthreads();
-  const int units = min(s_units, a.max_units);
-  for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
-  if (a.tile_rows == 0) {
-    for (int i = tid; i < kReadyLines; i += kThreads) {
-      a.s.ready[i * kReadyStride] = 0;
-      a.s.ready[i * kReadyStride + 1] = 0;
+  if (!s_flag) return;
+  // 4. thread = (token tl, expert e): probability and score
+  const int tl = tid >> 5, e = tid & (kExperts - 1);
+  const int tok = t0 + tl;
+  const bool tvalid = tl < nt;
+  {
+    const float l = tvalid ? a.s.logits[(size_t)tok * kExperts + e] : 0.0f;
+    const float p = ref_sigmoid(l);
+    s_prob[tl][e] = p;
+    s_score[tl][e] = p + (a.w.bias ? a.w.bias[e] : 0.0f);  // layer.cu:462
+  }
+  __syncthreads();
+  // 5. rank of e in the token's order (score descending, lower index first)
+  int sel = -1;
+  {
+    const float sc = s_score[tl][e];
+    int r = 0;
+#pragma unroll
+    for (int j = 0; j < kExperts; ++j) {
+      const float sj = s_score[tl][j];
+      r += (sj > sc) || (sj == sc && j < e);
     }
-    // slot = token block base + in-block rank (stable by token), as the
-    // dispatch tasks of the tiled plans compute it
-    for (int f = tid; f < T * kTopK; f += kThreads) {
-      const int t = f / kTopK;
-      const int ee = a.s.idx[f];
-      int slot = -1;
-      if (ee >= 0 && ee < kExperts) {
-        slot = a.s.blk[(t / RT) * kExperts + ee] + a.s.pos[f];
-        if (slot >= 0 && slot < T * kTopK) a.s.slot_token[slot] = t;
-        else slot = -1;
-      }
-      a.s.pos[f] = slot;
+    if (tvalid && r < kTopK) sel = r;
+    s_sel[tl][e] = sel;
+    if (sel >= 0) {
+      s_ti[tl][sel] = e;
+      s_tp[tl][sel] = s_prob[tl][e];
     }
   }
-  if (tid == 0) ctrl->router_done = 0;  // every token block has counted in
+  __syncthreads();
+  // 6. weights: sum in rank order (layer.cu:480-489)
+  if (tid < nt) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i) sum += s_tp[tid][i];
+    const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i) {
+      st_agent(&a.s.idx[(size_t)(t0 + tid) * kTopK + i], s_ti[tid][i]);
+      a.s.wts[(size_t)(t0 + tid) * kTopK + i] = s_tp[tid][i] * scale * 1.0f;
+    }
+  }
+  // 7. in-block rank among the block's tokens that chose e, and counts
+  if (sel >= 0) {
+    int c = 0;
+    for (int t2 = 0; t2 < tl; ++t2) c += s_sel[t2][e] >= 0;
+    st_agent(&a.s.pos[(size_t)tok * kTopK + sel], c);
+  }
+  if (tl == 0) {
+    int c = 0;
+    for (int t2 = 0; t2 < nt; ++t2) c += s_sel[t2][e] >= 0;
+    st_agent(&a.s.blk[tb * kExperts + e], c);
+  }
+  // 8. the token block that finishes last plans
+  const int nb = gridDim.x / kDecES;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    s_flag = nb == 1 || (fetch_add(&a.s.ctrl->router_done, 1) == nb - 1);
+    if (s_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  if (!s_flag) return;
+  router_plan<kDecRT>(a, nb, T, ps);
 }
 
 // ---------------------------------------------------------------------------
@@ -1678,16 +1915,27 @@ __global__ void pack_w13_kernel(float4 *dst, const float4 *w1, const float4 *w3,
 // Launchers
 // ---------------------------------------------------------------------------
 
-// Router shapes: decode (T <= 64) spreads the gate over 4 expert splits of 8
-// tokens so more CUs share it and each lane runs one chain; larger T uses
-// 64-token blocks with all 32 experts and 8 chains per lane.
-constexpr int kSmallRT = 8, kSmallES = 4, kSmallKC = 256;
+// Router shapes: decode (T <= 64) uses 8-token blocks with all 32 experts, so
+// each of the 256 lanes runs one chain and a token block needs no hand-off
+// between blocks; larger T uses 64-token blocks and 8 chains per lane.
+constexpr int kSmallRT = 8, kSmallES = 1, kSmallKC = 256;
 constexpr int kLargeRT = 64, kLargeES = 1, kLargeKC = 64;
 
 int router_tokens_per_block(int T) { return T <= 64 ? kSmallRT : kLargeRT; }
 
 hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) {
   const bool small = a.T <= 64;
+  if (small && !from_logits) {
+    const size_t lds = router_decode_lds(a.H);
+    if (lds > 65536) {
+      const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&router_decode_kernel),
+                                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return e;
+    }
+    const int nb = (a.T + kDecRT - 1) / kDecRT;
+    hipLaunchKernelGGL(router_decode_kernel, dim3(nb * kDecES), dim3(kThreads), lds, st, a);
+    return hipGetLastError();
+  }
   const int rt = small ? kSmallRT : kLargeRT;
   const int nb = (a.T + rt - 1) / rt;
   if (from_logits) {
@@ -1696,9 +1944,6 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
       hipLaunchKernelGGL((router_kernel<true, kSmallRT, 1, kSmallKC>), dim3(nb), dim3(kThreads), 0, st, a);
     else
       hipLaunchKernelGGL((router_kernel<true, kLargeRT, 1, kLargeKC>), dim3(nb), dim3(kThreads), 0, st, a);
-  } else if (small) {
-    hipLaunchKernelGGL((router_kernel<false, kSmallRT, kSmallES, kSmallKC>), dim3(nb * kSmallES),
-                       dim3(kThreads), 0, st, a);
   } else {
     hipLaunchKernelGGL((router_kernel<false, kLargeRT, kLargeES, kLargeKC>), dim3(nb * kLargeES),
                        dim3(kThreads), 0, st, a);
