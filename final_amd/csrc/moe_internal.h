@@ -13,9 +13,7 @@ constexpr int kTopK = 4;         // NUM_EXPERTS_PER_TOK, config.h:15
 constexpr int kMinRouterTokens = 8;  // smallest token block of the router
 constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
 constexpr int kCombineTokens = 8;  // tokens per combine task
-constexpr int kStreamRowsPerWave = 4;   // weight rows per wave, streaming kernel
-constexpr int kStreamRows = kStreamRowsPerWave * 4;  // rows per streaming task
-constexpr int kStreamTokens = 8;  // token rows per streaming pass (LDS staged)
+constexpr int kStreamRows = 16;  // weight rows per streaming-plan task
 // Streaming-plan blocks each get a private 128-byte line of ready bits (word
 // 0: units whose gate/up tasks are done, word 1: all down tasks done).
 constexpr int kReadyLines = 1024;

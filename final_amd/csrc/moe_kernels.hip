@@ -1,24 +1,27 @@
 // HIP kernels of the MI355X (gfx950) sparse-MoE block.
 //
 // Two launches per forward:
-//   1. router_kernel   -- gate GEMM as fp32 FMA chains (bit-exact with the
-//      reference's attn_matmul_tiled_kernel, layer.cu:9-141), sigmoid with a
-//      double exp, top-4 insertion (layer.cu:439-499), per-block expert
-//      histogram and in-block ranks by wavefront ballots; the last block to
-//      finish scans the histograms and writes the expert kernel's task plan.
-//   2. expert kernel   -- persistent, one dynamic task queue with four phases:
-//      dispatch (slot assignment, replaces moe_scatter_kernel layer.cu:501-542
-//      without copying x), gate/up projection with SwiGLU epilogue
-//      (layer.cu:773-972), down projection (layer.cu:974-1126) and the weighted
-//      top-4 combine with the residual add (layer.cu:695-721, 1860-1880).
-//      Large T uses MFMA 32x32x2 f32 tiles (expert_mfma_kernel); small T streams
-//      weights through VALU dot products (expert_stream_kernel).
+//   1. router -- gate GEMM as fp32 FMA chains (bit-exact with the reference's
+//      attn_matmul_tiled_kernel, layer.cu:9-141), sigmoid with a double exp,
+//      top-4 (layer.cu:439-499), per-token-block expert histogram and in-block
+//      ranks; the last token block scans the histograms and writes the expert
+//      kernel's task plan.  router_decode_kernel serves T <= 64 (expert-split
+//      blocks, whole rows staged in LDS), router_kernel larger T (64-token
+//      blocks) and routing from given logits.
+//   2. expert kernel -- persistent, gate/up projection with the SwiGLU
+//      epilogue (layer.cu:773-972), down projection (layer.cu:974-1126) and
+//      the weighted top-4 combine with the residual add (layer.cu:695-721,
+//      1860-1880).  Large T: expert_mfma_kernel, MFMA 32x32x2 f32 tiles with
+//      a dispatch phase that assigns slots (replaces moe_scatter_kernel,
+//      layer.cu:501-542, without copying x), one dynamic task queue.  Small T:
+//      expert_ring_kernel, weight streaming through MFMA 16x16x4 f32 with
+//      round-robin tasks and slots assigned by the router.
 //
-// Phase dependencies are counters in the control block.  Tasks are taken in
-// increasing order from one atomic head and a task only waits on tasks with a
-// smaller index, so the smallest unfinished task is always running and every
-// wait ends; each wait is still bounded and reports MOE_ERR_DEVICE_TIMEOUT
-// instead of spinning forever.
+// Phase dependencies are counters in the control block.  A task only waits
+// on tasks with a smaller index and every block runs its tasks in increasing
+// order, so the smallest unfinished task is always running and every wait
+// ends; each wait is still bounded and reports MOE_ERR_DEVICE_TIMEOUT instead
+// of spinning forever.
 #include "moe_internal.h"
 
 namespace moe {
@@ -1017,284 +1020,6 @@ void expert_mfma_kernel(ExpertArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Weight-streaming kernel (small T).  Every weight byte is read once: a wave
-// owns 4 weight rows and loads each as 1 KiB coalesced float4 wave loads, all
-// issued up front and kept in registers while up to kStreamTokens token rows
-// at a time are staged in LDS and dotted against them on VALU.  The 64 lanes'
-// partial sums are combined by a butterfly transpose-reduction.
-// ---------------------------------------------------------------------------
-
-// Butterfly transpose-reduction of V values over the 64 lanes of a wave,
-// stopping when KEEP values remain per lane.  Afterwards every value is the
-// sum over all 64 lanes; lane l holds the group of KEEP consecutive values
-// starting at index KEEP * (l >> (6 - log2(V / KEEP))).
-template <int V, int KEEP>
-__device__ __forceinline__ void wave_transpose_sum(float (&v)[V]) {
-  const int lane = threadIdx.x & 63;
-  int off = 32;
-#pragma unroll
-  for (int L = V; L > KEEP; L >>= 1, off >>= 1) {
-    const bool hi = (lane & off) != 0;
-#pragma unroll
-    for (int j = 0; j < L / 2; ++j) {
-      float lo_v = v[j], hi_v = v[L / 2 + j];
-      // keep both halves as register values: a select between two array
-      // elements would otherwise become a dynamically indexed (scratch) load
-      asm volatile("" : "+v"(lo_v), "+v"(hi_v));
-      const float send = hi ? lo_v : hi_v;
-      const float keep = hi ? hi_v : lo_v;
-      v[j] = keep + __shfl_xor(send, off, 64);
-    }
-  }
-#pragma unroll
-  for (; off > 0; off >>= 1)
-#pragma unroll
-    for (int j = 0; j < KEEP; ++j) v[j] += __shfl_xor(v[j], off, 64);
-}
-
-constexpr int log2i(int v) { return v <= 1 ? 0 : 1 + log2i(v / 2); }
-
-// Stage MT rows (length KCH*256, row m at base + off[m], off < 0 = zeros).
-// Loads are issued in batches of at most 4 float4 per thread so staging does
-// not compete for registers with the weight rows held across tasks.
-template <int MT, int KCH>
-__device__ __forceinline__ void stage_tokens(float *xs, const float *base, const int *off) {
-  constexpr int K4 = KCH * 64;
-  constexpr int N = MT * K4;
-  constexpr int PER = (N + kThreads - 1) / kThreads;
-  constexpr int BATCH = PER < 4 ? PER : 4;
-  const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int i0 = 0; i0 < PER; i0 += BATCH) {
-    f32x4 v[BATCH];
-#pragma unroll
-    for (int b = 0; b < BATCH; ++b) {
-      const int f = threadIdx.x + (i0 + b) * kThreads;
-      const int m = f / K4, c4 = f % K4;
-      const int o = (i0 + b < PER && (N % kThreads == 0 || f < N)) ? off[m] : -1;
-      v[b] = o >= 0 ? ld4(base + o + c4 * 4) : zero;
-    }
-#pragma unroll
-    for (int b = 0; b < BATCH; ++b) {
-      const int f = threadIdx.x + (i0 + b) * kThreads;
-      if (i0 + b < PER && (N % kThreads == 0 || f < N)) st4(xs + f * 4, v[b]);
-    }
-  }
-}
-
-constexpr int kStreamMaxChunks = 8;  // weight row length <= 2048 floats
-
-// acc[r][m] = wv[r] . xs[m] over KCH chunks (this lane's float4 of each).
-template <int MT, int KCH>
-__device__ __forceinline__ void stream_dots(const f32x4 (&wv)[kStreamRowsPerWave][kStreamMaxChunks],
-                                            const float *xs,
-                                            float (&acc)[kStreamRowsPerWave][MT]) {
-  constexpr int K = KCH * 256;
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int r = 0; r < kStreamRowsPerWave; ++r)
-#pragma unroll
-    for (int m = 0; m < MT; ++m) acc[r][m] = 0.0f;
-#pragma unroll
-  for (int c = 0; c < KCH; ++c) {
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-      const f32x4 xv = ld4(xs + m * K + c * 256 + lane * 4);
-#pragma unroll
-      for (int r = 0; r < kStreamRowsPerWave; ++r)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) acc[r][m] = __builtin_fmaf(wv[r][c][q], xv[q], acc[r][m]);
-    }
-  }
-}
-
-// A streaming-kernel task decoded: kind 0 dispatch, 1 gate/up rows, 2 down
-// rows, 3 combine, 4 none (past the end).  rows[] are this wave's 4 rows.
-struct StreamTask {
-  int kind, q, u, e, cnt, slot0, col;
-};
-
-__device__ __forceinline__ StreamTask stream_decode(const Ctrl *c, int task, int nb, int n1,
-                                                   int n2, int ntot, int p1u, int p2u,
-                                                   int wave) {
-  StreamTask t{4, 0, 0, 0, 0, 0, 0};
-  if (task >= ntot) return t;
-  if (task < nb) {
-    t.kind = 0;
-    t.q = task;
-  } else if (task < nb + n1) {
-    t.kind = 1;
-    t.q = task - nb;
-    t.u = t.q / p1u;
-    t.col = (t.q % p1u) * (kStreamRows / 2) + wave * 2;  // this wave's first n
-  } else if (task < nb + n1 + n2) {
-    t.kind = 2;
-    t.q = task - nb - n1;
-    t.u = t.q / p2u;
-    t.col = (t.q % p2u) * kStreamRows + wave * kStreamRowsPerWave;  // first h
-  } else {
-    t.kind = 3;
-    t.q = task - nb - n1 - n2;
-  }
-  if (t.kind == 1 || t.kind == 2) {
-    t.e = c->active[t.u];
-    t.cnt = c->counts[t.e];
-    t.slot0 = c->offsets[t.e];
-  }
-  return t;
-}
-
-// Issues the weight loads of a streaming task into wv (all chunks in flight),
-// unconditionally: tasks without weight rows (dispatch, combine, none) load
-// the first rows of W1/W3 as a harmless stand-in, so wv has one definition per
-// pass and stays in registers.  Gate/up: W1 rows n, n+1 and W3 rows n, n+1 of
-// the packed layout; down: W2 rows h .. h+3 (a row's last chunk is re-read
-// where I has fewer chunks than kStreamMaxChunks).
-template <int KCH1, int KCH2>
-__device__ __forceinline__ void stream_issue(const ExpertArgs &a, const StreamTask &t,
-                                             f32x4 (&wv)[kStreamRowsPerWave][kStreamMaxChunks]) {
-  const int lane = threadIdx.x & 63;
-  const int H = a.H, I = a.I;
-  const bool down = t.kind == 2;
-  const size_t pa = (size_t)(t.col >> 5) * 64 + (t.col & 31);  // packed row of W1 n
-  const float *w13 = a.w.w13 + (size_t)t.e * 2 * I * H;
-  const float *w2 = a.w.w2 + ((size_t)t.e * H + t.col) * I;
-  const bool rows13 = t.kind == 1;
-  const float *r0 = down ? w2 : (rows13 ? w13 + pa * H : a.w.w13);
-  const size_t step1 = down ? I : (rows13 ? H : H);        // row 1 - row 0
-  const size_t step2 = down ? 2 * (size_t)I : (rows13 ? 32 * (size_t)H : 2 * (size_t)H);
-  const size_t step3 = down ? 3 * (size_t)I : (rows13 ? 33 * (size_t)H : 3 * (size_t)H);
-  const int nch = down ? KCH2 : KCH1;
-  const float *rows[kStreamRowsPerWave] = {r0, r0 + step1, r0 + step2, r0 + step3};
-#pragma unroll
-  for (int c = 0; c < kStreamMaxChunks; ++c) {
-    const int cc = c < nch ? c : nch - 1;
-#pragma unroll
-    for (int r = 0; r < kStreamRowsPerWave; ++r) wv[r][c] = ld4(rows[r] + cc * 256 + lane * 4);
-  }
-}
-
-// Output half of a pass: reduce the lane partials of the wave's 4 rows x MT
-// tokens, gather the block's outputs in LDS, and write them as 16-byte stores
-// (8 floats per token for gate/up, 16 for down, contiguous in the row).
-template <int MT, bool GATED>
-__device__ __forceinline__ void stream_out(const ExpertArgs &a, const StreamTask &t, int m0,
-                                           int nt, float (&acc)[kStreamRowsPerWave][MT],
-                                           float (*s_res)[kStreamRows], const AgentOut &out) {
-  constexpr int R = kStreamRowsPerWave;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (GATED) {
-    // value (j*MT + m)*2 + w: j = which n, w = 0 W1 / 1 W3 (row w*2 + j)
-    float v[4 * MT];
-#pragma unroll
-    for (int j = 0; j < 2; ++j)
-#pragma unroll
-      for (int m = 0; m < MT; ++m)
-#pragma unroll
-        for (int w = 0; w < 2; ++w) v[(j * MT + m) * 2 + w] = acc[w * 2 + j][m];
-    wave_transpose_sum<4 * MT, 2>(v);
-    constexpr int SH = 6 - log2i(2 * MT);
-    const int p = lane >> SH;  // pair index j*MT + m
-    if ((lane & ((1 << SH) - 1)) == 0) s_res[p % MT][wave * 2 + p / MT] = silu(v[0]) * v[1];
-  } else {
-    float v[R * MT];  // value r*MT + m
-#pragma unroll
-    for (int r = 0; r < R; ++r)
-#pragma unroll
-      for (int m = 0; m < MT; ++m) v[r * MT + m] = acc[r][m];
-    wave_transpose_sum<R * MT, 1>(v);
-    constexpr int SH = 6 - log2i(R * MT);
-    const int i = lane >> SH;
-    if ((lane & ((1 << SH) - 1)) == 0) s_res[i % MT][wave * R + i / MT] = v[0];
-  }
-  __syncthreads();
-  constexpr int F4 = GATED ? 2 : 4;
-  if (tid < nt * F4) {
-    const int mm = tid / F4, q4 = tid % F4;
-    const int col0 = t.col - wave * (GATED ? 2 : R);
-    const int ld = GATED ? a.I : a.H;
-    out.store((uint32_t)(((size_t)(t.slot0 + m0 + mm) * ld + col0 + q4 * 4) * sizeof(float)),
-              ld4(&s_res[mm][q4 * 4]));
-  }
-  __syncthreads();
-}
-
-// KCH1 = H / 256 (gate/up rows), KCH2 = I / 256 (down rows), MT = token rows
-// per pass (LDS-staged; 2 for the smallest batches, else 8).  Every pass
-// issues the weight rows of what comes next (the next task after a task's last
-// pass, the same rows again otherwise) right after its dot products, so HBM
-// streams while the pass reduces, stores and signals, and a down task's
-// weights are already in flight while it waits for its expert's gate/up tasks.
-template <int KCH1, int KCH2, int MT>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void expert_stream_kernel(ExpertArgs a) {
-  static_assert(KCH1 <= kStreamMaxChunks && KCH2 <= kStreamMaxChunks, "row length");
-  constexpr int R = kStreamRowsPerWave;
-  extern __shared__ float xs[];  // [MT][max(H, I)]
-  __shared__ int s_task, s_next;
-  __shared__ int s_off[MT];
-  __shared__ float s_res[MT][kStreamRows];
-  Ctrl *c = a.s.ctrl;
-  const int tid = threadIdx.x, wave = tid >> 6;
-  const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
-  const int p1u = c->p1_per_unit, p2u = c->p2_per_unit, rt = c->rtokens;
-  const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
-  if (tid == 0) {
-    s_task = claim(&c->head);
-    s_next = claim(&c->head);
-  }
-  __syncthreads();
-  int task = s_task;
-  StreamTask cur = stream_decode(c, task, nb, n1, n2, ntot, p1u, p2u, wave);
-  f32x4 wv[R][kStreamMaxChunks];
-  stream_issue<KCH1, KCH2>(a, cur, wv);
-  while (task < ntot) {
-    const int next = s_next;
-    const StreamTask nxt = stream_decode(c, next, nb, n1, n2, ntot, p1u, p2u, wave);
-    const bool rows = cur.kind == 1 || cur.kind == 2;
-    if (cur.kind == 1 && nb > 0) block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
-    if (cur.kind == 2) block_wait(&a.s.dep[cur.u], p1u, a.wait_limit, &c->err);
-    const int npass = rows ? (cur.cnt + MT - 1) / MT : 1;
-    for (int ps = 0; ps < npass; ++ps) {
-      const int m0 = ps * MT;
-      const int nt = rows ? min(MT, cur.cnt - m0) : 0;
-      float acc[R][MT];
-      if (rows) {
-        if (tid < MT)
-          s_off[tid] = tid < nt ? (cur.kind == 1 ? slot_tok(a, cur.slot0 + m0 + tid) * a.H
-                                                 : (cur.slot0 + m0 + tid) * a.I)
-                                : -1;
-        __syncthreads();
-        if (cur.kind == 1) stage_tokens<MT, KCH1>(xs, a.x, s_off);
-        else stage_tokens<MT, KCH2>(xs, a.s.inter, s_off);
-        __syncthreads();
-        if (cur.kind == 1) stream_dots<MT, KCH1>(wv, xs, acc);
-        else stream_dots<MT, KCH2>(wv, xs, acc);
-      }
-      stream_issue<KCH1, KCH2>(a, ps + 1 < npass ? cur : nxt, wv);  // wv is dead: refill
-      if (cur.kind == 1) stream_out<MT, true>(a, cur, m0, nt, acc, s_res, inter_out);
-      else if (cur.kind == 2) stream_out<MT, false>(a, cur, m0, nt, acc, s_res, sout_out);
-    }
-    if (cur.kind == 0) {
-      assign_task(a, cur.q, rt);
-      block_signal(&c->assign_done);
-    } else if (cur.kind == 1) {
-      block_signal(&a.s.dep[cur.u]);
-    } else if (cur.kind == 2) {
-      block_signal(&c->p2_done);
-    } else {
-      block_wait(&c->p2_done, n2, a.wait_limit, &c->err);
-      combine_task(a, cur.q);
-    }
-    __syncthreads();  // every thread has read s_next
-    if (tid == 0) s_next = claim(&c->head);
-    task = next;
-    cur = nxt;
-    __syncthreads();
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Weight-streaming kernel for small T (expert_ring_kernel).
 //
 // HBM saturates with ~32 KiB of loads in flight per CU, and every round trip
@@ -1918,7 +1643,7 @@ __global__ void pack_w13_kernel(float4 *dst, const float4 *w1, const float4 *w3,
 // Router shapes: decode (T <= 64) uses 8-token blocks with all 32 experts, so
 // each of the 256 lanes runs one chain and a token block needs no hand-off
 // between blocks; larger T uses 64-token blocks and 8 chains per lane.
-constexpr int kSmallRT = 8, kSmallES = 1, kSmallKC = 256;
+constexpr int kSmallRT = kDecRT, kSmallKC = 256;
 constexpr int kLargeRT = 64, kLargeES = 1, kLargeKC = 64;
 
 int router_tokens_per_block(int T) { return T <= 64 ? kSmallRT : kLargeRT; }
