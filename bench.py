@@ -166,7 +166,7 @@ def main():
             tr = json.load(f).get(wl.name)
         if tr:
             roof["traffic"] = tr.get("bytes_per_launch")
-    roof["kernel"] = "expert_mfma_kernel<%d>" % plan if mfma_bound else "expert_stream_kernel"
+    roof["kernel"] = "expert_mfma_kernel<%d>" % plan if mfma_bound else "expert_ring_kernel"
     roof["kernel_ms"] = round(exp_avg, 4)
     roof["router_ms"] = round(route_avg, 4)
     roof["per_launch"] = ({"flop": expert_flops} if mfma_bound else {"bytes": expert_bytes})
