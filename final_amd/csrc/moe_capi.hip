@@ -315,7 +315,7 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   a.H = ctx->d.hidden;
   a.inter = ctx->d.inter;
   a.tile_rows = ctx_plan(ctx, T);
-  a.bn = expert_bn(a.tile_rows);
+  a.bn = expert_bn(a.tile_rows, T);
   a.max_units = ctx->max_units;
   if (launch_router(a, logits != nullptr, static_cast<hipStream_t>(stream)) != hipSuccess)
     return MOE_ERR_HIP;

@@ -13,7 +13,8 @@ constexpr int kTopK = 4;         // NUM_EXPERTS_PER_TOK, config.h:15
 constexpr int kMinRouterTokens = 8;  // smallest token block of the router
 constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
 constexpr int kCombineTokens = 8;  // tokens per combine task
-constexpr int kStreamRows = 16;  // weight rows per streaming-plan task
+constexpr int kStreamRows = 16;  // weight rows per streaming-plan task (small batches)
+constexpr int kStreamWideTokens = 32;  // batches from this size use 64-row tasks
 // Streaming-plan blocks each get a private 128-byte line of ready bits (word
 // 0: units whose gate/up tasks are done, word 1: all down tasks done).
 constexpr int kReadyLines = 1024;
@@ -39,6 +40,7 @@ struct Ctrl {
   int p2_per_unit;
   int n_active;     // experts with count > 0
   int rtokens;      // tokens per router block (dispatch task size)
+  int stream_rows;  // streaming plan: weight rows per task (16 or 64)
   int counts[kExperts];
   int offsets[kExperts + 1];
   int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)
@@ -106,7 +108,8 @@ bool stream_supported(int H, int I);
 int stream_max_tokens();
 // Max resident blocks per CU of the expert kernel for a plan.
 int expert_blocks_per_cu(int tile_rows);
-// Columns of the B tile of the MFMA kernel for a plan.
-int expert_bn(int tile_rows);
+// Columns of the B tile of the MFMA kernel, or weight rows per task of the
+// streaming kernel, for a plan and batch size.
+int expert_bn(int tile_rows, int T);
 
 }  // namespace moe

@@ -253,8 +253,10 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
       ctrl->unit_off[kExperts] = utotal;
       ctrl->n_active = nact;
       const int units = utotal;
-      const int p1u = tr > 0 ? a.inter / (a.bn / 2) : a.inter / (kStreamRows / 2);
-      const int p2u = tr > 0 ? a.H / a.bn : a.H / kStreamRows;
+      // a.bn: columns of an MFMA tile, or weight rows of a streaming task
+      const int p1u = a.inter / (a.bn / 2);
+      const int p2u = a.H / a.bn;
+      ctrl->stream_rows = tr > 0 ? 0 : a.bn;
       ctrl->p1_per_unit = p1u;
       ctrl->p2_per_unit = p2u;
       // The streaming plan (small T) gets its slots from this block below, so
@@ -1036,11 +1038,19 @@ void expert_mfma_kernel(ExpertArgs a) {
 // counters, sums the eight k-slice partials a task leaves in LDS, stores the
 // results (SwiGLU applied for gate/up), and signals.
 //
-// Tasks are dealt round-robin (block b runs tasks b, b + G, ...; G = grid) in
-// the plan's order: gate/up row blocks expert by expert, then down row
-// blocks, then the combine.  A task waits only on tasks of smaller index and
-// each block runs its tasks in increasing order, so the smallest unfinished
-// task always runs.
+// Row tasks follow the plan's order: gate/up row blocks expert by expert,
+// then down row blocks.  Block b starts with task b; every later task comes
+// from a queue counter (G + the counter's old value, G = grid), claimed by
+// streaming wave 0 at the first step of the block's current task, so a
+// block that draws cheap tasks takes more of them.  Only down tasks wait
+// (for every gate/up task of their unit), and a gate/up task never waits:
+// while a block runs a gate/up task, its waves do not wait for the inputs of
+// a down task that comes next (those may include the running task, or a
+// gate/up task of a block that is itself waiting); they finish the task
+// first and then wait and refill the ring.  So every gate/up task finishes,
+// and then every down task.  The combine tasks (one per token), which wait
+// for every down task, are dealt round-robin (block b runs tokens b, b + G,
+// ...) after the row tasks.
 // ---------------------------------------------------------------------------
 
 constexpr int kRingWaves = 8;                       // k-slice streaming waves
@@ -1052,6 +1062,9 @@ constexpr int kRingSlice = kRingSteps * 16;         // floats of k per wave (256
 constexpr int kRingMaxSlots = 4096;                 // slot -> token map kept in LDS
 static_assert(kRingWaves * kRingSlice == 2048, "k slices cover rows of <= 2048 floats");
 static_assert(kRingSteps % kRingDepth == 0, "ring rotation realigns at task boundaries");
+// 64-row tasks load 4 weight rows per step: half the depth keeps the bytes in
+// flight per CU about the same and the ring within the register budget.
+constexpr int ring_depth(int rg) { return rg == 1 ? kRingDepth : kRingDepth / 2; }
 
 struct RingShared {
   int active[kExperts], counts[kExperts], offsets[kExperts];
@@ -1061,6 +1074,8 @@ struct RingShared {
   int flushed;             // items whose partials the control wave has consumed
   int done[2];             // streaming waves that wrote item i's partials into buffer i & 1
   int abort;
+  int seq[8];              // the block's j-th row task id at seq[j & 7]
+  int nseq;                // row task ids published so far
 };
 
 __device__ __forceinline__ int lds_load(const int *p) {
@@ -1108,42 +1123,43 @@ __device__ __forceinline__ bool ring_wait(const int *p, Cond cond, int *abort_fl
 }
 
 struct RingPlan {
-  int n1, n2, ntot, p1u, p2u, grid;
+  int n1, n2, ncomb, p1u, p2u, grid, rows;
 };
 
-// A task of the block's sequence, wave-uniform.  kind: 1 gate/up rows, 2
-// down rows, 3 combine, 4 past the end.  A row task runs in groups of up to
-// 16 * P tokens (one pass of the ring per group).
+// A row task, wave-uniform.  kind: 1 gate/up rows, 2 down rows, 4 none (the
+// queue ran out).  A row task runs in groups of up to 16 * P tokens (one
+// pass of the ring per group).
 struct RingTask {
   int kind, q, u, e, cnt, slot0, col, ngroups;
 };
 
 template <int P>
-__device__ __forceinline__ RingTask ring_task(const RingShared &sh, const RingPlan &pl, int j) {
-  const int task = (int)blockIdx.x + j * pl.grid;
+__device__ __forceinline__ RingTask ring_task(const RingShared &sh, const RingPlan &pl, int task) {
+  task = __builtin_amdgcn_readfirstlane(task);
   RingTask t{4, 0, 0, 0, 0, 0, 0, 1};
-  if (task >= pl.ntot) return t;
+  if (task < 0 || task >= pl.n1 + pl.n2) return t;
   if (task < pl.n1) {
     t.kind = 1;
     t.q = task;
     t.u = task / pl.p1u;
-    t.col = (task % pl.p1u) * (kStreamRows / 2);
-  } else if (task < pl.n1 + pl.n2) {
+    t.col = (task % pl.p1u) * (pl.rows / 2);
+  } else {
     t.kind = 2;
     t.q = task - pl.n1;
     t.u = t.q / pl.p2u;
-    t.col = (t.q % pl.p2u) * kStreamRows;
-  } else {
-    t.kind = 3;
-    t.q = task - pl.n1 - pl.n2;
+    t.col = (t.q % pl.p2u) * pl.rows;
   }
-  if (t.kind != 3) {
-    t.e = __builtin_amdgcn_readfirstlane(sh.active[t.u]);
-    t.cnt = __builtin_amdgcn_readfirstlane(sh.counts[t.e]);
-    t.slot0 = __builtin_amdgcn_readfirstlane(sh.offsets[t.e]);
-    t.ngroups = t.cnt > 0 ? (t.cnt + kRingTokens * P - 1) / (kRingTokens * P) : 1;
-  }
+  t.e = __builtin_amdgcn_readfirstlane(sh.active[t.u]);
+  t.cnt = __builtin_amdgcn_readfirstlane(sh.counts[t.e]);
+  t.slot0 = __builtin_amdgcn_readfirstlane(sh.offsets[t.e]);
+  t.ngroups = t.cnt > 0 ? (t.cnt + kRingTokens * P - 1) / (kRingTokens * P) : 1;
   return t;
+}
+
+// The block's j-th row task; its id is published before any wave reads it.
+template <int P>
+__device__ __forceinline__ RingTask ring_seq_task(const RingShared &sh, const RingPlan &pl, int j) {
+  return ring_task<P>(sh, pl, lds_load(&sh.seq[j & 7]));
 }
 
 // Buffer descriptors: weights, token rows, intermediate rows, and an empty
@@ -1167,26 +1183,28 @@ __device__ __forceinline__ RingRsrc ring_rsrc(const ExpertArgs &a) {
 
 constexpr uint32_t kRingOff = 0xFFFF0000u;  // lane offset past any buffer: loads read 0
 
-// What one streaming lane loads for a group of a task: the weight row byte
-// offset (with this wave's k slice) and a token-row byte offset per pass.
-template <int P>
+// What one streaming lane loads for a group of a task: a weight row byte
+// offset per 16-row group (with this wave's k slice) and a token-row byte
+// offset per pass.
+template <int RG, int P>
 struct RingWork {
   __amdgpu_buffer_rsrc_t wr, xr;
-  uint32_t woff;
+  uint32_t woff[RG];
   uint32_t xoff[P];
   int npass;
 };
 
-template <int P>
-__device__ __forceinline__ RingWork<P> ring_work(const ExpertArgs &a, const RingShared &sh,
-                                                 const RingPlan &pl, const RingRsrc &rr,
-                                                 const RingTask &t, int g, int w) {
+template <int RG, int P>
+__device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const RingShared &sh,
+                                                     const RingRsrc &rr, const RingTask &t, int g,
+                                                     int w) {
   const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
-  RingWork<P> r;
+  RingWork<RG, P> r;
   r.wr = rr.none;
   r.xr = rr.none;
-  r.woff = kRingOff;
   r.npass = 0;
+#pragma unroll
+  for (int gg = 0; gg < RG; ++gg) r.woff[gg] = kRingOff;
 #pragma unroll
   for (int p = 0; p < P; ++p) r.xoff[p] = kRingOff;
   if (t.kind != 1 && t.kind != 2) return r;
@@ -1199,12 +1217,15 @@ __device__ __forceinline__ RingWork<P> ring_work(const ExpertArgs &a, const Ring
   if (k0 >= K) return r;  // this wave's slice is past the end of the rows
   const int kl = k0 + 4 * lg;
   if (t.kind == 1) {
-    // MFMA row li: W1 row col + li (li < 8) or W3 row col + li - 8, packed
-    // [I/32][2][32][H] so that the two are 32 rows apart
-    const int n = t.col + (li & 7);
-    const uint32_t prow = (uint32_t)(n >> 5) * 64 + (li >= 8 ? 32 : 0) + (n & 31);
+    // MFMA row li of group gg: W1 row col + 8gg + li (li < 8) or the W3 row
+    // of the same column, packed [I/32][2][32][H] so the two are 32 rows apart
+#pragma unroll
+    for (int gg = 0; gg < RG; ++gg) {
+      const int n = t.col + 8 * gg + (li & 7);
+      const uint32_t prow = (uint32_t)(n >> 5) * 64 + (li >= 8 ? 32 : 0) + (n & 31);
+      r.woff[gg] = (((uint32_t)t.e * 2 * a.I + prow) * (uint32_t)a.H + kl) * 4u;
+    }
     r.wr = rr.w13;
-    r.woff = (((uint32_t)t.e * 2 * a.I + prow) * (uint32_t)a.H + kl) * 4u;
     r.xr = rr.x;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -1217,8 +1238,10 @@ __device__ __forceinline__ RingWork<P> ring_work(const ExpertArgs &a, const Ring
       }
     }
   } else {
+#pragma unroll
+    for (int gg = 0; gg < RG; ++gg)
+      r.woff[gg] = (((uint32_t)t.e * a.H + t.col + 16 * gg + li) * (uint32_t)a.I + kl) * 4u;
     r.wr = rr.w2;
-    r.woff = (((uint32_t)t.e * a.H + t.col + li) * (uint32_t)a.I + kl) * 4u;
     r.xr = rr.inter;
 #pragma unroll
     for (int p = 0; p < P; ++p) {
@@ -1229,131 +1252,186 @@ __device__ __forceinline__ RingWork<P> ring_work(const ExpertArgs &a, const Ring
   return r;
 }
 
-// One ring step's loads (weights + every pass's token rows) into one slot.
-template <int P>
-__device__ __forceinline__ void ring_issue(const RingWork<P> &r, int s, f32x4 &wt,
+// One ring step's loads (each row group's weights + every pass's token rows)
+// into one slot.
+template <int RG, int P>
+__device__ __forceinline__ void ring_issue(const RingWork<RG, P> &r, int s, f32x4 (&wt)[RG],
                                            f32x4 (&xv)[P]) {
-  wt = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.wr, r.woff + s * 64, 0, 0));
+#pragma unroll
+  for (int gg = 0; gg < RG; ++gg)
+    wt[gg] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.wr, r.woff[gg] + s * 64, 0, 0));
 #pragma unroll
   for (int p = 0; p < P; ++p)
     xv[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + s * 64, 0, 0));
 }
 
-// Combine task q (tokens 8q .. 8q + 7) by the 512 threads of the streaming
-// waves: thread ts takes column quads ts, ts + 512, ... of every token, two
-// tokens at a time so that 10 loads are in flight per thread.  Same
-// arithmetic as combine_task: FMA chain over k ascending, then the residual.
-__device__ void ring_combine(const ExpertArgs &a, int q, int ts) {
+// A token's routing: slots of its four expert rows and their weights.
+struct RingRoute {
+  int slot[kTopK];
+  float w[kTopK];
+};
+
+__device__ __forceinline__ RingRoute ring_route(const ExpertArgs &a, int tok) {
+  RingRoute r;
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    int slot = a.s.pos[(size_t)tok * kTopK + k];
+    float w = a.s.wts[(size_t)tok * kTopK + k];
+    if (slot < 0 || slot >= a.T * kTopK) {
+      slot = 0;
+      w = 0.0f;
+    }
+    r.slot[k] = slot;
+    r.w[k] = w;
+  }
+  return r;
+}
+
+// Combine of token tok by the 512 threads of the streaming waves (thread ts:
+// float4 columns ts, ts + 512, ...), with the arithmetic of combine_task:
+// FMA chain over k ascending, then the residual.  y may alias the residual:
+// each thread reads its columns before it writes them.
+__device__ void ring_combine(const ExpertArgs &a, int tok, const RingRoute &r, int ts) {
 #pragma clang fp contract(off)
-  constexpr int TB = 2;  // tokens per batch
   const int H4 = a.H >> 2;
   const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
   const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
   float4 *y4 = reinterpret_cast<float4 *>(a.y);
-  const int t0 = q * kCombineTokens;
-  const int nt = min(kCombineTokens, a.T - t0);
-  for (int k0 = 0; k0 < nt; k0 += TB) {
-    for (int c4 = ts; c4 < H4; c4 += kRingWaves * 64) {
-      float4 v[TB][kTopK], rv[TB];
-      float wk[TB][kTopK];
+  for (int c4 = ts; c4 < H4; c4 += kRingWaves * 64) {
+    float4 v[kTopK];
 #pragma unroll
-      for (int i = 0; i < TB; ++i) {
-        const int tok = t0 + min(k0 + i, nt - 1);
+    for (int k = 0; k < kTopK; ++k) v[k] = so[(size_t)r.slot[k] * H4 + c4];
+    const float4 rv = r4 ? r4[(size_t)tok * H4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int k = 0; k < kTopK; ++k) {
-          int slot = a.s.pos[(size_t)tok * kTopK + k];
-          wk[i][k] = a.s.wts[(size_t)tok * kTopK + k];
-          if (slot < 0 || slot >= a.T * kTopK) {
-            slot = 0;
-            wk[i][k] = 0.0f;
-          }
-          v[i][k] = so[(size_t)slot * H4 + c4];
-        }
-        rv[i] = r4 ? r4[(size_t)tok * H4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int i = 0; i < TB; ++i) {
-        if (k0 + i >= nt) break;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k) {
-          acc.x = __builtin_fmaf(v[i][k].x, wk[i][k], acc.x);
-          acc.y = __builtin_fmaf(v[i][k].y, wk[i][k], acc.y);
-          acc.z = __builtin_fmaf(v[i][k].z, wk[i][k], acc.z);
-          acc.w = __builtin_fmaf(v[i][k].w, wk[i][k], acc.w);
-        }
-        if (r4) {
-          acc.x = rv[i].x + acc.x;
-          acc.y = rv[i].y + acc.y;
-          acc.z = rv[i].z + acc.z;
-          acc.w = rv[i].w + acc.w;
-        }
-        y4[(size_t)(t0 + k0 + i) * H4 + c4] = acc;
-      }
+    for (int k = 0; k < kTopK; ++k) {
+      acc.x = __builtin_fmaf(v[k].x, r.w[k], acc.x);
+      acc.y = __builtin_fmaf(v[k].y, r.w[k], acc.y);
+      acc.z = __builtin_fmaf(v[k].z, r.w[k], acc.z);
+      acc.w = __builtin_fmaf(v[k].w, r.w[k], acc.w);
     }
+    if (r4) {
+      acc.x = rv.x + acc.x;
+      acc.y = rv.y + acc.y;
+      acc.z = rv.z + acc.z;
+      acc.w = rv.w + acc.w;
+    }
+    y4[(size_t)tok * H4 + c4] = acc;
   }
 }
 
-// Partials of item i: res[i & 1][wave][pass][row][token], 16 x 16 per pass.
-template <int P>
-__device__ __forceinline__ float *ring_res(float *res, int b, int w, int p) {
-  return res + ((((size_t)b * kRingWaves + w) * P + p) * kRingTokens * kRingTokens);
+// Partials of item i: res[i & 1][wave][row group][pass][row][token], 16 x 16.
+template <int RG, int P>
+__device__ __forceinline__ float *ring_res(float *res, int b, int w, int gg, int p) {
+  return res + (((((size_t)b * kRingWaves + w) * RG + gg) * P + p) * kRingTokens * kRingTokens);
 }
 
-template <int P>
+// Streaming side: RG row groups of 16 rows share every token-row load; with
+// one group two accumulators per pass break the MFMA dependency chain.
+template <int RG, int P>
 __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, const RingPlan &pl,
                               long long ticks) {
+  constexpr int NA = RG == 1 ? 2 : 1;
+  constexpr int D = ring_depth(RG);
+  static_assert(kRingSteps % D == 0, "ring rotation realigns at task boundaries");
+  static_assert(D < kRingSteps - D - 1, "the next task is published before it is read");
   int *err = &a.s.ctrl->err;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
   const RingRsrc rr = ring_rsrc(a);
-  f32x4 wt[kRingDepth];
-  f32x4 xv[kRingDepth][P];
+  const RingTask none{4, 0, 0, 0, 0, 0, 0, 1};
+  f32x4 wt[D][RG];
+  f32x4 xv[D][P];
   int j = 0, g = 0, it = 0;  // task, group within it, item (group) counter
-  RingTask t = ring_task<P>(sh, pl, 0);
-  RingWork<P> cur = ring_work<P>(a, sh, pl, rr, t, 0, w);
+  RingTask t = ring_seq_task<P>(sh, pl, 0);
+  RingWork<RG, P> cur = ring_work<RG, P>(a, sh, rr, t, 0, w);
   bool ok = true;
   if (t.kind == 2)
     ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> t.u) & 1; }, &sh.abort, err, ticks);
-  if (!ok) cur = ring_work<P>(a, sh, pl, rr, RingTask{4, 0, 0, 0, 0, 0, 0, 1}, 0, w);
+  if (!ok) cur = ring_work<RG, P>(a, sh, rr, none, 0, w);
+  // in step order: the first step's MFMAs then wait only for the first
+  // step's loads (the scheduler would otherwise issue them last)
 #pragma unroll
-  for (int s = 0; s < kRingDepth; ++s) ring_issue<P>(cur, s, wt[s], xv[s]);
-  // Row tasks run through the ring; the combine tasks, which come after
-  // every row task, run after it with the ring's registers free.
-  while (ok && (t.kind == 1 || t.kind == 2)) {
-    // the next group: another group of this task or the first of the next
+  for (int s = 0; s < D; ++s) {
+    ring_issue<RG, P>(cur, s, wt[s], xv[s]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the queue counter, claimed by lane 0 only (other lanes' offsets are out
+  // of range: no-ops that return 0) without a divergent branch
+  const __amdgpu_buffer_rsrc_t cr =
+      __builtin_amdgcn_make_buffer_rsrc(a.s.ctrl, 0, (int)sizeof(Ctrl), kBufferRsrcWord3);
+  const uint32_t claim_off = lane == 0 ? (uint32_t)offsetof(Ctrl, head) : kRingOff;
+  int claimed = 0;
+  bool refill = false;  // the ring holds no loads for task t yet
+  while (ok && t.kind != 4) {
+    if (refill) {
+      // a down task whose inputs were not ready when the gate/up task before
+      // it was still running: wait for them now, then fill the ring
+      refill = false;
+      ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> t.u) & 1; }, &sh.abort, err, ticks);
+      cur = ring_work<RG, P>(a, sh, rr, ok ? t : none, 0, w);
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        ring_issue<RG, P>(cur, s, wt[s], xv[s]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    // Wave 0 claims the block's next task as this one starts.  Loads
+    // complete in issue order, so the reply has arrived by the time step D's
+    // weights have, and the id is published then, well before the waves
+    // need it to issue the next task's loads.
+    const bool claim_now = w == 0 && g == 0;
+    if (claim_now) claimed = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, cr, claim_off, 0, 0);
     int jn = j, gn = g + 1;
     RingTask tn = t;
-    if (gn >= t.ngroups) {
-      jn = j + 1;
-      gn = 0;
-      tn = ring_task<P>(sh, pl, jn);
-    }
-    RingWork<P> nxt;
-    f32x4 acc[P][2];
+    RingWork<RG, P> nxt;
+    f32x4 acc[RG][P][NA];
 #pragma unroll
-    for (int p = 0; p < P; ++p) acc[p][0] = acc[p][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int gg = 0; gg < RG; ++gg)
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int n = 0; n < NA; ++n) acc[gg][p][n] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int s = 0; s < kRingSteps; ++s) {
-      const int sl = s % kRingDepth;
+      const int sl = s % D;
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         if (p < cur.npass) {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            acc[p][q & 1] = __builtin_amdgcn_mfma_f32_16x16x4f32(wt[sl][q], xv[sl][p][q],
-                                                                 acc[p][q & 1], 0, 0, 0);
+#pragma unroll
+            for (int gg = 0; gg < RG; ++gg)
+              acc[gg][p][q % NA] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                  wt[sl][gg][q], xv[sl][p][q], acc[gg][p][q % NA], 0, 0, 0);
         }
       }
-      if (s == kRingSteps - kRingDepth - 1) {
-        // the next group's rows are about to be issued: a down task needs
-        // every gate/up task of its unit done before its rows are read
-        if (ok && tn.kind == 2 && gn == 0)
-          ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> tn.u) & 1; }, &sh.abort, err, ticks);
-        nxt = ring_work<P>(a, sh, pl, rr, ok ? tn : RingTask{4, 0, 0, 0, 0, 0, 0, 1}, gn, w);
+      if (s == D && claim_now) {
+        if (lane == 0) lds_store(&sh.seq[(j + 1) & 7], pl.grid + claimed);
+        release_lds();
+        if (lane == 0) lds_store(&sh.nseq, j + 2);
       }
-      if (s + kRingDepth < kRingSteps) ring_issue<P>(cur, s + kRingDepth, wt[sl], xv[sl]);
-      else ring_issue<P>(nxt, s + kRingDepth - kRingSteps, wt[sl], xv[sl]);
+      if (s == kRingSteps - D - 1) {
+        // the next group's rows are about to be issued
+        if (gn >= t.ngroups) {
+          jn = j + 1;
+          gn = 0;
+          if (ok) ok = ring_wait(&sh.nseq, [&](int v) { return v >= j + 2; }, &sh.abort, err, ticks);
+          tn = ok ? ring_seq_task<P>(sh, pl, jn) : none;
+        }
+        // a down task needs every gate/up task of its unit done before its
+        // rows are read; a gate/up task does not wait for them
+        if (ok && tn.kind == 2 && gn == 0) {
+          const bool ready = (__builtin_amdgcn_readfirstlane(lds_load(&sh.dep_ok)) >> tn.u) & 1;
+          if (!ready && t.kind == 1)
+            refill = true;
+          else
+            ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> tn.u) & 1; }, &sh.abort, err, ticks);
+        }
+        nxt = ring_work<RG, P>(a, sh, rr, ok && !refill ? tn : none, gn, w);
+      }
+      if (s + D < kRingSteps) ring_issue<RG, P>(cur, s + D, wt[sl], xv[sl]);
+      else ring_issue<RG, P>(nxt, s + D - kRingSteps, wt[sl], xv[sl]);
     }
     if (ok) {
       // partials of item it into buffer it & 1, once item it - 2 is consumed
@@ -1361,12 +1439,16 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
       if (ok) {
         const int b = it & 1;
 #pragma unroll
-        for (int p = 0; p < P; ++p) {
-          if (p < cur.npass) {
-            float *r = ring_res<P>(res, b, w, p);
-            const f32x4 v = acc[p][0] + acc[p][1];
+        for (int gg = 0; gg < RG; ++gg) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) r[(4 * lg + i) * kRingTokens + li] = v[i];
+          for (int p = 0; p < P; ++p) {
+            if (p < cur.npass) {
+              float *r = ring_res<RG, P>(res, b, w, gg, p);
+              f32x4 v = acc[gg][p][0];
+              if (NA == 2) v += acc[gg][p][NA - 1];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) r[(4 * lg + i) * kRingTokens + li] = v[i];
+            }
           }
         }
         release_lds();
@@ -1379,26 +1461,31 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
     t = tn;
     cur = nxt;
   }
-  for (; ok && t.kind == 3; t = ring_task<P>(sh, pl, ++j)) {
+  // combine tasks (one token each), after every row task, with the ring's
+  // registers free; the routing is read before the wait
+  for (int tok = blockIdx.x; ok && tok < pl.ncomb; tok += pl.grid) {
+    const RingRoute r = ring_route(a, tok);
     ok = ring_wait(&sh.p2_ok, [&](int v) { return v != 0; }, &sh.abort, err, ticks);
-    if (ok) ring_combine(a, t.q, (int)threadIdx.x);
+    if (ok) ring_combine(a, tok, r, (int)threadIdx.x);
   }
 }
 
 // Control side: sums the 8 k-slice partials of item (t, g) and stores the
 // outputs with 16-byte agent-scope stores (gate/up: silu(W1 x) * (W3 x) for
-// 8 columns; down: 16 columns).
-template <int P>
+// 8 columns per row group; down: 16 columns per row group).
+template <int RG, int P>
 __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &t, int g,
                                            const float *res, int b, const AgentOut &inter_out,
                                            const AgentOut &sout_out) {
   const int lane = threadIdx.x & 63;
   const int m0 = g * kRingTokens * P;
   const int nt = min(kRingTokens * P, t.cnt - m0);
-  // gate/up: lane -> (token, 4 columns): 2 lanes per token; down: 4 lanes
+  // gate/up: lane -> (token, 4 columns): 2 lanes per token and row group;
+  // down: 4 lanes
   const int per = t.kind == 1 ? 2 : 4;
-  for (int f = lane; f < nt * per; f += 64) {
-    const int m = f / per, q = f % per;
+  for (int f = lane; f < nt * per * RG; f += 64) {
+    const int gg = f / (nt * per), fr = f % (nt * per);
+    const int m = fr / per, q = fr % per;
     const int p = m / kRingTokens, mt = m % kRingTokens;
     f32x4 o;
 #pragma unroll
@@ -1408,7 +1495,7 @@ __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &
         float gs = 0.f, us = 0.f;
 #pragma unroll
         for (int w = 0; w < kRingWaves; ++w) {
-          const float *r = ring_res<P>(const_cast<float *>(res), b, w, p);
+          const float *r = ring_res<RG, P>(const_cast<float *>(res), b, w, gg, p);
           gs += r[c * kRingTokens + mt];
           us += r[(8 + c) * kRingTokens + mt];
         }
@@ -1416,15 +1503,16 @@ __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &
       } else {
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < kRingWaves; ++w) s += ring_res<P>(const_cast<float *>(res), b, w, p)[c * kRingTokens + mt];
+        for (int w = 0; w < kRingWaves; ++w)
+          s += ring_res<RG, P>(const_cast<float *>(res), b, w, gg, p)[c * kRingTokens + mt];
         o[jj] = s;
       }
     }
     const int slot = t.slot0 + m0 + m;
     if (t.kind == 1)
-      inter_out.store((uint32_t)(((size_t)slot * a.I + t.col + q * 4) * sizeof(float)), o);
+      inter_out.store((uint32_t)(((size_t)slot * a.I + t.col + 8 * gg + q * 4) * sizeof(float)), o);
     else
-      sout_out.store((uint32_t)(((size_t)slot * a.H + t.col + q * 4) * sizeof(float)), o);
+      sout_out.store((uint32_t)(((size_t)slot * a.H + t.col + 16 * gg + q * 4) * sizeof(float)), o);
   }
 }
 
@@ -1441,7 +1529,7 @@ __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &
 constexpr int kRingHorizon = 4;            // tasks (from the flush position) polled for
 constexpr long long kRingPollTicks = 20;   // at most one poll per 200 ns
 
-template <int P>
+template <int RG, int P>
 __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *res,
                              const RingPlan &pl) {
   Ctrl *c = a.s.ctrl;
@@ -1451,28 +1539,29 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
   uint32_t dep_ok = 0;  // units whose gate/up tasks are all done
   bool p2_ok = false;   // every down task done
   int j = 0, g = 0, it = 0;  // next item to flush
-  RingTask t = ring_task<P>(sh, pl, 0);
+  RingTask t = ring_seq_task<P>(sh, pl, 0);
+  const bool combines = (int)blockIdx.x < pl.ncomb;
   int sig = 0;
   long long last = ring_now(), last_poll = 0;
   while (true) {
     // inputs one of the next tasks needs and nobody has seen yet
     int pu = -1;
     bool pp2 = false;
-    for (int d = 0; d < kRingHorizon; ++d) {
-      const RingTask tt = d == 0 ? t : ring_task<P>(sh, pl, j + d);
-      if (tt.kind == 4) break;
+    const int ns = __builtin_amdgcn_readfirstlane(lds_load(&sh.nseq));
+    acquire_lds();
+    for (int d = 0; d < kRingHorizon && j + d < ns; ++d) {
+      const RingTask tt = d == 0 ? t : ring_seq_task<P>(sh, pl, j + d);
+      if (tt.kind == 4) {  // the block's last row task: its combine tasks follow
+        pp2 = combines && !p2_ok;
+        break;
+      }
       if (tt.kind == 2 && !((dep_ok >> tt.u) & 1u)) {
         pu = tt.u;
         break;
       }
-      if (tt.kind == 3 && !p2_ok) {
-        pp2 = true;
-        break;
-      }
     }
-    // every row task flushed (only combine tasks or the end remain) and no
-    // input left to poll for: done
-    if (t.kind != 1 && t.kind != 2 && pu < 0 && !pp2) break;
+    // every row task flushed and no input left to poll for: done
+    if (t.kind == 4 && pu < 0 && !pp2) break;
     bool prog = false;
     const long long now = ring_now();
     const bool poll = (pu >= 0 || pp2) && now - last_poll >= kRingPollTicks;
@@ -1483,11 +1572,11 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
     }
     // flush every complete item (in order)
     int flushed_now = 0;
-    while (t.kind == 1 || t.kind == 2) {
+    while (t.kind != 4) {
       const int b = it & 1;
       if (__builtin_amdgcn_readfirstlane(lds_load(&sh.done[b])) != kRingWaves) break;
       acquire_lds();
-      ring_flush<P>(a, t, g, res, b, inter_out, sout_out);
+      ring_flush<RG, P>(a, t, g, res, b, inter_out, sout_out);
       lds_store(&sh.done[b], 0);
       ++it;
       ++flushed_now;
@@ -1495,7 +1584,7 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
         if ((t.kind == 1 && lane == t.u) || (t.kind == 2 && lane == 32)) ++sig;
         g = 0;
         ++j;
-        t = ring_task<P>(sh, pl, j);
+        t = ring_seq_task<P>(sh, pl, j);  // published before task j - 1's partials
       }
       if (flushed_now == 2) break;
     }
@@ -1558,17 +1647,32 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
   }
 }
 
-// Token passes per ring step: the fewest that cover the largest expert's
-// tokens (up to 4 passes; larger experts run in several groups).  A pass that
-// holds no tokens would still move 1 KiB per wave per step through the CU's
+// Token passes per ring step: 1 or 2, the fewest that cover the largest
+// expert's tokens (larger experts run in several groups).  A pass that holds
+// no tokens would still move 1 KiB per wave per step through the CU's
 // load-return path, so the kernel picks the count from the plan at run time.
-constexpr int kRingMaxPasses = 4;
+constexpr int kRingMaxPasses = 2;
+constexpr int kRingWideGroups = 4;  // row groups of a 64-row task
+
+// LDS of the partials: [2][kRingWaves][row groups][passes][16][16]
+constexpr size_t ring_res_bytes(int rg, int p) {
+  return (size_t)2 * kRingWaves * rg * p * kRingTokens * kRingTokens * sizeof(float);
+}
+
+template <int RG, int P>
+__device__ __forceinline__ void ring_role(const ExpertArgs &a, RingShared &sh, float *res,
+                                          const RingPlan &pl, long long ticks) {
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == kRingWaves)  // uniform branch per wave
+    ring_control<RG, P>(a, sh, res, pl);
+  else
+    ring_streamer<RG, P>(a, sh, res, pl, 2 * ticks);
+}
 
 template <int KCH1, int KCH2>
 __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a) {
   static_assert(KCH1 * 256 <= kRingWaves * kRingSlice && KCH2 * 256 <= kRingWaves * kRingSlice,
                 "row length");
-  extern __shared__ float res[];  // [2][kRingWaves][passes][16][16]
+  extern __shared__ float res[];  // partials, ring_res_bytes(row groups, passes)
   __shared__ RingShared sh;
   const Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
@@ -1585,17 +1689,21 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     sh.p2_ok = 0;
     sh.flushed = 0;
     sh.abort = 0;
+    sh.seq[0] = blockIdx.x;  // past the row tasks when the grid is larger
+    sh.nseq = 1;
   }
   RingPlan pl;
   pl.n1 = c->n_p1;
   pl.n2 = c->n_p2;
-  pl.ntot = c->n_total;
+  pl.ncomb = a.T;  // combine tasks: one per token
   pl.p1u = c->p1_per_unit;
   pl.p2u = c->p2_per_unit;
   pl.grid = gridDim.x;
-  // plans for this kernel take their slots from the router, and every block
-  // needs a ready line
-  if (c->n_rblocks != 0 || (int)gridDim.x > kReadyLines) {
+  pl.rows = __builtin_amdgcn_readfirstlane(c->stream_rows);
+  // plans for this kernel take their slots from the router, every block
+  // needs a ready line, and a task covers 16 or 64 rows
+  if (c->n_rblocks != 0 || (int)gridDim.x > kReadyLines ||
+      (pl.rows != kStreamRows && pl.rows != kStreamRows * kRingWideGroups)) {
     if (tid == 0) st_agent(&a.s.ctrl->err, 2);
     return;
   }
@@ -1603,16 +1711,13 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   int maxcnt = 0;
   for (int e = 0; e < kExperts; ++e) maxcnt = max(maxcnt, sh.counts[e]);
   maxcnt = __builtin_amdgcn_readfirstlane(maxcnt);
-  const int passes = maxcnt <= kRingTokens ? 1 : (maxcnt <= 2 * kRingTokens ? 2 : kRingMaxPasses);
   const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
-  if (__builtin_amdgcn_readfirstlane(tid >> 6) == kRingWaves) {  // uniform branch per wave
-    if (passes == 1) ring_control<1>(a, sh, res, pl);
-    else if (passes == 2) ring_control<2>(a, sh, res, pl);
-    else ring_control<kRingMaxPasses>(a, sh, res, pl);
+  if (pl.rows == kStreamRows) {
+    if (maxcnt <= kRingTokens) ring_role<1, 1>(a, sh, res, pl, ticks);
+    else ring_role<1, kRingMaxPasses>(a, sh, res, pl, ticks);
   } else {
-    if (passes == 1) ring_streamer<1>(a, sh, res, pl, 2 * ticks);
-    else if (passes == 2) ring_streamer<2>(a, sh, res, pl, 2 * ticks);
-    else ring_streamer<kRingMaxPasses>(a, sh, res, pl, 2 * ticks);
+    if (maxcnt <= kRingTokens) ring_role<kRingWideGroups, 1>(a, sh, res, pl, ticks);
+    else ring_role<kRingWideGroups, kRingMaxPasses>(a, sh, res, pl, ticks);
   }
 }
 
@@ -1677,7 +1782,7 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
 }
 
 static size_t stream_lds_bytes() {
-  return (size_t)2 * kRingWaves * kRingMaxPasses * kRingTokens * kRingTokens * sizeof(float);
+  return ring_res_bytes(kRingWideGroups, kRingMaxPasses);  // the largest variant
 }
 
 static const void *stream_fn(int H, int I) {
@@ -1744,12 +1849,14 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
   return hipGetLastError();
 }
 
-int expert_bn(int tile_rows) {
+int expert_bn(int tile_rows, int T) {
   switch (tile_rows) {
     case 32: return Tile<32>::BN;
     case 64: return Tile<64>::BN;
     case 128: return Tile<128>::BN;
-    default: return kStreamRows;
+    // streaming: 64-row tasks once a batch has enough tokens per expert that
+    // sharing each token-row load across 4 row groups pays
+    default: return T >= kStreamWideTokens ? kStreamRows * kRingWideGroups : kStreamRows;
   }
 }
 

@@ -100,6 +100,37 @@ def test_zipf_skew_t16384(block, real_weights, oracle_mod):
 
 
 @pytest.mark.gpu
+def test_streaming_four_experts(block, real_weights, oracle_mod):
+    """Every token routed to the same four experts (bias +10) under the
+    weight-streaming plan: few row tasks per expert, so blocks claim down
+    tasks of an expert while its gate/up tasks are still running, the case
+    where a block must finish its own gate/up task before waiting for the
+    down task's inputs.  T = 200 also runs several token groups per task."""
+    from final_amd import workloads as W
+    w = dict(real_weights)
+    bias = np.array(real_weights["bias"], np.float32).copy()
+    hot = [3, 7, 19, 28]
+    bias[hot] += 10.0
+    w["bias"] = bias
+    block.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+    block.force_tile_rows(0)
+    try:
+        for T in (1, 8, 31, 32, 64, 200):
+            say(f"[four experts] T={T} plan=0")
+            x = W.gen_x(T, seed=11)
+            y = block.forward(x)
+            rt = block.last_routing()
+            ref = oracle_forward(oracle_mod, w, x)
+            check_routing(rt, ref)
+            assert sorted(np.nonzero(rt["counts"])[0].tolist()) == hot
+            np.testing.assert_allclose(y, ref["y"], rtol=RTOL, atol=ATOL)
+    finally:
+        block.force_tile_rows(-1)
+        rw = real_weights
+        block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
+
+
+@pytest.mark.gpu
 def test_residual_fused_and_in_place(block, real_weights, oracle_mod):
     """y = residual + MoE(x) (the decoder layer's add, layer.cu:1917), also
     with y aliasing the residual buffer."""
