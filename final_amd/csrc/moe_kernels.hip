@@ -1124,6 +1124,7 @@ __device__ __forceinline__ bool ring_wait(const int *p, Cond cond, int *abort_fl
 
 struct RingPlan {
   int n1, n2, ncomb, p1u, p2u, grid, rows;
+  uint32_t units;  // bit u for every unit (active expert)
 };
 
 // A row task, wave-uniform.  kind: 1 gate/up rows, 2 down rows, 4 none (the
@@ -1528,6 +1529,11 @@ __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &
 // are never more than 3 tasks past the control wave's flush position.
 constexpr int kRingHorizon = 4;            // tasks (from the flush position) polled for
 constexpr long long kRingPollTicks = 20;   // at most one poll per 200 ns
+// While some expert's gate/up tasks are not known to be done, the line is
+// also polled in the background (every 1 us), so that a down task claimed
+// later rarely waits for a poll that the control wave issues only once it
+// sees that task.
+constexpr long long kRingBgPollTicks = 100;
 
 template <int RG, int P>
 __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *res,
@@ -1564,7 +1570,8 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
     if (t.kind == 4 && pu < 0 && !pp2) break;
     bool prog = false;
     const long long now = ring_now();
-    const bool poll = (pu >= 0 || pp2) && now - last_poll >= kRingPollTicks;
+    const bool poll = ((pu >= 0 || pp2) && now - last_poll >= kRingPollTicks) ||
+                      ((dep_ok & pl.units) != pl.units && now - last_poll >= kRingBgPollTicks);
     int pv = 0;
     if (poll) {
       last_poll = now;
@@ -1700,6 +1707,10 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   pl.p2u = c->p2_per_unit;
   pl.grid = gridDim.x;
   pl.rows = __builtin_amdgcn_readfirstlane(c->stream_rows);
+  {
+    const int na = __builtin_amdgcn_readfirstlane(c->n_active);
+    pl.units = na >= 32 ? 0xFFFFFFFFu : (na > 0 ? (1u << na) - 1u : 0u);
+  }
   // plans for this kernel take their slots from the router, every block
   // needs a ready line, and a task covers 16 or 64 rows
   if (c->n_rblocks != 0 || (int)gridDim.x > kReadyLines ||
