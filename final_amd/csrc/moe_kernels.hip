@@ -710,39 +710,75 @@ __device__ void assign_task(const ExpertArgs &a, int q, int rt) {
 
 // Combine task q: tokens [8q, 8q+8).  y = residual + sum_k w_k * out_k with
 // the reference's order: sum from 0.0f, fma over k ascending
-// (layer.cu:708-720), then the residual add (layer.cu:1866-1871).
-__device__ void combine_task(const ExpertArgs &a, int q) {
+// (layer.cu:708-720), then the residual add (layer.cu:1866-1871).  The
+// tokens' slots and weights are staged in LDS first (combine_route, after
+// the dispatch and before the wait for the expert outputs), so the output
+// loads of two tokens at a time are all independent.
+struct CombineRoute {
+  int slot[kCombineTokens * kTopK];  // -1: no expert output (skipped)
+  float w[kCombineTokens * kTopK];
+};
+
+__device__ __forceinline__ void combine_route(const ExpertArgs &a, int q, CombineRoute &r) {
+  const int tid = threadIdx.x;
+  if (tid < kCombineTokens * kTopK) {
+    const int tok = q * kCombineTokens + tid / kTopK;
+    int slot = -1;
+    float w = 0.0f;
+    if (tok < a.T) {
+      slot = a.s.pos[(size_t)tok * kTopK + tid % kTopK];
+      w = a.s.wts[(size_t)tok * kTopK + tid % kTopK];
+      if (slot < 0 || slot >= a.T * kTopK) slot = -1;
+    }
+    r.slot[tid] = slot;
+    r.w[tid] = w;
+  }
+}
+
+__device__ void combine_task(const ExpertArgs &a, int q, const CombineRoute &r) {
 #pragma clang fp contract(off)
+  constexpr int TB = 2;  // tokens per batch: 10 loads in flight per thread
   const int H4 = a.H >> 2;
-  const int n = kCombineTokens * H4;
   const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
   const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
   float4 *y4 = reinterpret_cast<float4 *>(a.y);
-  for (int f = threadIdx.x; f < n; f += kThreads) {
-    const int tok = q * kCombineTokens + f / H4;
-    const int c4 = f % H4;
-    if (tok >= a.T) break;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int t0 = q * kCombineTokens;
+  const int nt = min(kCombineTokens, a.T - t0);
+  for (int k0 = 0; k0 < nt; k0 += TB) {
+    for (int c4 = threadIdx.x; c4 < H4; c4 += kThreads) {
+      float4 v[TB][kTopK], rv[TB];
 #pragma unroll
-    for (int k = 0; k < kTopK; ++k) {
-      const int slot = a.s.pos[(size_t)tok * kTopK + k];
-      if (slot >= 0 && slot < a.T * kTopK) {
-        const float wk = a.s.wts[(size_t)tok * kTopK + k];
-        const float4 v = so[(size_t)slot * H4 + c4];
-        acc.x = __builtin_fmaf(v.x, wk, acc.x);
-        acc.y = __builtin_fmaf(v.y, wk, acc.y);
-        acc.z = __builtin_fmaf(v.z, wk, acc.z);
-        acc.w = __builtin_fmaf(v.w, wk, acc.w);
+      for (int i = 0; i < TB; ++i) {
+        const int m = min(k0 + i, nt - 1);
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) {
+          const int slot = r.slot[m * kTopK + k];
+          v[i][k] = so[(size_t)(slot < 0 ? 0 : slot) * H4 + c4];
+        }
+        rv[i] = r4 ? r4[(size_t)(t0 + m) * H4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+#pragma unroll
+      for (int i = 0; i < TB; ++i) {
+        if (k0 + i >= nt) break;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k) {
+          if (r.slot[(k0 + i) * kTopK + k] < 0) continue;
+          const float wk = r.w[(k0 + i) * kTopK + k];
+          acc.x = __builtin_fmaf(v[i][k].x, wk, acc.x);
+          acc.y = __builtin_fmaf(v[i][k].y, wk, acc.y);
+          acc.z = __builtin_fmaf(v[i][k].z, wk, acc.z);
+          acc.w = __builtin_fmaf(v[i][k].w, wk, acc.w);
+        }
+        if (r4) {
+          acc.x = rv[i].x + acc.x;
+          acc.y = rv[i].y + acc.y;
+          acc.z = rv[i].z + acc.z;
+          acc.w = rv[i].w + acc.w;
+        }
+        y4[(size_t)(t0 + k0 + i) * H4 + c4] = acc;
       }
     }
-    if (r4) {
-      const float4 r = r4[(size_t)tok * H4 + c4];
-      acc.x = r.x + acc.x;
-      acc.y = r.y + acc.y;
-      acc.z = r.z + acc.z;
-      acc.w = r.w + acc.w;
-    }
-    y4[(size_t)tok * H4 + c4] = acc;
   }
 }
 
@@ -961,6 +997,7 @@ void expert_mfma_kernel(ExpertArgs a) {
   __shared__ int s_offsets[kExperts + 1];
   __shared__ int s_counts[kExperts];
   __shared__ int s_aoff[BM];
+  __shared__ CombineRoute s_route;
   Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
   if (tid <= kExperts) {
@@ -1011,8 +1048,12 @@ void expert_mfma_kernel(ExpertArgs a) {
       block_signal(&c->p2_done);
     } else {
       const int q = task - nb - n1 - n2;
-      block_wait(&c->p2_done, n2, a.wait_limit, &c->err);
-      combine_task(a, q);
+      // slots are final once the dispatch tasks are done (long before the
+      // down tiles): stage them, then wait for the expert outputs
+      block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
+      combine_route(a, q, s_route);
+      block_wait(&c->p2_done, n2, a.wait_limit, &c->err);  // ends with a block barrier
+      combine_task(a, q, s_route);
     }
     __syncthreads();
     if (tid == 0) s_task = next;
