@@ -24,7 +24,8 @@ CAPI_SYMBOLS = (
     "moe_create", "moe_destroy", "moe_set_weights", "moe_forward", "moe_route",
     "moe_experts", "moe_route_logits", "moe_last_routing", "moe_device_status",
     "moe_plan_tile_rows", "moe_force_tile_rows", "moe_set_wait_divisor",
-    "moe_strerror", "moe_version",
+    "moe_strerror", "moe_version", "moe_set_norm_weight", "moe_forward_norm",
+    "moe_last_normed",
 )
 SYNTH_SYMBOLS = (
     "moe_synth_normal", "moe_synth_stream_gate", "moe_synth_stream_bias",
@@ -68,6 +69,9 @@ def lib() -> ctypes.CDLL:
     L.moe_route_logits.argtypes = [_vp, _vp, _i, _vp]
     L.moe_last_routing.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp]
     L.moe_device_status.argtypes = [_vp, _vp]
+    L.moe_set_norm_weight.argtypes = [_vp, _vp, _i, _vp]
+    L.moe_forward_norm.argtypes = [_vp, _vp, _vp, _i, _vp]
+    L.moe_last_normed.argtypes = [_vp, _vp, _vp]
     L.moe_plan_tile_rows.argtypes = [_vp, _i]
     L.moe_force_tile_rows.argtypes = [_vp, _i]
     L.moe_set_wait_divisor.argtypes = [_vp, _i]

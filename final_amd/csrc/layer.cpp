@@ -194,6 +194,22 @@ void SparseMoeBlock::forward_gpu(float *x, float *y, const float *residual, int 
   check(moe_forward(ctx_, x, y, residual, batch * seq_len, stream), "moe_forward");
 }
 
+void SparseMoeBlock::set_post_attention_norm(const Tensor &weight) {
+  if (!ctx_) throw std::logic_error("SparseMoeBlock::set_post_attention_norm before init_gpu");
+  if (weight.size() != gate_.shape()[1])
+    throw std::invalid_argument("SparseMoeBlock::set_post_attention_norm: weight must have H entries");
+  check(moe_set_norm_weight(ctx_, weight.data(), 0, nullptr), "moe_set_norm_weight");
+}
+
+void SparseMoeBlock::forward_gpu_norm(float *h, float *out, int batch, int seq_len,
+                                      int hidden_size, hipStream_t stream) {
+  if (!ctx_) throw std::logic_error("SparseMoeBlock::forward_gpu_norm before init_gpu");
+  if ((size_t)hidden_size != gate_.shape()[1])
+    throw std::invalid_argument("SparseMoeBlock::forward_gpu_norm: hidden_size mismatch");
+  if (batch < 0 || seq_len < 0) throw std::invalid_argument("negative batch/seq_len");
+  check(moe_forward_norm(ctx_, h, out, batch * seq_len, stream), "moe_forward_norm");
+}
+
 void SparseMoeBlock::forward(const Tensor &x, Tensor &y, Tensor &router_logits) {
   if (!ctx_) throw std::logic_error("SparseMoeBlock::forward before init_gpu");
   const size_t H = gate_.shape()[1];

@@ -62,6 +62,10 @@ struct moe_ctx {
   float *bias = nullptr;
   float *w13 = nullptr;
   float *w2 = nullptr;
+  // post-attention RMSNorm (moe_forward_norm)
+  float *norm_w = nullptr;  // [H]
+  float *xn = nullptr;      // [max_tokens][H]: normalised rows
+  int normed_T = -1;
   Scratch s{};
   std::vector<void *> allocs;
 };
@@ -291,7 +295,8 @@ static int check_tokens(const moe_ctx *ctx, int T) {
 }
 
 static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
-                    moe_stream_t stream) {
+                    moe_stream_t stream, const float *norm_w = nullptr,
+                    float *xn = nullptr) {
   if (!ctx) return MOE_ERR_INVALID_ARG;
   int rc = check_tokens(ctx, T);
   if (rc) return rc;
@@ -317,6 +322,8 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   a.tile_rows = ctx_plan(ctx, T);
   a.bn = expert_bn(a.tile_rows, T);
   a.max_units = ctx->max_units;
+  a.norm_w = norm_w;
+  a.xn = xn;
   if (launch_router(a, logits != nullptr, static_cast<hipStream_t>(stream)) != hipSuccess)
     return MOE_ERR_HIP;
   ctx->routed_T = T;
@@ -374,6 +381,72 @@ int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
   int rc = moe_route(ctx, x, num_tokens, stream);
   if (rc) return rc;
   return moe_experts(ctx, x, y, residual, num_tokens, stream);
+}
+
+int moe_set_norm_weight(moe_ctx *ctx, const float *weight, int src_on_device,
+                        moe_stream_t stream) {
+  if (!ctx || !weight) return MOE_ERR_INVALID_ARG;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t H = ctx->d.hidden;
+  if (!ctx->norm_w) {
+    float *nw = nullptr, *xn = nullptr;
+    int rc = dev_alloc(ctx, &nw, H);
+    if (rc) return rc;
+    rc = dev_alloc(ctx, &xn, (size_t)ctx->d.max_tokens * H);
+    if (rc) return rc;
+    ctx->norm_w = nw;
+    ctx->xn = xn;
+  }
+  const hipMemcpyKind kind = src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  if (hipMemcpyAsync(ctx->norm_w, weight, H * sizeof(float), kind, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return MOE_ERR_HIP;
+  return MOE_OK;
+}
+
+int moe_forward_norm(moe_ctx *ctx, const float *h, float *out, int num_tokens,
+                     moe_stream_t stream) {
+  if (!ctx) return MOE_ERR_INVALID_ARG;
+  int rc = check_tokens(ctx, num_tokens);
+  if (rc) return rc;
+  if (!ctx->weights_set || !ctx->norm_w) return MOE_ERR_NOT_READY;
+  if (!h || !out || !aligned16(h) || !aligned16(out)) return MOE_ERR_INVALID_ARG;
+  if (num_tokens == 0) {
+    ctx->normed_T = 0;
+    return do_route(ctx, h, nullptr, 0, stream);
+  }
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (router_fuses_norm(num_tokens)) {
+    // the router normalises the rows it stages and stores them for the experts
+    rc = do_route(ctx, h, nullptr, num_tokens, stream, ctx->norm_w, ctx->xn);
+  } else {
+    if (launch_rmsnorm(h, ctx->norm_w, ctx->xn, num_tokens, ctx->d.hidden, st) != hipSuccess)
+      return MOE_ERR_HIP;
+    rc = do_route(ctx, ctx->xn, nullptr, num_tokens, stream);
+  }
+  if (rc) return rc;
+  ctx->normed_T = num_tokens;
+  // the residual is h itself; out may alias it (the experts read the
+  // normalised rows, and the combine reads each residual element before it
+  // writes the same element of out)
+  return moe_experts(ctx, ctx->xn, out, h, num_tokens, stream);
+}
+
+int moe_last_normed(moe_ctx *ctx, float *xn, moe_stream_t stream) {
+  if (!ctx || !xn) return MOE_ERR_INVALID_ARG;
+  if (ctx->normed_T < 0 || !ctx->xn) return MOE_ERR_NOT_READY;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t n = (size_t)ctx->normed_T * ctx->d.hidden;
+  if (n && hipMemcpyAsync(xn, ctx->xn, n * sizeof(float), hipMemcpyDeviceToHost, st) != hipSuccess)
+    return MOE_ERR_HIP;
+  if (hipStreamSynchronize(st) != hipSuccess) return MOE_ERR_HIP;
+  return MOE_OK;
 }
 
 int moe_last_routing(moe_ctx *ctx, int *idx, float *w, int *counts, float *logits,

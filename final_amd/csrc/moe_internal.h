@@ -82,6 +82,8 @@ struct RouterArgs {
   int inter;             // I (for task counts)
   int bn;                // MFMA n-tile width (columns of the B tile)
   int max_units;
+  const float *norm_w;   // post-attention RMSNorm weight [H]: x is h, normalise it (T <= 64 only)
+  float *xn;             // [T][H]: the normalised rows, for the expert kernel
 };
 
 struct ExpertArgs {
@@ -102,6 +104,11 @@ hipError_t launch_pack_w13(float *dst, const float *w1, const float *w3, int H,
                            int I, hipStream_t st);
 // Tokens per router block for a forward of T tokens.
 int router_tokens_per_block(int T);
+// Whether the router normalises h itself (RouterArgs::norm_w) for T tokens;
+// otherwise launch_rmsnorm writes the normalised rows first.
+bool router_fuses_norm(int T);
+hipError_t launch_rmsnorm(const float *h, const float *w, float *out, int T, int H,
+                          hipStream_t st);
 // Whether the weight-streaming kernel is compiled for (H, I).
 bool stream_supported(int H, int I);
 // Largest batch the streaming plan handles (its slot -> token map is in LDS).

@@ -120,6 +120,63 @@ __device__ __forceinline__ float ref_sigmoid(float x) {
   return 1.0f / (1.0f + e);
 }
 
+// ---------------------------------------------------------------------------
+// Post-attention RMSNorm (rms_norm_kernel, layer.cu:144-193), bit for bit:
+// 256 threads per row; thread t accumulates h[i]^2 for i = t, t+256, ... with
+// FMA (nvcc contracts "sum_sq += src[i] * src[i]"); each group of 32 threads
+// (a CUDA warp) folds its sums with shuffle-down at 16, 8, 4, 2, 1, where a
+// lane whose source lies outside its 32 keeps its own value; the first group
+// folds the 8 group sums (the rest 0) at 4, 2, 1; rms = 1 / sqrt(sum / H +
+// 1e-5) with IEEE division and square root; x = (h * rms) * weight.
+// ---------------------------------------------------------------------------
+constexpr int kNormThreads = 256;
+constexpr int kNormGroups = kNormThreads / 32;
+constexpr float kNormEps = 1e-5f;  // layer.cu:189 (RMS_NORM_EPS, config.h)
+
+// Sum of the 256 threads' partials of NR rows at once; every thread gets the
+// totals in tot[].  s_grp: [NR][kNormGroups] LDS scratch.  Block of 256.
+template <int NR>
+__device__ __forceinline__ void norm_totals(float (&part)[NR], float *s_grp, float *s_tot) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int m = 0; m < NR; ++m) {
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) part[m] += __shfl_down(part[m], off, 32);
+    if ((tid & 31) == 0) s_grp[m * kNormGroups + (tid >> 5)] = part[m];
+  }
+  __syncthreads();
+  if (tid < 32) {
+#pragma unroll
+    for (int m = 0; m < NR; ++m) {
+      float v = tid < kNormGroups ? s_grp[m * kNormGroups + tid] : 0.0f;
+#pragma unroll
+      for (int off = kNormGroups / 2; off > 0; off >>= 1) v += __shfl_down(v, off, 32);
+      if (tid == 0) s_tot[m] = v;
+    }
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ float norm_rms(float total, int H) {
+#pragma clang fp contract(off)
+  return 1.0f / sqrtf(total / (float)H + kNormEps);
+}
+
+// One row per block: out = rmsnorm(h) (large batches; small ones normalise
+// inside router_decode_kernel).
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float *h, const float *w,
+                                                               float *out, int H) {
+#pragma clang fp contract(off)
+  __shared__ float s_grp[kNormGroups], s_tot[1];
+  const float *src = h + (size_t)blockIdx.x * H;
+  float *dst = out + (size_t)blockIdx.x * H;
+  float part[1] = {0.0f};
+  for (int i = threadIdx.x; i < H; i += kNormThreads) part[0] = __builtin_fmaf(src[i], src[i], part[0]);
+  norm_totals<1>(part, s_grp, s_tot);
+  const float rms = norm_rms(s_tot[0], H);
+  for (int i = threadIdx.x; i < H; i += kNormThreads) dst[i] = (src[i] * rms) * w[i];
+}
+
 // acc = FMA chain over k = 0 .. K-1 of x[k] * g[k] (LDS rows xp, gp), k
 // ascending (layer.cu:109-127).  The chain is latency-bound, so the operands
 // of the next 16 k are read while this 16 k's FMAs run; the loop body has no
@@ -573,6 +630,7 @@ void router_decode_kernel(RouterArgs a) {
   __shared__ float s_tp[kDecRT][kTopK];
   __shared__ PlanShared ps;
   __shared__ int s_flag;
+  __shared__ float s_ngrp[kDecRT][kNormGroups], s_ntot[kDecRT];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tb = blockIdx.x / kDecES, es = blockIdx.x % kDecES;
@@ -594,6 +652,30 @@ void router_decode_kernel(RouterArgs a) {
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
     }
     __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+  }
+  // 1b. fused post-attention RMSNorm: the staged rows are h; normalise them in
+  // place, and the first of the token block's blocks stores them for the
+  // expert kernel
+  if (a.norm_w) {
+    static_assert(kThreads == kNormThreads, "one reference row-block per router block");
+    float part[kDecRT];
+#pragma unroll
+    for (int m = 0; m < kDecRT; ++m) {
+      float sq = 0.0f;
+      if (m < nt)
+        for (int i = tid; i < H; i += kNormThreads) sq = __builtin_fmaf(xs[m * P + i], xs[m * P + i], sq);
+      part[m] = sq;
+    }
+    norm_totals<kDecRT>(part, &s_ngrp[0][0], s_ntot);
+    for (int m = 0; m < nt; ++m) {
+      const float rms = norm_rms(s_ntot[m], H);
+      for (int i = tid; i < H; i += kNormThreads) {
+        const float v = (xs[m * P + i] * rms) * a.norm_w[i];
+        xs[m * P + i] = v;
+        if (es == 0) a.xn[(size_t)(t0 + m) * H + i] = v;
+      }
+    }
     __syncthreads();
   }
   // 2. chains: wave 0, lane = (token l / 4, expert l % 4)
@@ -1804,6 +1886,14 @@ constexpr int kSmallRT = kDecRT, kSmallKC = 256;
 constexpr int kLargeRT = 64, kLargeES = 1, kLargeKC = 64;
 
 int router_tokens_per_block(int T) { return T <= 64 ? kSmallRT : kLargeRT; }
+
+bool router_fuses_norm(int T) { return T <= 64; }
+
+hipError_t launch_rmsnorm(const float *h, const float *w, float *out, int T, int H, hipStream_t st) {
+  if (T <= 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, st, h, w, out, H);
+  return hipGetLastError();
+}
 
 hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) {
   const bool small = a.T <= 64;

@@ -73,7 +73,40 @@ class SparseMoeBlock:
             self._ctx, _ptr(gate), _ptr(bias), arr(w1_ptrs), arr(w3_ptrs), arr(w2_ptrs), 1,
             _stream(stream)), "moe_set_weights")
 
+    def set_norm_weight(self, weight, stream=None) -> None:
+        """The decoder layer's post-attention RMSNorm weight [H] (host numpy)."""
+        w = np.ascontiguousarray(weight, dtype=np.float32)
+        if w.shape != (self.hidden,):
+            raise ValueError(f"norm weight must have shape ({self.hidden},)")
+        _native.check(_native.lib().moe_set_norm_weight(self._ctx, w.ctypes.data, 0, _stream(stream)),
+                      "moe_set_norm_weight")
+
     # -- forward ------------------------------------------------------------
+    def forward_norm_gpu(self, h, out, num_tokens: int, stream=None) -> None:
+        """out = h + MoE(rmsnorm(h)) on device buffers; out may be h."""
+        _native.check(_native.lib().moe_forward_norm(self._ctx, _ptr(h), _ptr(out), int(num_tokens),
+                                                     _stream(stream)), "moe_forward_norm")
+        self._last_T = int(num_tokens)
+
+    def forward_norm(self, h: np.ndarray) -> np.ndarray:
+        """Host convenience for forward_norm_gpu."""
+        h = np.ascontiguousarray(h, dtype=np.float32)
+        T = h.shape[0]
+        dh = hip.DeviceArray.from_numpy(h)
+        do = hip.DeviceArray((T, self.hidden))
+        self.forward_norm_gpu(dh, do, T)
+        hip.synchronize()
+        self.check_device()
+        return do.download()
+
+    def last_normed(self, stream=None) -> np.ndarray:
+        """Normalised rows of the last forward_norm ([T][H])."""
+        T = max(self._last_T, 0)
+        out = np.empty((T, self.hidden), np.float32)
+        _native.check(_native.lib().moe_last_normed(self._ctx, out.ctypes.data, _stream(stream)),
+                      "moe_last_normed")
+        return out
+
     def forward_gpu(self, x, y, num_tokens: int, residual=None, stream=None) -> None:
         _native.check(_native.lib().moe_forward(self._ctx, _ptr(x), _ptr(y), _ptr(residual),
                                                 int(num_tokens), _stream(stream)), "moe_forward")

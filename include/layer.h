@@ -88,6 +88,16 @@ public:
   void forward_gpu(float *x, float *y, const float *residual, int batch,
                    int seq_len, int hidden_size, hipStream_t stream);
 
+  // The decoder layer's post-attention RMSNorm weight [H] (RMSNorm,
+  // layer.h:10-24, loaded as layers.{i}.post_attention_layernorm.weight at
+  // layer.cu:1793).  After init_gpu.
+  void set_post_attention_norm(const Tensor &weight);
+  // Steps 4-6 of DecoderLayer::forward_gpu (layer.cu:1903-1918) in one call:
+  // out = h + MoE(rmsnorm(h)), rmsnorm as rms_norm_kernel (layer.cu:144-193).
+  // out may alias h (the reference updates the layer output in place).
+  void forward_gpu_norm(float *h, float *out, int batch, int seq_len, int hidden_size,
+                        hipStream_t stream = 0);
+
   int layer_idx() const { return layer_idx_; }
   int max_tokens() const { return max_tokens_; }
   void set_max_tokens(int n);  // before init_gpu

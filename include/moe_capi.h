@@ -103,6 +103,31 @@ int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
 int moe_route_logits(moe_ctx *ctx, const float *logits, int num_tokens,
                      moe_stream_t stream);
 
+/* The post-attention RMSNorm weight [hidden] of the decoder layer that owns
+ * this block (RMSNorm post_attention_layernorm_, layer.cu:1793, weight
+ * layers.{i}.post_attention_layernorm.weight; RMSNorm::init_gpu uploads it,
+ * layer.cu:1128-1142).  Host memory when src_on_device == 0.  Allocates the
+ * normalised-row scratch ([max_tokens][hidden]) on first use.  Synchronises
+ * `stream`. */
+int moe_set_norm_weight(moe_ctx *ctx, const float *weight, int src_on_device,
+                        moe_stream_t stream);
+
+/* Steps 4-6 of DecoderLayer::forward_gpu (layer.cu:1903-1918) in one call:
+ * out = h + MoE(rmsnorm(h)), with rmsnorm exactly rms_norm_kernel
+ * (layer.cu:144-193, eps 1e-5) and the MoE block of moe_forward.  h, out:
+ * device [num_tokens][hidden] fp32, 16-byte aligned; out may alias h (the
+ * reference writes the layer output in place, layer.cu:1917).  Needs
+ * moe_set_weights and moe_set_norm_weight.  For up to 64 tokens the router
+ * normalises the rows it already stages (no extra launch); larger batches
+ * run one normalisation kernel first.  Asynchronous on `stream`. */
+int moe_forward_norm(moe_ctx *ctx, const float *h, float *out, int num_tokens,
+                     moe_stream_t stream);
+
+/* Copies the normalised rows of the last moe_forward_norm ([T][hidden]) to
+ * host memory (parity tests: the reference's normed_hidden_gpu_,
+ * layer.cu:1904-1905).  Synchronises `stream`. */
+int moe_last_normed(moe_ctx *ctx, float *xn, moe_stream_t stream);
+
 /* Copies the routing of the last moe_route/moe_forward to host memory:
  * idx [T][4] (rank order, -1 = none), w [T][4], counts [E], logits [T][E]
  * (any may be NULL).  Synchronises `stream`.  The topk_indices_gpu_,

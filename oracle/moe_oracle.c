@@ -337,6 +337,49 @@ void orc_combine(const float *sorted_out, const int *pos, const float *w,
 }
 
 /* ------------------------------------------------------------------------ */
+/* post-attention RMSNorm (layer.cu:144-193)                                 */
+/* ------------------------------------------------------------------------ */
+
+#define ORC_NORM_THREADS 256 /* RMSNorm::forward_gpu, layer.cu:1146 */
+#define ORC_WARP 32
+
+/* __shfl_down_sync(mask, v, off) over one 32-lane warp, all lanes at once:
+ * lane l reads lane l+off, or its own value when l+off is outside the warp. */
+static void shfl_down_add(float *v, int off) {
+  float nv[ORC_WARP];
+  for (int l = 0; l < ORC_WARP; ++l) nv[l] = v[l] + (l + off < ORC_WARP ? v[l + off] : v[l]);
+  memcpy(v, nv, sizeof(nv));
+}
+
+static void rmsnorm_row(const float *src, const float *weight, int H, float *dst) {
+  float part[ORC_NORM_THREADS];
+  for (int t = 0; t < ORC_NORM_THREADS; ++t) { /* layer.cu:157-160 */
+    float s = 0.0f;
+    for (int i = t; i < H; i += ORC_NORM_THREADS) s = fmaf(src[i], src[i], s);
+    part[t] = s;
+  }
+  float warp_sum[ORC_NORM_THREADS / ORC_WARP];
+  for (int wi = 0; wi < ORC_NORM_THREADS / ORC_WARP; ++wi) { /* layer.cu:163-170 */
+    float v[ORC_WARP];
+    memcpy(v, part + wi * ORC_WARP, sizeof(v));
+    for (int off = ORC_WARP / 2; off > 0; off /= 2) shfl_down_add(v, off);
+    warp_sum[wi] = v[0];
+  }
+  float v[ORC_WARP]; /* layer.cu:173-182: warp 0, lanes >= 8 hold 0 */
+  for (int l = 0; l < ORC_WARP; ++l) v[l] = l < ORC_NORM_THREADS / ORC_WARP ? warp_sum[l] : 0.0f;
+  for (int off = (ORC_NORM_THREADS / ORC_WARP) / 2; off > 0; off /= 2) shfl_down_add(v, off);
+  const float rms = 1.0f / sqrtf(v[0] / (float)H + 1e-5f); /* layer.cu:189 */
+  for (int i = 0; i < H; ++i) dst[i] = (src[i] * rms) * weight[i]; /* layer.cu:191-193 */
+}
+
+void orc_rmsnorm(const float *h, const float *weight, int64_t T, int H, float *out) {
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+#endif
+  for (int64_t t = 0; t < T; ++t) rmsnorm_row(h + t * H, weight, H, out + t * H);
+}
+
+/* ------------------------------------------------------------------------ */
 /* whole block                                                               */
 /* ------------------------------------------------------------------------ */
 

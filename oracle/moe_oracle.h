@@ -89,6 +89,20 @@ void orc_expert_w2(const float *inter, int64_t M, const float *w2, int H, int I,
 void orc_combine(const float *sorted_out, const int *pos, const float *w,
                  const float *residual, int64_t T, int H, float *y);
 
+/* Post-attention RMSNorm, rms_norm_kernel layer.cu:144-193 as launched by
+ * RMSNorm::forward_gpu layer.cu:1144-1148 (one block of 256 threads per row,
+ * warpSize 32).  Restated in the kernel's exact order: thread t (0..255)
+ * accumulates h[i]*h[i] for i = t, t+256, ... from 0.0f with fmaf (nvcc's
+ * default --fmad=true contracts "sum_sq += src[i] * src[i]"); each 32-thread
+ * warp folds its sums with __shfl_down_sync at offsets 16, 8, 4, 2, 1 (lane l
+ * adds lane l+off, or itself when l+off >= 32); warp 0 then folds the 8 warp
+ * sums (lanes 8..31 hold 0) at offsets 4, 2, 1; rms = 1.0f / sqrtf(sum / H +
+ * 1e-5f) (IEEE division and square root: no fast-math in the reference
+ * build); out[i] = (h[i] * rms) * weight[i].  h, out: [T][H]; out may alias
+ * h.  The fmaf choice is the one point not pinned by the reference (its
+ * rounding differs from mul+add only in the partial sums' last bits). */
+void orc_rmsnorm(const float *h, const float *weight, int64_t T, int H, float *out);
+
 /* The whole block, SparseMoeBlock::forward_gpu layer.cu:1428-1498 (+1917).
  * token_mask (may be NULL = all) selects the tokens whose y row is computed;
  * routing (idx, w, counts, logits) always covers all T tokens, and rows of y

@@ -56,6 +56,7 @@ def lib():
         L.orc_expert_w1w3.argtypes = [_f32p, _i64, _f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p]
         L.orc_expert_w2.argtypes = [_f32p, _i64, _f32p, ctypes.c_int, ctypes.c_int, _f32p]
         L.orc_combine.argtypes = [_f32p, _i32p, _f32p, _f32p, _i64, ctypes.c_int, _f32p]
+        L.orc_rmsnorm.argtypes = [_f32p, _f32p, _i64, ctypes.c_int, _f32p]
         L.orc_moe_forward.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                                       _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       _u8p, _f32p, _f32p, _i32p, _f32p, _i32p]
@@ -156,6 +157,25 @@ def combine(sorted_out, pos, w, residual=None):
     y = np.empty((T, H), np.float32)
     lib().orc_combine(_f(sorted_out), _i(pos), _f(w), _f(residual), T, H, _f(y))
     return y
+
+
+def rmsnorm(h, weight):
+    """Post-attention RMSNorm of every row of h [T][H] (layer.cu:144-193)."""
+    h = np.ascontiguousarray(h, dtype=np.float32)
+    T, H = h.shape
+    out = np.empty((T, H), np.float32)
+    lib().orc_rmsnorm(_f(h), _f(np.ascontiguousarray(weight, dtype=np.float32)), T, H, _f(out))
+    return out
+
+
+def moe_forward_norm(h, norm_weight, gate, bias, w1, w3, w2, token_mask=None):
+    """Steps 4-6 of DecoderLayer::forward_gpu (layer.cu:1903-1918):
+    out = h + MoE(rmsnorm(h)).  Returns the moe_forward dict plus xn, the
+    normalised rows."""
+    xn = rmsnorm(h, norm_weight)
+    r = moe_forward(xn, gate, bias, w1, w3, w2, residual=h, token_mask=token_mask)
+    r["xn"] = xn
+    return r
 
 
 def moe_forward(x, gate, bias, w1, w3, w2, residual=None, token_mask=None):

@@ -245,6 +245,35 @@ void gpu_tests() {
     (void)hipStreamDestroy(st);
     std::printf("gpu T=%d ok\n", T);
   }
+  // post-attention RMSNorm fused in front of the block, output in place
+  {
+    std::mt19937 rng(7);
+    std::vector<float> nw = normal(rng, kH, 0.1f);
+    for (float &v : nw) v += 1.0f;
+    Tensor tnw({(size_t)kH}, nw.data(), true);
+    blk.set_post_attention_norm(tnw);
+    for (int T : {1, 37, 300}) {
+      std::vector<float> h = normal(rng, (size_t)T * kH, 2.0f), xn((size_t)T * kH),
+                         yref((size_t)T * kH);
+      orc_rmsnorm(h.data(), nw.data(), T, kH, xn.data());
+      CHECK(orc_moe_forward(xn.data(), w.gate.data(), w.bias.data(), w.w1.data(), w.w3.data(),
+                            w.w2.data(), h.data(), T, kH, kI, kE, nullptr, yref.data(), nullptr,
+                            nullptr, nullptr, nullptr) == 0);
+      float *dh = nullptr;
+      const size_t bytes = (size_t)T * kH * 4;
+      CHECK(hipMalloc(&dh, bytes) == hipSuccess);
+      CHECK(hipMemcpy(dh, h.data(), bytes, hipMemcpyHostToDevice) == hipSuccess);
+      blk.forward_gpu_norm(dh, dh, 1, T, kH, 0);
+      std::vector<float> y((size_t)T * kH);
+      CHECK(hipDeviceSynchronize() == hipSuccess);
+      CHECK(hipMemcpy(y.data(), dh, bytes, hipMemcpyDeviceToHost) == hipSuccess);
+      int bad = 0;
+      for (size_t i = 0; i < y.size(); ++i) bad += !close(y[i], yref[i]);
+      CHECK(bad == 0);
+      (void)hipFree(dh);
+      std::printf("gpu norm T=%d ok\n", T);
+    }
+  }
   // route_tokens on crafted logits (equal logits, large margins) vs the oracle
   Tensor lt({3, (size_t)kE});
   lt.zero();

@@ -150,3 +150,52 @@ def test_residual_fused_and_in_place(block, real_weights, oracle_mod):
     hip.synchronize()
     block.check_device()
     np.testing.assert_allclose(dr.download(), ref["y"], rtol=RTOL, atol=ATOL)
+
+
+def _norm_weight(H):
+    return (1.0 + 0.1 * np.random.RandomState(17).randn(H)).astype(np.float32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 8, 64, 100, 4096])
+def test_forward_norm_matches_oracle(T, block, real_weights, oracle_mod):
+    """out = h + MoE(rmsnorm(h)) (DecoderLayer steps 4-6, layer.cu:1903-1918):
+    the normalised rows and the routing bit-exact, out within tolerance.  T <= 64
+    normalises inside the router, larger T in its own kernel."""
+    from final_amd import workloads as W
+    w = real_weights
+    nw = _norm_weight(W.H)
+    block.set_norm_weight(nw)
+    say(f"[norm] T={T} plan={block.plan(T)}")
+    h = W.gen_x(T, seed=21) * np.float32(2.5)
+    out = block.forward_norm(h)
+    xn = block.last_normed()
+    rt = block.last_routing()
+    mask = None
+    if T > 1000:
+        mask = np.zeros(T, np.uint8)
+        mask[::8] = 1
+    ref = oracle_mod.moe_forward_norm(h, nw, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"],
+                                      token_mask=mask)
+    assert np.array_equal(bits(xn), bits(ref["xn"])), "normalised rows differ"
+    check_routing(rt, ref)
+    sel = slice(None) if mask is None else mask.astype(bool)
+    np.testing.assert_allclose(out[sel], ref["y"][sel], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+def test_forward_norm_in_place(block, real_weights, oracle_mod):
+    """out aliasing h, as the reference's layer output (layer.cu:1917)."""
+    from final_amd import hip
+    from final_amd import workloads as W
+    w = real_weights
+    nw = _norm_weight(W.H)
+    block.set_norm_weight(nw)
+    for T in (8, 300):
+        h = W.gen_x(T, seed=23)
+        ref = oracle_mod.moe_forward_norm(h, nw, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+        dh = hip.DeviceArray.from_numpy(h)
+        block.forward_norm_gpu(dh, dh, T)
+        hip.synchronize()
+        block.check_device()
+        np.testing.assert_allclose(dh.download(), ref["y"], rtol=RTOL, atol=ATOL)

@@ -379,3 +379,131 @@ def test_block_pieces_compose(oracle_mod):
     sel = mask.astype(bool)
     assert np.array_equal(bits(part["y"][sel]), bits(y[sel]))
     assert np.all(np.isnan(part["y"][~sel]))
+
+
+# ---------------------------------------------------------------------------
+# Post-attention RMSNorm (rms_norm_kernel, layer.cu:144-193)
+# ---------------------------------------------------------------------------
+
+def _rms_from_total(total, H=2048):
+    """rms = 1.0f / sqrtf(total / H + 1e-5f) in float32 (IEEE ops)."""
+    f = np.float32
+    return f(1.0) / np.sqrt(f(total) / f(H) + f(1e-5))
+
+
+def test_rmsnorm_one_hot_rows(oracle_mod):
+    """A single nonzero element contributes its square exactly whatever the
+    reduction order: every index (one per thread, warp and stride position)
+    must enter the sum once -- a dropped or doubled term fails."""
+    H = 2048
+    rng = np.random.RandomState(5)
+    wgt = (1.0 + 0.1 * rng.randn(H)).astype(np.float32)
+    cols = [0, 1, 16, 31, 32, 255, 256, 511, 1000, 1791, 2047]
+    h = np.zeros((len(cols), H), np.float32)
+    vals = np.float32(1.5) ** np.arange(len(cols), dtype=np.float32)
+    for r, (c, v) in enumerate(zip(cols, vals)):
+        h[r, c] = v
+    out = oracle_mod.rmsnorm(h, wgt)
+    for r, (c, v) in enumerate(zip(cols, vals)):
+        rms = _rms_from_total(np.float32(v) * np.float32(v))
+        want = (np.float32(v) * rms) * wgt[c]
+        assert out[r, c] == want, (c, out[r, c], want)
+        assert np.count_nonzero(out[r]) == 1
+
+
+def _sequential_total(row):
+    """float32 sum of squares in index order (the order a plain loop takes)."""
+    t = np.float32(0.0)
+    for v in row:
+        t = np.float32(t + np.float32(v) * np.float32(v))
+    return t
+
+
+# Rows whose sum of squares depends on the reduction order: one large square
+# (4096) and several squares of 2^-12, each half an ulp of 4096.  Added to the
+# large one first, every small square is lost; the reference's order adds the
+# small ones to each other first, so they survive.  Each case gives the total
+# the reference's order produces (exact in float32).
+_B = 2.0 ** -6   # square 2^-12
+
+
+def _reverse_total(row):
+    """float32 sum of squares in descending index order."""
+    return _sequential_total(row[::-1])
+
+
+# name -> (elements, total in the reference's order, a plausible wrong order)
+_ORDER_CASES = {
+    # warp tree (__shfl_down at 16, 8, 4, 2, 1): the large square at lane 0,
+    # small ones at lanes 1..15 and 17..31 (lane 16 empty).  Lane 0 meets
+    # lane 8 (2 small), lane 4 (4), lane 2 (8) and lane 1 (16): 4096 + 30 *
+    # 2^-12 exactly; a plain loop over the lanes loses them all.
+    "warp tree": ({0: 64.0, **{l: _B for l in list(range(1, 16)) + list(range(17, 32))}},
+                  4096.0 + 30 * 2.0 ** -12, _sequential_total),
+    # block tree over the 8 warp sums (offsets 4, 2, 1): large at warp 0,
+    # one small square in each of warps 1..7 (thread 32w).  w0 + w4 loses its
+    # small square; (w2 + w6) and (w1 + w5) + (w3 + w7) keep theirs:
+    # 4096 + 6 * 2^-12; a plain loop over the warps loses them all.
+    "block tree": ({0: 64.0, **{32 * w: _B for w in range(1, 8)}},
+                   4096.0 + 6 * 2.0 ** -12, _sequential_total),
+    # one thread's fma chain runs over i = t, t+256, ..., t+1792 ascending:
+    # the large square first (i = 7), then seven small ones, each lost:
+    # 4096.  Descending order keeps them (7 * 2^-12 first, then 4096 + 3.5
+    # ulps, ties to even: 4096 + 8 * 2^-12).
+    "thread chain": ({7: 64.0, **{7 + 256 * j: _B for j in range(1, 8)}},
+                     4096.0, _reverse_total),
+}
+
+
+@pytest.mark.parametrize("case", sorted(_ORDER_CASES))
+def test_rmsnorm_reduction_order(oracle_mod, case):
+    """The reference's reduction order (layer.cu:157-186), each stage pinned
+    by a row whose total differs from a plausible other order's by several
+    ulps, enough to change rms."""
+    H = 2048
+    elems, total_ref, other_order = _ORDER_CASES[case]
+    h = np.zeros((1, H), np.float32)
+    for i, v in elems.items():
+        h[0, i] = np.float32(v)
+    assert np.float32(total_ref) == total_ref          # exact in float32
+    total_other = other_order(h[0])
+    assert total_other != np.float32(total_ref)
+    rms_ref = _rms_from_total(np.float32(total_ref))
+    assert rms_ref != _rms_from_total(total_other)      # distinguishable at this input
+    wgt = np.ones(H, np.float32)
+    out = oracle_mod.rmsnorm(h, wgt)
+    i_big = max(elems, key=lambda i: elems[i])
+    assert out[0, i_big] == np.float32(64.0) * rms_ref
+
+
+def test_rmsnorm_matches_float64(oracle_mod):
+    """Random rows: within a few float32 ulps of the float64 formula."""
+    rng = np.random.RandomState(9)
+    T, H = 16, 2048
+    h = rng.randn(T, H).astype(np.float32) * np.float32(3.0)
+    wgt = (1.0 + 0.05 * rng.randn(H)).astype(np.float32)
+    out = oracle_mod.rmsnorm(h, wgt)
+    h64 = h.astype(np.float64)
+    ref = h64 / np.sqrt((h64 ** 2).mean(axis=1, keepdims=True) + 1e-5) * wgt
+    np.testing.assert_allclose(out, ref, rtol=4e-7, atol=0)
+
+
+def test_moe_forward_norm_is_norm_then_block(oracle_mod):
+    """The fused-step oracle is exactly rmsnorm followed by the block with the
+    pre-norm rows as the residual."""
+    from final_amd import workloads as W
+    rng = np.random.RandomState(3)
+    T, H, I, E = 4, 64, 32, 8
+    h = rng.randn(T, H).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.randn(H)).astype(np.float32)
+    gate = (0.1 * rng.randn(E, H)).astype(np.float32)
+    bias = (0.01 * rng.randn(E)).astype(np.float32)
+    w1 = (0.1 * rng.randn(E, I, H)).astype(np.float32)
+    w3 = (0.1 * rng.randn(E, I, H)).astype(np.float32)
+    w2 = (0.1 * rng.randn(E, H, I)).astype(np.float32)
+    r = oracle_mod.moe_forward_norm(h, nw, gate, bias, w1, w3, w2)
+    xn = oracle_mod.rmsnorm(h, nw)
+    r2 = oracle_mod.moe_forward(xn, gate, bias, w1, w3, w2, residual=h)
+    assert np.array_equal(r["xn"], xn)
+    assert np.array_equal(r["y"], r2["y"])
+    assert np.array_equal(r["idx"], r2["idx"])
