@@ -69,6 +69,73 @@ def cpu_baseline(w, x, threads: int):
                       f"{med:.3f} s each, OpenMP {threads} threads"}
 
 
+def bench_dense(args, wl):
+    """The dense FFN of layers 0-1 (MLP::forward_gpu): one step = one forward
+    of W2 (silu(W1 x) * (W3 x)) with I = 7168 (the fixed-routing router plus
+    the expert kernel over 4 chunks of 1792)."""
+    from final_amd import DenseMLP, hip
+    from final_amd import workloads as W
+    T = wl.T
+    I = W.DENSE_I
+    log(f"[bench] dense FFN T={T} I={I}: generating weights")
+    dw = W.gen_dense_weights(wl.seed)
+    x = W.gen_x(T, wl.seed)
+    nsets = args.weight_sets if args.weight_sets > 0 else (1 if T >= 512 else 3)
+    mlps = []
+    for _ in range(nsets):
+        m = DenseMLP(W.H, I, max_tokens=max(T, 64))
+        m.set_weights(dw["w1"], dw["w3"], dw["w2"])
+        mlps.append(m)
+    stream = hip.Stream()
+    dx = hip.DeviceArray.from_numpy(x)
+    dy = hip.DeviceArray((T, W.H))
+    plan = mlps[0].plan(T)
+    for i in range(args.warmup):
+        mlps[i % nsets].forward_gpu(dx, dy, T, stream=stream)
+    stream.synchronize()
+    mlps[0].check_device(stream)
+    K = args.steps
+    start, stop = hip.Event(), hip.Event()
+    hip.synchronize()
+    t_wall = time.perf_counter()
+    start.record(stream)
+    for i in range(K):
+        mlps[i % nsets].forward_gpu(dx, dy, T, stream=stream)
+    stop.record(stream)
+    stop.synchronize()
+    wall = time.perf_counter() - t_wall
+    for m in mlps:
+        m.check_device(stream)
+    ms_step = start.elapsed_ms(stop) / K
+    flops = T * 3 * 2 * W.H * I
+    wbytes = 3 * W.H * I * 4 + 2 * T * W.H * 4  # weights + x + y
+    if plan != 0:
+        achieved = flops / (ms_step / 1e3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_F32_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_F32_TFLOPS, 4),
+                "per_launch": {"flop": flops}}
+    else:
+        achieved = wbytes / (ms_step / 1e3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                "per_launch": {"bytes": wbytes}}
+    roof["traffic"] = None
+    roof["kernel"] = ("expert_mfma_kernel<%d>" % plan if plan else "expert_ring_kernel") + " (whole step)"
+    out = {
+        "metric": "dense-FFN tokens/sec fp32, 1 GPU; % of MFMA / HBM roofline",
+        "value": round(T * K / (ms_step * K / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
+        "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) tokens)",
+        "config": {"workload": wl.name, "tokens": T, "hidden": W.H, "inter": I,
+                   "plan_tile_rows": plan, "weight_sets": nsets, "wall_s": round(wall, 4)},
+        "roofline": roof, "cpu_baseline": None,
+    }
+    for m in mlps:
+        m.close()
+    print(json.dumps(out), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -94,6 +161,8 @@ def main():
     T = wl.T
     if hip.device_count() < 1:
         raise RuntimeError("no HIP device visible")
+    if wl.kind == "dense":
+        return bench_dense(args, wl)
     log(f"[bench] workload={wl.name} T={T}: generating weights")
     w = W.gen_weights(wl.seed, bias=wl.bias)
     x = W.gen_x(T, wl.seed)

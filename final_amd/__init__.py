@@ -3,6 +3,6 @@ SwiGLU experts and combine as hand-written HIP kernels behind a C-ABI
 (include/moe_capi.h), with the reference's C++ layer interface
 (include/layer.h) and this Python mirror of it."""
 from . import _native
-from .moe import SparseMoeBlock
+from .moe import DenseMLP, SparseMoeBlock
 
-__all__ = ["SparseMoeBlock", "_native"]
+__all__ = ["DenseMLP", "SparseMoeBlock", "_native"]

@@ -25,7 +25,7 @@ CAPI_SYMBOLS = (
     "moe_experts", "moe_route_logits", "moe_last_routing", "moe_device_status",
     "moe_plan_tile_rows", "moe_force_tile_rows", "moe_set_wait_divisor",
     "moe_strerror", "moe_version", "moe_set_norm_weight", "moe_forward_norm",
-    "moe_last_normed",
+    "moe_last_normed", "moe_dense_create", "moe_dense_set_weights", "moe_dense_forward",
 )
 SYNTH_SYMBOLS = (
     "moe_synth_normal", "moe_synth_stream_gate", "moe_synth_stream_bias",
@@ -72,6 +72,9 @@ def lib() -> ctypes.CDLL:
     L.moe_set_norm_weight.argtypes = [_vp, _vp, _i, _vp]
     L.moe_forward_norm.argtypes = [_vp, _vp, _vp, _i, _vp]
     L.moe_last_normed.argtypes = [_vp, _vp, _vp]
+    L.moe_dense_create.argtypes = [_i, _i, _i, ctypes.POINTER(_vp)]
+    L.moe_dense_set_weights.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
+    L.moe_dense_forward.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
     L.moe_plan_tile_rows.argtypes = [_vp, _i]
     L.moe_force_tile_rows.argtypes = [_vp, _i]
     L.moe_set_wait_divisor.argtypes = [_vp, _i]

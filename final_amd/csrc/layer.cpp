@@ -57,8 +57,9 @@ MLP::~MLP() { release_gpu(); }
 MLP::MLP(MLP &&o) noexcept
     : w1_gpu_(o.w1_gpu_), w3_gpu_(o.w3_gpu_), w2_gpu_(o.w2_gpu_),
       temp_buf_gpu_(o.temp_buf_gpu_), w1_(std::move(o.w1_)), w3_(std::move(o.w3_)),
-      w2_(std::move(o.w2_)) {
+      w2_(std::move(o.w2_)), dense_ctx_(o.dense_ctx_), max_tokens_(o.max_tokens_) {
   o.w1_gpu_ = o.w3_gpu_ = o.w2_gpu_ = o.temp_buf_gpu_ = nullptr;
+  o.dense_ctx_ = nullptr;
 }
 
 MLP &MLP::operator=(MLP &&o) noexcept {
@@ -71,7 +72,10 @@ MLP &MLP::operator=(MLP &&o) noexcept {
     w2_gpu_ = o.w2_gpu_;
     w3_gpu_ = o.w3_gpu_;
     temp_buf_gpu_ = o.temp_buf_gpu_;
+    dense_ctx_ = o.dense_ctx_;
+    max_tokens_ = o.max_tokens_;
     o.w1_gpu_ = o.w3_gpu_ = o.w2_gpu_ = o.temp_buf_gpu_ = nullptr;
+    o.dense_ctx_ = nullptr;
   }
   return *this;
 }
@@ -81,27 +85,48 @@ void MLP::release_gpu() {
   if (w2_gpu_) (void)hipFree(w2_gpu_);
   if (w3_gpu_) (void)hipFree(w3_gpu_);
   w1_gpu_ = w2_gpu_ = w3_gpu_ = nullptr;
+  if (dense_ctx_) moe_destroy(dense_ctx_);
+  dense_ctx_ = nullptr;
+}
+
+void MLP::set_max_tokens(int n) {
+  if (dense_ctx_) throw std::logic_error("MLP::set_max_tokens after init_gpu");
+  if (n <= 0) throw std::invalid_argument("MLP::set_max_tokens: n <= 0");
+  max_tokens_ = n;
 }
 
 void MLP::init_gpu() {
   release_gpu();
-  auto up = [](const Tensor &t, float **dst) {
-    check_hip(hipMalloc(reinterpret_cast<void **>(dst), t.size() * sizeof(float)),
-              "hipMalloc");
-    check_hip(hipMemcpy(*dst, t.data(), t.size() * sizeof(float), hipMemcpyHostToDevice),
-              "hipMemcpy");
-  };
-  up(w1_, &w1_gpu_);
-  up(w2_, &w2_gpu_);
-  up(w3_, &w3_gpu_);
+  if (w1_.ndim() != 2 || w3_.shape() != w1_.shape() || w2_.ndim() != 2 ||
+      w2_.shape()[0] != w1_.shape()[1] || w2_.shape()[1] != w1_.shape()[0])
+    throw std::invalid_argument("MLP::init_gpu: w1/w3 must be [I][H] and w2 [H][I]");
+  const int I = (int)w1_.shape()[0], H = (int)w1_.shape()[1];
+  check(moe_dense_create(H, I, max_tokens_, &dense_ctx_), "moe_dense_create");
+  check(moe_dense_set_weights(dense_ctx_, w1_.data(), w3_.data(), w2_.data(), 0, nullptr),
+        "moe_dense_set_weights");
 }
 
-void MLP::forward(const Tensor &, Tensor &) {
-  throw std::logic_error("MLP::forward: the dense FFN is not part of this MoE build");
+void MLP::forward_gpu(float *x, float *y, int batch, int seq_len, int hidden_size,
+                      hipStream_t stream) {
+  if (!dense_ctx_) throw std::logic_error("MLP::forward_gpu before init_gpu");
+  if ((size_t)hidden_size != w1_.shape()[1])
+    throw std::invalid_argument("MLP::forward_gpu: hidden_size mismatch");
+  if (batch < 0 || seq_len < 0) throw std::invalid_argument("negative batch/seq_len");
+  check(moe_dense_forward(dense_ctx_, x, y, nullptr, batch * seq_len, stream), "moe_dense_forward");
 }
 
-void MLP::forward_gpu(float *, float *, int, int, int, hipStream_t) {
-  throw std::logic_error("MLP::forward_gpu: the dense FFN is not part of this MoE build");
+void MLP::forward(const Tensor &x, Tensor &y) {
+  if (!dense_ctx_) throw std::logic_error("MLP::forward before init_gpu");
+  const size_t H = w1_.shape()[1];
+  if (x.ndim() < 1 || x.size() % H != 0)
+    throw std::invalid_argument("MLP::forward: x must be [T][H]");
+  const size_t T = x.size() / H;
+  DevBuf dx(T * H * sizeof(float)), dy(T * H * sizeof(float));
+  check_hip(hipMemcpy(dx.f(), x.data(), T * H * sizeof(float), hipMemcpyHostToDevice), "hipMemcpy");
+  check(moe_dense_forward(dense_ctx_, dx.f(), dy.f(), nullptr, (int)T, nullptr), "moe_dense_forward");
+  y = Tensor({T, H});
+  check_hip(hipMemcpy(y.data(), dy.f(), T * H * sizeof(float), hipMemcpyDeviceToHost), "hipMemcpy");
+  check(moe_device_status(dense_ctx_, nullptr), "device status");
 }
 
 // ---------------------------------------------------------------------------

@@ -51,6 +51,8 @@ struct moe_ctx {
   int wait_div = 1;
   bool weights_set = false;
   bool has_bias = false;
+  bool dense = false;      // dense FFN context (moe_dense_create): kDenseChunks chunk experts
+  int dense_inter = 0;     // its full intermediate size
   bool stream_ok = false;  // streaming kernel compiled for (H, I)
   int max_units = 0;
   int grid[4] = {1, 1, 1, 1};  // plans 0, 32, 64, 128
@@ -129,16 +131,9 @@ const char *moe_strerror(int status) {
 
 const char *moe_version(void) { return "final_amd-moe 0.1.0 gfx950"; }
 
-int moe_create(const moe_dims *dims, moe_ctx **out) {
-  if (!dims || !out) return MOE_ERR_INVALID_ARG;
-  *out = nullptr;
-  const moe_dims d = *dims;
-  if (d.hidden <= 0 || d.inter <= 0 || d.max_tokens <= 0 ||
-      d.max_tokens > kMaxTokensLimit)
-    return MOE_ERR_INVALID_ARG;
-  if (d.num_experts != kExperts || d.top_k != kTopK || d.hidden % 256 != 0 ||
-      d.inter % 256 != 0)
-    return MOE_ERR_UNSUPPORTED;
+// A context with expert weights for e_alloc experts (all kExperts for the
+// MoE block, kDenseChunks for the dense FFN, which has no gate).
+static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **out) {
   moe_ctx *ctx = new (std::nothrow) moe_ctx();
   if (!ctx) return MOE_ERR_OUT_OF_MEMORY;
   ctx->d = d;
@@ -153,6 +148,7 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
   }
   ctx->cus = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 1;
   ctx->stream_ok = stream_supported(d.hidden, d.inter);
+  ctx->dense = dense;
   const size_t H = d.hidden, I = d.inter, E = kExperts;
   const size_t Tm = d.max_tokens, S = Tm * kTopK;
   const size_t nb = (Tm + kMinRouterTokens - 1) / kMinRouterTokens;
@@ -163,10 +159,10 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
     return MOE_ERR_UNSUPPORTED;
   }
   int rc = MOE_OK;
-  if ((rc = dev_alloc(ctx, &ctx->gate, E * H)) ||
-      (rc = dev_alloc(ctx, &ctx->bias, E)) ||
-      (rc = dev_alloc(ctx, &ctx->w13, E * 2 * I * H)) ||
-      (rc = dev_alloc(ctx, &ctx->w2, E * H * I)) ||
+  if ((!dense && (rc = dev_alloc(ctx, &ctx->gate, E * H))) ||
+      (!dense && (rc = dev_alloc(ctx, &ctx->bias, E))) ||
+      (rc = dev_alloc(ctx, &ctx->w13, e_alloc * 2 * I * H)) ||
+      (rc = dev_alloc(ctx, &ctx->w2, e_alloc * H * I)) ||
       (rc = dev_alloc(ctx, &ctx->s.logits, Tm * E)) ||
       (rc = dev_alloc(ctx, &ctx->s.idx, S)) ||
       (rc = dev_alloc(ctx, &ctx->s.wts, S)) ||
@@ -210,6 +206,36 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
   return MOE_OK;
 }
 
+int moe_create(const moe_dims *dims, moe_ctx **out) {
+  if (!dims || !out) return MOE_ERR_INVALID_ARG;
+  *out = nullptr;
+  const moe_dims d = *dims;
+  if (d.hidden <= 0 || d.inter <= 0 || d.max_tokens <= 0 ||
+      d.max_tokens > kMaxTokensLimit)
+    return MOE_ERR_INVALID_ARG;
+  if (d.num_experts != kExperts || d.top_k != kTopK || d.hidden % 256 != 0 ||
+      d.inter % 256 != 0)
+    return MOE_ERR_UNSUPPORTED;
+  return create_ctx(d, kExperts, false, out);
+}
+
+int moe_dense_create(int hidden, int inter, int max_tokens, moe_ctx **out) {
+  if (!out) return MOE_ERR_INVALID_ARG;
+  *out = nullptr;
+  if (hidden <= 0 || inter <= 0 || max_tokens <= 0 || max_tokens > kMaxTokensLimit)
+    return MOE_ERR_INVALID_ARG;
+  if (hidden % 256 != 0 || inter % (kDenseChunks * 256) != 0) return MOE_ERR_UNSUPPORTED;
+  moe_dims d{};
+  d.hidden = hidden;
+  d.inter = inter / kDenseChunks;  // each chunk is one "expert"
+  d.num_experts = kExperts;
+  d.top_k = kTopK;
+  d.max_tokens = max_tokens;
+  const int rc = create_ctx(d, kDenseChunks, true, out);
+  if (rc == MOE_OK) (*out)->dense_inter = inter;
+  return rc;
+}
+
 int moe_destroy(moe_ctx *ctx) {
   if (!ctx) return MOE_OK;
   DeviceGuard g(ctx->device);
@@ -222,7 +248,7 @@ int moe_set_weights(moe_ctx *ctx, const float *gate, const float *bias,
                     const float *const *w1, const float *const *w3,
                     const float *const *w2, int src_on_device,
                     moe_stream_t stream) {
-  if (!ctx || !gate || !w1 || !w3 || !w2) return MOE_ERR_INVALID_ARG;
+  if (!ctx || !gate || !w1 || !w3 || !w2 || ctx->dense) return MOE_ERR_INVALID_ARG;
   for (int e = 0; e < kExperts; ++e)
     if (!w1[e] || !w3[e] || !w2[e]) return MOE_ERR_INVALID_ARG;
   DeviceGuard g(ctx->device);
@@ -297,7 +323,7 @@ static int check_tokens(const moe_ctx *ctx, int T) {
 static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
                     moe_stream_t stream, const float *norm_w = nullptr,
                     float *xn = nullptr) {
-  if (!ctx) return MOE_ERR_INVALID_ARG;
+  if (!ctx || ctx->dense) return MOE_ERR_INVALID_ARG;
   int rc = check_tokens(ctx, T);
   if (rc) return rc;
   if (!ctx->weights_set) return MOE_ERR_NOT_READY;
@@ -380,6 +406,77 @@ int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
                 int num_tokens, moe_stream_t stream) {
   int rc = moe_route(ctx, x, num_tokens, stream);
   if (rc) return rc;
+  return moe_experts(ctx, x, y, residual, num_tokens, stream);
+}
+
+int moe_dense_set_weights(moe_ctx *ctx, const float *w1, const float *w3, const float *w2,
+                          int src_on_device, moe_stream_t stream) {
+  if (!ctx || !ctx->dense || !w1 || !w3 || !w2) return MOE_ERR_INVALID_ARG;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t H = ctx->d.hidden, Ic = ctx->d.inter, I = (size_t)ctx->dense_inter;
+  const hipMemcpyKind kind = src_on_device ? hipMemcpyDeviceToDevice : hipMemcpyHostToDevice;
+  float *stage = nullptr;  // [2][Ic][H] staging of a host chunk
+  if (!src_on_device) {
+    if (hipMalloc(&stage, 2 * Ic * H * sizeof(float)) != hipSuccess) {
+      (void)hipGetLastError();
+      return MOE_ERR_OUT_OF_MEMORY;
+    }
+  }
+  int rc = MOE_OK;
+  for (size_t c = 0; c < (size_t)kDenseChunks && rc == MOE_OK; ++c) {
+    // chunk c: W1/W3 rows [c Ic, (c+1) Ic), W2 columns [c Ic, (c+1) Ic)
+    const float *s1 = w1 + c * Ic * H, *s3 = w3 + c * Ic * H;
+    if (!src_on_device) {
+      if (hipMemcpyAsync(stage, s1, Ic * H * sizeof(float), kind, st) != hipSuccess ||
+          hipMemcpyAsync(stage + Ic * H, s3, Ic * H * sizeof(float), kind, st) != hipSuccess) {
+        rc = MOE_ERR_HIP;
+        break;
+      }
+      s1 = stage;
+      s3 = stage + Ic * H;
+    }
+    if (launch_pack_w13(ctx->w13 + c * 2 * Ic * H, s1, s3, (int)H, (int)Ic, st) != hipSuccess ||
+        hipMemcpy2DAsync(ctx->w2 + c * H * Ic, Ic * sizeof(float), w2 + c * Ic, I * sizeof(float),
+                         Ic * sizeof(float), H, kind, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess) {
+      rc = MOE_ERR_HIP;
+      break;
+    }
+  }
+  if (stage) (void)hipFree(stage);
+  if (rc == MOE_OK) ctx->weights_set = true;
+  return rc;
+}
+
+int moe_dense_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
+                      int num_tokens, moe_stream_t stream) {
+  if (!ctx || !ctx->dense) return MOE_ERR_INVALID_ARG;
+  int rc = check_tokens(ctx, num_tokens);
+  if (rc) return rc;
+  if (!ctx->weights_set) return MOE_ERR_NOT_READY;
+  if (num_tokens == 0) {
+    ctx->routed_T = 0;
+    return MOE_OK;
+  }
+  if (!x || !aligned16(x)) return MOE_ERR_INVALID_ARG;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  RouterArgs a{};
+  a.x = x;
+  a.w.w13 = ctx->w13;
+  a.w.w2 = ctx->w2;
+  a.s = ctx->s;
+  a.T = num_tokens;
+  a.H = ctx->d.hidden;
+  a.inter = ctx->d.inter;
+  a.tile_rows = ctx_plan(ctx, num_tokens);
+  a.bn = expert_bn(a.tile_rows, num_tokens);
+  a.max_units = ctx->max_units;
+  if (launch_router_dense(a, static_cast<hipStream_t>(stream)) != hipSuccess) return MOE_ERR_HIP;
+  ctx->routed_T = num_tokens;
+  ctx->routed_plan = a.tile_rows;
   return moe_experts(ctx, x, y, residual, num_tokens, stream);
 }
 

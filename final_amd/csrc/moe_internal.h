@@ -9,6 +9,7 @@
 namespace moe {
 
 constexpr int kExperts = 32;     // NUM_EXPERTS, reference include/config.h:14
+constexpr int kDenseChunks = 4;  // dense FFN: intermediate cut into 4 chunk "experts"
 constexpr int kTopK = 4;         // NUM_EXPERTS_PER_TOK, config.h:15
 constexpr int kMinRouterTokens = 8;  // smallest token block of the router
 constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
@@ -109,6 +110,9 @@ int router_tokens_per_block(int T);
 bool router_fuses_norm(int T);
 hipError_t launch_rmsnorm(const float *h, const float *w, float *out, int T, int H,
                           hipStream_t st);
+// Fixed routing of the dense FFN (every token to chunks 0..kDenseChunks-1,
+// weight 1) and the plan for it; a.tile_rows/bn/inter as for launch_router.
+hipError_t launch_router_dense(const RouterArgs &a, hipStream_t st);
 // Whether the weight-streaming kernel is compiled for (H, I).
 bool stream_supported(int H, int I);
 // Largest batch the streaming plan handles (its slot -> token map is in LDS).

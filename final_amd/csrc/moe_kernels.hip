@@ -763,6 +763,39 @@ void router_decode_kernel(RouterArgs a) {
   router_plan<kDecRT>(a, nb, T, ps);
 }
 
+// Dense SwiGLU FFN (MLP::forward_gpu, layer.cu:1231-1269) as the block with
+// its intermediate dimension cut into kDenseChunks "experts": every token
+// goes to all of them with weight 1, so the combine adds the chunks' partial
+// down-projections (W2 x = sum over chunks of W2[:, chunk] x[chunk]).  This
+// router writes that fixed routing the way the routers write theirs (ids in
+// rank order, in-block ranks, per-block counts) and plans with router_plan.
+template <int RT>
+__global__ __launch_bounds__(kThreads) void router_dense_kernel(RouterArgs a) {
+  __shared__ PlanShared ps;
+  __shared__ int s_flag;
+  const int tid = threadIdx.x;
+  const int T = a.T, t0 = blockIdx.x * RT;
+  const int nt = min(RT, T - t0);
+  for (int f = tid; f < nt * kTopK; f += kThreads) {
+    const size_t g = (size_t)t0 * kTopK + f;
+    const int k = f % kTopK;
+    st_agent(&a.s.idx[g], k < kDenseChunks ? k : -1);
+    a.s.wts[g] = k < kDenseChunks ? 1.0f : 0.0f;
+    st_agent(&a.s.pos[g], f / kTopK);  // every token of the block chose chunk k
+  }
+  if (tid < kExperts) st_agent(&a.s.blk[(size_t)blockIdx.x * kExperts + tid], tid < kDenseChunks ? nt : 0);
+  const int nb = gridDim.x;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid == 0) {
+    s_flag = nb == 1 || (fetch_add(&a.s.ctrl->router_done, 1) == nb - 1);
+    if (s_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  __syncthreads();
+  if (!s_flag) return;
+  router_plan<RT>(a, nb, T, ps);
+}
+
 // ---------------------------------------------------------------------------
 // Expert kernel building blocks
 // ---------------------------------------------------------------------------
@@ -1888,6 +1921,17 @@ constexpr int kLargeRT = 64, kLargeES = 1, kLargeKC = 64;
 int router_tokens_per_block(int T) { return T <= 64 ? kSmallRT : kLargeRT; }
 
 bool router_fuses_norm(int T) { return T <= 64; }
+
+hipError_t launch_router_dense(const RouterArgs &a, hipStream_t st) {
+  if (a.T <= 64) {
+    const int nb = (a.T + kSmallRT - 1) / kSmallRT;
+    hipLaunchKernelGGL(router_dense_kernel<kSmallRT>, dim3(nb), dim3(kThreads), 0, st, a);
+  } else {
+    const int nb = (a.T + kLargeRT - 1) / kLargeRT;
+    hipLaunchKernelGGL(router_dense_kernel<kLargeRT>, dim3(nb), dim3(kThreads), 0, st, a);
+  }
+  return hipGetLastError();
+}
 
 hipError_t launch_rmsnorm(const float *h, const float *w, float *out, int T, int H, hipStream_t st) {
   if (T <= 0) return hipSuccess;

@@ -172,3 +172,55 @@ class SparseMoeBlock:
             self.close()
         except Exception:
             pass
+
+
+class DenseMLP:
+    """Dense SwiGLU FFN of the first layers (reference MLP::forward_gpu,
+    layer.cu:1231-1269): y = W2 (silu(W1 x) * (W3 x)) [+ residual], on the
+    MoE kernels with the intermediate dimension cut into 4 chunk experts."""
+
+    def __init__(self, hidden: int = 2048, inter: int = 7168, max_tokens: int = 4096):
+        self._ctx = ctypes.c_void_p()
+        _native.check(_native.lib().moe_dense_create(int(hidden), int(inter), int(max_tokens),
+                                                     ctypes.byref(self._ctx)), "moe_dense_create")
+        self.hidden, self.inter, self.max_tokens = hidden, inter, max_tokens
+
+    def set_weights(self, w1, w3, w2, stream=None) -> None:
+        """Host numpy: w1, w3 [I][H], w2 [H][I]."""
+        w1, w3, w2 = (np.ascontiguousarray(a, dtype=np.float32) for a in (w1, w3, w2))
+        _native.check(_native.lib().moe_dense_set_weights(
+            self._ctx, w1.ctypes.data, w3.ctypes.data, w2.ctypes.data, 0, _stream(stream)),
+            "moe_dense_set_weights")
+
+    def forward_gpu(self, x, y, num_tokens: int, residual=None, stream=None) -> None:
+        _native.check(_native.lib().moe_dense_forward(self._ctx, _ptr(x), _ptr(y), _ptr(residual),
+                                                      int(num_tokens), _stream(stream)),
+                      "moe_dense_forward")
+
+    def forward(self, x: np.ndarray, residual: np.ndarray | None = None) -> np.ndarray:
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        T = x.shape[0]
+        dx = hip.DeviceArray.from_numpy(x)
+        dy = hip.DeviceArray((T, self.hidden))
+        dr = hip.DeviceArray.from_numpy(residual) if residual is not None else None
+        self.forward_gpu(dx, dy, T, residual=dr)
+        hip.synchronize()
+        self.check_device()
+        return dy.download()
+
+    def plan(self, num_tokens: int) -> int:
+        return int(_native.lib().moe_plan_tile_rows(self._ctx, int(num_tokens)))
+
+    def check_device(self, stream=None) -> None:
+        _native.check(_native.lib().moe_device_status(self._ctx, _stream(stream)), "device status")
+
+    def close(self) -> None:
+        if self._ctx:
+            _native.lib().moe_destroy(self._ctx)
+            self._ctx = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

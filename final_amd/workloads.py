@@ -38,6 +38,7 @@ class Workload:
     T: int
     seed: int = 0
     bias: str = "normal"  # "normal" | "zipf"
+    kind: str = "moe"     # "moe" | "dense" (the dense FFN of layers 0-1, I = DENSE_I)
 
 
 WORKLOADS = {
@@ -48,7 +49,12 @@ WORKLOADS = {
     "decode_t8": Workload("decode_t8", 8),
     "decode_t64": Workload("decode_t64", 64),
     "decode_t256": Workload("decode_t256", 256),
+    "dense_t1": Workload("dense_t1", 1, kind="dense"),
+    "dense_t64": Workload("dense_t64", 64, kind="dense"),
+    "dense_t4096": Workload("dense_t4096", 4096, kind="dense"),
 }
+
+DENSE_I = 7168  # INTERMEDIATE_SIZE, reference include/config.h:6
 
 
 def normal(seed: int, stream: int, std: float, n: int, first: int = 0) -> np.ndarray:
@@ -78,6 +84,16 @@ def gen_weights(seed: int = 0, h: int = H, inter: int = I, e: int = E,
         L.moe_synth_normal(seed, L.moe_synth_stream_w3(x), WEIGHT_STD, 0, w3[x].ctypes.data, inter * h)
         L.moe_synth_normal(seed, L.moe_synth_stream_w2(x), WEIGHT_STD, 0, w2[x].ctypes.data, h * inter)
     return {"gate": gate, "bias": b, "w1": w1, "w3": w3, "w2": w2}
+
+
+def gen_dense_weights(seed: int = 0, h: int = H, inter: int = DENSE_I) -> dict:
+    """Dense FFN weights N(0, 0.02): w1, w3 [I][H], w2 [H][I], drawn from
+    streams past the 32 experts' (expert ids 32..34 of the same generator)."""
+    L = _native.lib()
+    w1 = normal(seed, L.moe_synth_stream_w1(E), WEIGHT_STD, inter * h).reshape(inter, h)
+    w3 = normal(seed, L.moe_synth_stream_w3(E + 1), WEIGHT_STD, inter * h).reshape(inter, h)
+    w2 = normal(seed, L.moe_synth_stream_w2(E + 2), WEIGHT_STD, h * inter).reshape(h, inter)
+    return {"w1": w1, "w3": w3, "w2": w2}
 
 
 def gen_x(T: int, seed: int = 0, h: int = H, e: int = E) -> np.ndarray:

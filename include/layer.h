@@ -29,15 +29,21 @@ public:
   MLP(const MLP &) = delete;
   MLP &operator=(const MLP &) = delete;
 
-  // Dense FFN path of layers 0-1 (layer.cu:1231-1269): not part of this
-  // build; both throw std::logic_error.
+  // Dense FFN of layers 0-1 (layer.cu:1231-1269): y = W2 (silu(W1 x) * (W3 x))
+  // on the MoE kernels (moe_dense_*, include/moe_capi.h).  forward: host
+  // tensors x [T][H] -> y [T][H] (synchronous); forward_gpu: device pointers,
+  // asynchronous on stream.  Both need init_gpu.
   void forward(const Tensor &x, Tensor &y);
   void forward_gpu(float *x, float *y, int batch, int seq_len, int hidden_size,
                    hipStream_t stream = 0);
 
-  // Uploads w1/w2/w3 as separate device buffers (layer.cu:1216-1228).  The MoE
-  // block does not need it: it uploads the experts itself.
+  // Uploads the weights for forward_gpu (layer.cu:1216-1228): a dense context
+  // with its own scratch for max_tokens() tokens.  The MoE block does not call
+  // it: it uploads its experts itself.  w1_gpu_/w2_gpu_/w3_gpu_ stay null (the
+  // weights live repacked inside the context).
   void init_gpu();
+  void set_max_tokens(int n);  // before init_gpu (default 4096, layer.cu:1399)
+  int max_tokens() const { return max_tokens_; }
 
   const Tensor &w1() const { return w1_; }
   const Tensor &w2() const { return w2_; }
@@ -52,6 +58,8 @@ private:
   Tensor w1_;  // [I][H]
   Tensor w3_;  // [I][H]
   Tensor w2_;  // [H][I]
+  moe_ctx *dense_ctx_ = nullptr;
+  int max_tokens_ = 4096;
   void release_gpu();
 };
 

@@ -103,6 +103,27 @@ int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
 int moe_route_logits(moe_ctx *ctx, const float *logits, int num_tokens,
                      moe_stream_t stream);
 
+/* Dense SwiGLU FFN of the first NUM_DENSE_LAYERS layers (config.h:16;
+ * MLP::forward_gpu, layer.cu:1231-1269, INTERMEDIATE_SIZE = 7168):
+ * y = W2 (silu(W1 x) * (W3 x)) [+ residual].  Replaces MLP::init_gpu
+ * (layer.cu:1216-1228) and its missing scratch (the reference never allocates
+ * temp_buf_gpu_, layer.cu:1237).  The context runs the MoE kernels with the
+ * intermediate dimension cut into 4 chunks, every token sent to all four with
+ * weight 1: hidden % 256 == 0 and inter % 1024 == 0 (inter / 4 == 1792 at
+ * hidden 2048 gets the weight-streaming kernel for small batches).  Release
+ * with moe_destroy.  moe_forward / moe_route / moe_set_weights reject a dense
+ * context and moe_dense_* reject a MoE context. */
+int moe_dense_create(int hidden, int inter, int max_tokens, moe_ctx **out);
+/* w1, w3 [inter][hidden], w2 [hidden][inter] (MLP's w1/w3/w2 tensors,
+ * layer.cu:1199-1204); host memory when src_on_device == 0.  Synchronises
+ * `stream`. */
+int moe_dense_set_weights(moe_ctx *ctx, const float *w1, const float *w3, const float *w2,
+                          int src_on_device, moe_stream_t stream);
+/* x, y, residual (may be NULL): device [num_tokens][hidden]; y may alias
+ * residual but not x.  Asynchronous on `stream`. */
+int moe_dense_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
+                      int num_tokens, moe_stream_t stream);
+
 /* The post-attention RMSNorm weight [hidden] of the decoder layer that owns
  * this block (RMSNorm post_attention_layernorm_, layer.cu:1793, weight
  * layers.{i}.post_attention_layernorm.weight; RMSNorm::init_gpu uploads it,

@@ -337,6 +337,36 @@ void orc_combine(const float *sorted_out, const int *pos, const float *w,
 }
 
 /* ------------------------------------------------------------------------ */
+/* dense FFN (MLP::forward_gpu, layer.cu:1231-1269)                          */
+/* ------------------------------------------------------------------------ */
+
+float orc_silu_dexp(float x) { return x / (1.0f + (float)exp(-(double)x)); }
+
+int orc_dense_mlp(const float *x, const float *w1, const float *w3, const float *w2,
+                  const float *residual, int64_t T, int H, int I, float *y) {
+  if (T <= 0) return 0;
+  float *gate = (float *)malloc(sizeof(float) * (size_t)(T * I));
+  float *up = (float *)malloc(sizeof(float) * (size_t)(T * I));
+  if (!gate || !up) {
+    free(gate);
+    free(up);
+    return -1;
+  }
+  orc_gemm_nt_chain(x, T, w1, I, H, gate); /* layer.cu:1250-1251 */
+  orc_gemm_nt_chain(x, T, w3, I, H, up);   /* layer.cu:1254-1255 */
+#ifdef _OPENMP
+#pragma omp parallel for schedule(static) num_threads(orc_get_threads())
+#endif
+  for (int64_t i = 0; i < T * I; ++i) gate[i] = orc_silu_dexp(gate[i]) * up[i]; /* layer.cu:679-682 */
+  orc_gemm_nt_chain(gate, T, w2, H, I, y);  /* layer.cu:1266-1268 */
+  if (residual)
+    for (int64_t i = 0; i < T * H; ++i) y[i] = residual[i] + y[i];
+  free(gate);
+  free(up);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* post-attention RMSNorm (layer.cu:144-193)                                 */
 /* ------------------------------------------------------------------------ */
 

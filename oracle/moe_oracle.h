@@ -89,6 +89,21 @@ void orc_expert_w2(const float *inter, int64_t M, const float *w2, int H, int I,
 void orc_combine(const float *sorted_out, const int *pos, const float *w,
                  const float *residual, int64_t T, int H, float *y);
 
+/* d_silu, layer.cu:436: x / (1.0f + (float)exp(-(double)x)), the SwiGLU of
+ * the dense FFN (moe_swiglu_kernel layer.cu:670-691; the experts use
+ * d_silu_opt, orc_silu). */
+float orc_silu_dexp(float x);
+
+/* Dense SwiGLU FFN, MLP::forward_gpu layer.cu:1231-1269 (I = 7168 in the
+ * reference): gate = x W1^T and up = x W3^T (attn_matmul_tiled_kernel: one
+ * fmaf chain per output over k ascending, layer.cu:109-127), inter =
+ * d_silu(gate) * up (moe_swiglu_kernel layer.cu:670-691), y = inter W2^T
+ * (the same chains over I), then y = residual + y (add_kernel layer.cu:1860-1880
+ * as at layer.cu:1917) when residual != NULL.  x [T][H], w1/w3 [I][H],
+ * w2 [H][I], y [T][H].  Returns 0, or -1 on allocation failure. */
+int orc_dense_mlp(const float *x, const float *w1, const float *w3, const float *w2,
+                  const float *residual, int64_t T, int H, int I, float *y);
+
 /* Post-attention RMSNorm, rms_norm_kernel layer.cu:144-193 as launched by
  * RMSNorm::forward_gpu layer.cu:1144-1148 (one block of 256 threads per row,
  * warpSize 32).  Restated in the kernel's exact order: thread t (0..255)

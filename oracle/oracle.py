@@ -57,6 +57,10 @@ def lib():
         L.orc_expert_w2.argtypes = [_f32p, _i64, _f32p, ctypes.c_int, ctypes.c_int, _f32p]
         L.orc_combine.argtypes = [_f32p, _i32p, _f32p, _f32p, _i64, ctypes.c_int, _f32p]
         L.orc_rmsnorm.argtypes = [_f32p, _f32p, _i64, ctypes.c_int, _f32p]
+        L.orc_silu_dexp.argtypes = [ctypes.c_float]
+        L.orc_silu_dexp.restype = ctypes.c_float
+        L.orc_dense_mlp.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _i64, ctypes.c_int,
+                                    ctypes.c_int, _f32p]
         L.orc_moe_forward.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
                                       _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       _u8p, _f32p, _f32p, _i32p, _f32p, _i32p]
@@ -156,6 +160,33 @@ def combine(sorted_out, pos, w, residual=None):
     H = sorted_out.shape[1]
     y = np.empty((T, H), np.float32)
     lib().orc_combine(_f(sorted_out), _i(pos), _f(w), _f(residual), T, H, _f(y))
+    return y
+
+
+def silu_dexp(v: float) -> float:
+    return float(lib().orc_silu_dexp(v))
+
+
+def dense_mlp(x, w1, w3, w2, residual=None, token_mask=None):
+    """Dense SwiGLU FFN (MLP::forward_gpu, layer.cu:1231-1269).  x [T][H],
+    w1/w3 [I][H], w2 [H][I].  Rows of unselected tokens are NaN."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    T, H = x.shape
+    I = w1.shape[0]
+    y = np.full((T, H), np.nan, np.float32)
+    sel = np.arange(T) if token_mask is None else np.nonzero(np.asarray(token_mask))[0]
+    if len(sel) == 0:
+        return y
+    xs = np.ascontiguousarray(x[sel])
+    rs = None if residual is None else np.ascontiguousarray(np.asarray(residual, np.float32)[sel])
+    ys = np.empty((len(sel), H), np.float32)
+    rc = lib().orc_dense_mlp(_f(xs), _f(np.ascontiguousarray(w1, dtype=np.float32)),
+                             _f(np.ascontiguousarray(w3, dtype=np.float32)),
+                             _f(np.ascontiguousarray(w2, dtype=np.float32)), _f(rs),
+                             len(sel), H, I, _f(ys))
+    if rc != 0:
+        raise RuntimeError("orc_dense_mlp failed")
+    y[sel] = ys
     return y
 
 

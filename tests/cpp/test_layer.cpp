@@ -274,6 +274,31 @@ void gpu_tests() {
       std::printf("gpu norm T=%d ok\n", T);
     }
   }
+  // dense FFN (MLP::forward_gpu, layer.cu:1231-1269) on the MoE kernels
+  {
+    constexpr int kDI = 1024;  // the intermediate must split into 4 chunks of 256
+    std::mt19937 rng(9);
+    std::vector<float> w1 = normal(rng, (size_t)kDI * kH, 0.05f),
+                       w3 = normal(rng, (size_t)kDI * kH, 0.05f),
+                       w2 = normal(rng, (size_t)kH * kDI, 0.05f);
+    MLP dense(Tensor({(size_t)kDI, (size_t)kH}, w1.data(), true),
+              Tensor({(size_t)kH, (size_t)kDI}, w2.data(), true),
+              Tensor({(size_t)kDI, (size_t)kH}, w3.data(), true));
+    CHECK(throws([&] { dense.forward_gpu(nullptr, nullptr, 1, 1, kH, 0); }));  // before init_gpu
+    dense.set_max_tokens(256);
+    dense.init_gpu();
+    for (int T : {1, 24, 200}) {
+      std::vector<float> x = normal(rng, (size_t)T * kH, 1.0f), yref((size_t)T * kH);
+      CHECK(orc_dense_mlp(x.data(), w1.data(), w3.data(), w2.data(), nullptr, T, kH, kDI,
+                          yref.data()) == 0);
+      Tensor tx({(size_t)T, (size_t)kH}, x.data(), true), ty;
+      dense.forward(tx, ty);
+      int bad = 0;
+      for (size_t i = 0; i < yref.size(); ++i) bad += !close(ty.data()[i], yref[i]);
+      CHECK(bad == 0);
+      std::printf("gpu dense T=%d ok\n", T);
+    }
+  }
   // route_tokens on crafted logits (equal logits, large margins) vs the oracle
   Tensor lt({3, (size_t)kE});
   lt.zero();

@@ -507,3 +507,62 @@ def test_moe_forward_norm_is_norm_then_block(oracle_mod):
     assert np.array_equal(r["xn"], xn)
     assert np.array_equal(r["y"], r2["y"])
     assert np.array_equal(r["idx"], r2["idx"])
+
+
+# ---------------------------------------------------------------------------
+# Dense SwiGLU FFN (MLP::forward_gpu, layer.cu:1231-1269)
+# ---------------------------------------------------------------------------
+
+def test_silu_dexp_within_three_roundings(oracle_mod):
+    """d_silu (layer.cu:436): exp in double, then three float roundings (the
+    cast, 1.0f + e, the quotient), each at most 2^-24 relative: within
+    3 * 2^-24 (plus double-rounding slack) of float64 silu; exact at 0."""
+    xs = np.concatenate([np.linspace(-30, 30, 2001), [0.0, -1e-30, 1e-30, 88.0, -88.0]])
+    for x in xs.astype(np.float32):
+        got = np.float32(oracle_mod.silu_dexp(float(x)))
+        ref = float(x) / (1.0 + math.exp(-float(x)))
+        assert abs(float(got) - ref) <= 3.01 * 2.0 ** -24 * abs(ref) + 1e-45, (x, got, ref)
+    assert oracle_mod.silu_dexp(0.0) == 0.0
+
+
+def test_dense_mlp_matches_float64(oracle_mod):
+    """Small shapes: within float32 accumulation error of the float64 SwiGLU
+    MLP, with silu on the W1 branch (a W1/W3 swap would fail) and the
+    residual added last."""
+    rng = np.random.RandomState(11)
+    T, H, I = 5, 64, 256
+    x = rng.randn(T, H).astype(np.float32)
+    w1 = (0.2 * rng.randn(I, H)).astype(np.float32)
+    w3 = (0.2 * rng.randn(I, H)).astype(np.float32)
+    w2 = (0.2 * rng.randn(H, I)).astype(np.float32)
+    r = rng.randn(T, H).astype(np.float32)
+    y = oracle_mod.dense_mlp(x, w1, w3, w2, residual=r)
+    x64, w164, w364, w264 = (a.astype(np.float64) for a in (x, w1, w3, w2))
+    g = x64 @ w164.T
+    u = x64 @ w364.T
+    ref = (g / (1.0 + np.exp(-g)) * u) @ w264.T + r
+    np.testing.assert_allclose(y, ref, rtol=2e-5, atol=2e-5)
+    swapped = oracle_mod.dense_mlp(x, w3, w1, w2, residual=r)
+    assert np.abs(swapped - ref).max() > 1e-2
+    # rows are independent: a token mask computes the selected rows only
+    m = np.array([1, 0, 1, 0, 0], np.uint8)
+    ym = oracle_mod.dense_mlp(x, w1, w3, w2, residual=r, token_mask=m)
+    assert np.array_equal(ym[m.astype(bool)], y[m.astype(bool)])
+    assert np.isnan(ym[~m.astype(bool)]).all()
+
+
+def test_dense_mlp_is_chained_gemms(oracle_mod):
+    """The three products are the pinned fma chains (gemm_nt_chain), the
+    SwiGLU is d_silu(gate) * up elementwise."""
+    rng = np.random.RandomState(12)
+    T, H, I = 3, 32, 64
+    x = rng.randn(T, H).astype(np.float32)
+    w1 = (0.3 * rng.randn(I, H)).astype(np.float32)
+    w3 = (0.3 * rng.randn(I, H)).astype(np.float32)
+    w2 = (0.3 * rng.randn(H, I)).astype(np.float32)
+    gate = oracle_mod.gemm_nt_chain(x, w1)
+    up = oracle_mod.gemm_nt_chain(x, w3)
+    inter = np.array([[np.float32(oracle_mod.silu_dexp(float(g))) * u for g, u in zip(gr, ur)]
+                      for gr, ur in zip(gate, up)], np.float32)
+    want = oracle_mod.gemm_nt_chain(inter, w2)
+    assert np.array_equal(bits(oracle_mod.dense_mlp(x, w1, w3, w2)), bits(want))
