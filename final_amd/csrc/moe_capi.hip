@@ -472,7 +472,7 @@ int moe_dense_forward(moe_ctx *ctx, const float *x, float *y, const float *resid
   a.H = ctx->d.hidden;
   a.inter = ctx->d.inter;
   a.tile_rows = ctx_plan(ctx, num_tokens);
-  a.bn = expert_bn(a.tile_rows, num_tokens);
+  a.bn = a.tile_rows == 0 ? stream_rows_dense(num_tokens) : expert_bn(a.tile_rows, num_tokens);
   a.max_units = ctx->max_units;
   if (launch_router_dense(a, static_cast<hipStream_t>(stream)) != hipSuccess) return MOE_ERR_HIP;
   ctx->routed_T = num_tokens;

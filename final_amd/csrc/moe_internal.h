@@ -122,5 +122,8 @@ int expert_blocks_per_cu(int tile_rows);
 // Columns of the B tile of the MFMA kernel, or weight rows per task of the
 // streaming kernel, for a plan and batch size.
 int expert_bn(int tile_rows, int T);
+// Weight rows per streaming task for the dense FFN, whose chunks all hold T
+// tokens: 32-row tasks with 4 token passes above 32 tokens.
+int stream_rows_dense(int T);
 
 }  // namespace moe

@@ -1816,6 +1816,10 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
 // load-return path, so the kernel picks the count from the plan at run time.
 constexpr int kRingMaxPasses = 2;
 constexpr int kRingWideGroups = 4;  // row groups of a 64-row task
+// 32-row tasks with 4 passes: batches where every expert holds up to 64
+// tokens (the dense FFN's chunks hold all of them); 64-row tasks with 4
+// passes would need twice the LDS for their partials.
+constexpr int kRingDenseGroups = 2, kRingDensePasses = 4;
 
 // LDS of the partials: [2][kRingWaves][row groups][passes][16][16]
 constexpr size_t ring_res_bytes(int rg, int p) {
@@ -1870,7 +1874,8 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   // plans for this kernel take their slots from the router, every block
   // needs a ready line, and a task covers 16 or 64 rows
   if (c->n_rblocks != 0 || (int)gridDim.x > kReadyLines ||
-      (pl.rows != kStreamRows && pl.rows != kStreamRows * kRingWideGroups)) {
+      (pl.rows != kStreamRows && pl.rows != kStreamRows * kRingWideGroups &&
+       pl.rows != kStreamRows * kRingDenseGroups)) {
     if (tid == 0) st_agent(&a.s.ctrl->err, 2);
     return;
   }
@@ -1882,9 +1887,11 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   if (pl.rows == kStreamRows) {
     if (maxcnt <= kRingTokens) ring_role<1, 1>(a, sh, res, pl, ticks);
     else ring_role<1, kRingMaxPasses>(a, sh, res, pl, ticks);
-  } else {
+  } else if (pl.rows == kStreamRows * kRingWideGroups) {
     if (maxcnt <= kRingTokens) ring_role<kRingWideGroups, 1>(a, sh, res, pl, ticks);
     else ring_role<kRingWideGroups, kRingMaxPasses>(a, sh, res, pl, ticks);
+  } else {
+    ring_role<kRingDenseGroups, kRingDensePasses>(a, sh, res, pl, ticks);
   }
 }
 
@@ -1968,7 +1975,9 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
 }
 
 static size_t stream_lds_bytes() {
-  return ring_res_bytes(kRingWideGroups, kRingMaxPasses);  // the largest variant
+  const size_t a = ring_res_bytes(kRingWideGroups, kRingMaxPasses),
+               b = ring_res_bytes(kRingDenseGroups, kRingDensePasses);
+  return a > b ? a : b;
 }
 
 static const void *stream_fn(int H, int I) {
@@ -2033,6 +2042,10 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+int stream_rows_dense(int T) {
+  return T > 2 * kRingTokens ? kStreamRows * kRingDenseGroups : expert_bn(0, T);
 }
 
 int expert_bn(int tile_rows, int T) {

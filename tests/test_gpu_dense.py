@@ -39,7 +39,7 @@ def mlp(dense_weights):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T", [1, 8, 31, 32, 64, 100, 1000])
+@pytest.mark.parametrize("T", [1, 8, 31, 32, 48, 64, 100, 1000])
 def test_dense_matches_oracle(T, mlp, dense_weights, oracle_mod):
     from final_amd import workloads as W
     say(f"[dense] T={T} plan={mlp.plan(T)}")
