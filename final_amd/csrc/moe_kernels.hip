@@ -1031,16 +1031,18 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
   const int wrows = min(max(rows_valid - wrow0, 0), WM * 32);
 
   const int nslab = K / BK;
+  // Global loads run two slabs ahead in two register sets: slab s + 2 is
+  // loaded while slab s's MFMAs run, and slab s + 1 (loaded a whole slab
+  // earlier) is written to LDS after them.
+  f32x4 ra2[A_PER], rb2[B_PER];
   slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra, rb, a_src, abase, bsrc, K, 0);
+  if (nslab > 1) slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra2, rb2, a_src, abase, bsrc, K, BK);
   slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(ra, rb, As, Bs, lds_st, lrow);
   __syncthreads();
   const int lr = lane & 31, lh = (lane >> 5) * 4;
   const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
   const float *b_rd = Bs + (wn * 64 + lr) * PITCH + lh;
-  for (int s = 0; s < nslab; ++s) {
-    const int cur = s & 1;
-    if (s + 1 < nslab)
-      slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra, rb, a_src, abase, bsrc, K, (s + 1) * BK);
+  auto mfma_slab = [&](int cur) {
     const float *Ac = a_rd + cur * BM * PITCH;
     const float *Bc = b_rd + cur * TL::BN * PITCH;
     if (wrows > 0) {
@@ -1063,9 +1065,24 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
         }
       }
     }
+  };
+  // two slabs per iteration so each register set has a fixed name
+  for (int s = 0; s < nslab; s += 2) {
+    // slab s from LDS buffer 0; slab s + 1 sits in (ra2, rb2)
+    if (s + 2 < nslab)
+      slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra, rb, a_src, abase, bsrc, K, (s + 2) * BK);
+    mfma_slab(0);
     if (s + 1 < nslab)
       slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(
-          ra, rb, As + (cur ^ 1) * BM * PITCH, Bs + (cur ^ 1) * TL::BN * PITCH, lds_st, lrow);
+          ra2, rb2, As + BM * PITCH, Bs + TL::BN * PITCH, lds_st, lrow);
+    __syncthreads();
+    if (s + 1 >= nslab) break;
+    // slab s + 1 from LDS buffer 1; slab s + 2 sits in (ra, rb)
+    if (s + 3 < nslab)
+      slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra2, rb2, a_src, abase, bsrc, K, (s + 3) * BK);
+    mfma_slab(1);
+    if (s + 2 < nslab)
+      slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(ra, rb, As, Bs, lds_st, lrow);
     __syncthreads();
   }
 
