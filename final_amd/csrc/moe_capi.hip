@@ -153,8 +153,9 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
   const size_t Tm = d.max_tokens, S = Tm * kTopK;
   const size_t nb = (Tm + kMinRouterTokens - 1) / kMinRouterTokens;
   ctx->max_units = (int)(S / 32 + E + 1);
-  // inter and sout are addressed with 32-bit byte offsets
-  if (S * (H > I ? H : I) * sizeof(float) >= 0xFFFFFFF0ull) {
+  // inter and sout are addressed with 32-bit byte offsets, and the MFMA
+  // tiles use offsets from 0xFF000000 up as out-of-range (zero) loads
+  if (S * (H > I ? H : I) * sizeof(float) >= 0xFF000000ull) {
     delete ctx;
     return MOE_ERR_UNSUPPORTED;
   }

@@ -954,21 +954,27 @@ template <int BM> struct Tile {
   static_assert(BK % 8 == 0, "k groups of 8");
 };
 
-// Slab staging of the MFMA tile: global float4 loads into registers (A rows
-// gathered, a_src < 0 = zero row; B rows contiguous with stride K), then LDS
-// stores.  Fully unrolled with compile-time indices so the arrays stay in
-// registers while the loads are in flight.
+// Slab staging of the MFMA tile: buffer float4 loads into registers (A rows
+// gathered; an empty row's offset lies past the buffer, so its loads return
+// zeros without a branch; B rows contiguous with stride K), then LDS stores.
+// Every load is unconditional, so the compiler's count of loads in flight
+// stays exact and a slab's LDS stores wait only for that slab.  Fully
+// unrolled with compile-time indices so the arrays stay in registers while
+// the loads are in flight.
+constexpr uint32_t kTileOOB = 0xFF000000u;  // past every A buffer (moe_create bounds them)
+
 template <int A_PER, int B_PER, int RPP>
 __device__ __forceinline__ void slab_load(f32x4 (&ra)[A_PER], f32x4 (&rb)[B_PER],
-                                          const int (&a_src)[A_PER], const float *abase,
-                                          const float *bsrc, int K, int k0) {
+                                          const uint32_t (&a_off)[A_PER],
+                                          __amdgpu_buffer_rsrc_t ar, uint32_t b_off,
+                                          __amdgpu_buffer_rsrc_t br, int K, int k0) {
 #pragma unroll
-  for (int i = 0; i < A_PER; ++i) {
-    const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-    ra[i] = a_src[i] >= 0 ? ld4(abase + a_src[i] + k0) : zero;
-  }
+  for (int i = 0; i < A_PER; ++i)
+    ra[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, a_off[i] + k0 * 4u, 0, 0));
 #pragma unroll
-  for (int i = 0; i < B_PER; ++i) rb[i] = ld4(bsrc + (size_t)i * RPP * K + k0);
+  for (int i = 0; i < B_PER; ++i)
+    rb[i] = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(br, b_off + (uint32_t)(i * RPP * K + k0) * 4u, 0, 0));
 }
 
 template <int BM, int A_PER, int B_PER, int RPP, int PITCH>
@@ -982,16 +988,19 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
   for (int i = 0; i < B_PER; ++i) st4(Bs + lds_st + i * RPP * PITCH, rb[i]);
 }
 
+// Slabs of global loads in flight ahead of the MFMAs (register sets).
+constexpr int kTilePrefetch = 3;
+
 // One output tile of C[rows][cols] = A[rows][K] . B[cols][K]^T.
 // A rows are gathered: row r starts at abase + aoff[r] (aoff in LDS; rows at
-// or past rows_valid are zero).  B rows are contiguous with stride K from
-// brow0.  GATED: per wave the B tile holds 32 rows of W1 then the same 32 of
+// or past rows_valid are zero; abytes = bytes readable from abase).  B rows
+// are contiguous with stride K from brow0.  GATED: per wave the B tile holds 32 rows of W1 then the same 32 of
 // W3 and the epilogue writes silu(W1 x) * (W3 x); otherwise the product.
 //
 // Slab pipeline: global loads of slab s+1 are in flight while the MFMAs of
 // slab s run from LDS; one barrier per slab (double-buffered LDS).
 template <int BM, bool GATED>
-__device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
+__device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32_t abytes,
                                           const int *aoff, int rows_valid,
                                           const float *brow0, int K, const AgentOut &out,
                                           int row0, int ldo, int col0) {
@@ -1007,13 +1016,22 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
   const int wm = wave % TL::WAVES_M, wn = wave / TL::WAVES_M;
   const int lrow = tid / KV, lc4 = (tid % KV) * 4;
 
-  int a_src[A_PER];  // element offset of this thread's A float4, -1 = zero
+  uint32_t a_src[A_PER];  // byte offset of this thread's A float4 (kTileOOB: zero row)
 #pragma unroll
   for (int i = 0; i < A_PER; ++i) {
     const int r = lrow + i * ROWS_PER_PASS;
-    a_src[i] = (r < BM && r < rows_valid) ? aoff[r] + lc4 : -1;
+    a_src[i] = (r < BM && r < rows_valid) ? (uint32_t)(aoff[r] + lc4) * 4u : kTileOOB;
   }
-  const float *bsrc = brow0 + (size_t)lrow * K + lc4;
+  const __amdgpu_buffer_rsrc_t abase_r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(abase), 0, (int)abytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t bsrc_r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(brow0), 0, (int)((uint32_t)TL::BN * K * 4u), kBufferRsrcWord3);
+  // loads past the last slab use descriptors of size 0 (zeros, no traffic):
+  // every load and LDS store of the loop is unconditional, which keeps the
+  // compiler's count of loads in flight exact across the loop
+  const __amdgpu_buffer_rsrc_t none_r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(brow0), 0, 0, kBufferRsrcWord3);
+  const uint32_t bsrc = (uint32_t)(lrow * K + lc4) * 4u;
   const int lds_st = lrow * PITCH + lc4;
 
   f32x4 ra[A_PER], rb[B_PER];
@@ -1031,59 +1049,62 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase,
   const int wrows = min(max(rows_valid - wrow0, 0), WM * 32);
 
   const int nslab = K / BK;
-  // Global loads run two slabs ahead in two register sets: slab s + 2 is
-  // loaded while slab s's MFMAs run, and slab s + 1 (loaded a whole slab
-  // earlier) is written to LDS after them.
-  f32x4 ra2[A_PER], rb2[B_PER];
-  slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra, rb, a_src, abase, bsrc, K, 0);
-  if (nslab > 1) slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra2, rb2, a_src, abase, bsrc, K, BK);
-  slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(ra, rb, As, Bs, lds_st, lrow);
+  // Global loads run kPrefetch slabs ahead in kPrefetch register sets: slab
+  // t + kPrefetch is loaded while slab t's MFMAs run, and slab t + 1 (loaded
+  // kPrefetch - 1 slabs earlier) is written to LDS after them.
+  constexpr int NS = kTilePrefetch;
+  constexpr int L = NS % 2 == 0 ? NS : 2 * NS;  // steps per unrolled round
+  f32x4 sa[NS][A_PER], sb[NS][B_PER];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const bool in = j < nslab;
+    slab_load<A_PER, B_PER, ROWS_PER_PASS>(sa[j], sb[j], a_src, in ? abase_r : none_r, bsrc,
+                                           in ? bsrc_r : none_r, K, in ? j * BK : 0);
+  }
+  slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(sa[0], sb[0], As, Bs, lds_st, lrow);
   __syncthreads();
   const int lr = lane & 31, lh = (lane >> 5) * 4;
   const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
   const float *b_rd = Bs + (wn * 64 + lr) * PITCH + lh;
-  auto mfma_slab = [&](int cur) {
-    const float *Ac = a_rd + cur * BM * PITCH;
-    const float *Bc = b_rd + cur * TL::BN * PITCH;
-    if (wrows > 0) {
+  for (int s = 0; s < nslab; s += L) {
 #pragma unroll
-      for (int g8 = 0; g8 < BK / 8; ++g8) {
-        f32x4 af[WM], bf[2];
+    for (int u = 0; u < L; ++u) {
+      const int t = s + u;
+      if (t >= nslab) break;
+      // the set of slab t is free (written to LDS a step ago): slab t + NS
+      {
+        const bool in = t + NS < nslab;
+        slab_load<A_PER, B_PER, ROWS_PER_PASS>(sa[u % NS], sb[u % NS], a_src, in ? abase_r : none_r,
+                                               bsrc, in ? bsrc_r : none_r, K, in ? (t + NS) * BK : 0);
+      }
+      const float *Ac = a_rd + (u & 1) * BM * PITCH;
+      const float *Bc = b_rd + (u & 1) * TL::BN * PITCH;
+      if (wrows > 0) {
 #pragma unroll
-        for (int i = 0; i < WM; ++i) af[i] = ld4(Ac + i * 32 * PITCH + g8 * 8);
+        for (int g8 = 0; g8 < BK / 8; ++g8) {
+          f32x4 af[WM], bf[2];
 #pragma unroll
-        for (int c = 0; c < 2; ++c) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
+          for (int i = 0; i < WM; ++i) af[i] = ld4(Ac + i * 32 * PITCH + g8 * 8);
 #pragma unroll
-        for (int i = 0; i < WM; ++i) {
-          if (i > 0 && wrows <= 32) break;
+          for (int c = 0; c < 2; ++c) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
 #pragma unroll
-          for (int c = 0; c < 2; ++c) {
+          for (int i = 0; i < WM; ++i) {
+            if (i > 0 && wrows <= 32) break;
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[c][q], acc[i][c], 0, 0, 0);
+            for (int c = 0; c < 2; ++c) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[c][q], acc[i][c], 0, 0, 0);
+            }
           }
         }
       }
-    }
-  };
-  // two slabs per iteration so each register set has a fixed name
-  for (int s = 0; s < nslab; s += 2) {
-    // slab s from LDS buffer 0; slab s + 1 sits in (ra2, rb2)
-    if (s + 2 < nslab)
-      slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra, rb, a_src, abase, bsrc, K, (s + 2) * BK);
-    mfma_slab(0);
-    if (s + 1 < nslab)
+      // slab t + 1 (past the end: zeros into a buffer nobody reads again)
       slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(
-          ra2, rb2, As + BM * PITCH, Bs + TL::BN * PITCH, lds_st, lrow);
-    __syncthreads();
-    if (s + 1 >= nslab) break;
-    // slab s + 1 from LDS buffer 1; slab s + 2 sits in (ra, rb)
-    if (s + 3 < nslab)
-      slab_load<A_PER, B_PER, ROWS_PER_PASS>(ra2, rb2, a_src, abase, bsrc, K, (s + 3) * BK);
-    mfma_slab(1);
-    if (s + 2 < nslab)
-      slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(ra, rb, As, Bs, lds_st, lrow);
-    __syncthreads();
+          sa[(u + 1) % NS], sb[(u + 1) % NS], As + ((u + 1) & 1) * BM * PITCH,
+          Bs + ((u + 1) & 1) * TL::BN * PITCH, lds_st, lrow);
+      __syncthreads();
+    }
   }
 
   // Epilogue through LDS (the slab buffers are free after the last barrier):
@@ -1161,8 +1182,8 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
       __syncthreads();
       const float *brow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TL::BN) * H;
-      mfma_tile<BM, true>(lds, a.x, s_aoff, rows, brow0, H, inter_out, slot0, I,
-                          nt * (TL::BN / 2));
+      mfma_tile<BM, true>(lds, a.x, (uint32_t)((size_t)a.T * H * sizeof(float)), s_aoff, rows,
+                          brow0, H, inter_out, slot0, I, nt * (TL::BN / 2));
       block_signal(&a.s.dep[u]);
     } else if (task < nb + n1 + n2) {
       const int q = task - nb - n1;
@@ -1175,8 +1196,9 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (tid < BM) s_aoff[tid] = tid < rows ? tid * I : -1;
       __syncthreads();
       const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
-      mfma_tile<BM, false>(lds, a.s.inter + (size_t)slot0 * I, s_aoff, rows, brow0, I,
-                           sout_out, slot0, H, ht * TL::BN);
+      mfma_tile<BM, false>(lds, a.s.inter + (size_t)slot0 * I,
+                           a.s.inter_bytes - (uint32_t)((size_t)slot0 * I * sizeof(float)), s_aoff,
+                           rows, brow0, I, sout_out, slot0, H, ht * TL::BN);
       block_signal(&c->p2_done);
     } else {
       const int q = task - nb - n1 - n2;
