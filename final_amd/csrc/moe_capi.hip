@@ -58,6 +58,7 @@ struct moe_ctx {
   int grid[4] = {1, 1, 1, 1};  // plans 0, 32, 64, 128
   // last routing state
   int routed_T = -1;
+  bool route_pending = false;  // a routing not yet consumed by moe_experts
   int routed_plan = -1;
   // device memory
   float *gate = nullptr;
@@ -180,10 +181,8 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
   ctx->s.inter_bytes = (uint32_t)(S * I * sizeof(float));
   ctx->s.sout_bytes = (uint32_t)(S * H * sizeof(float));
   char *ctrl_mem = nullptr;
-  // Ctrl, dep[max_units], then the ready lines on a 128-byte boundary
-  const size_t dep_end = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
-  const size_t ready_off = (dep_end + 127) / 128 * 128;
-  const size_t ctrl_bytes = ready_off + sizeof(int) * (size_t)kReadyLines * kReadyStride;
+  // Ctrl, then dep[max_units]
+  const size_t ctrl_bytes = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
   if ((rc = dev_alloc(ctx, &ctrl_mem, ctrl_bytes))) {
     free_all(ctx);
     delete ctx;
@@ -191,7 +190,6 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
   }
   ctx->s.ctrl = reinterpret_cast<Ctrl *>(ctrl_mem);
   ctx->s.dep = reinterpret_cast<int *>(ctrl_mem + sizeof(Ctrl));
-  ctx->s.ready = reinterpret_cast<int *>(ctrl_mem + ready_off);
   if (hipMemset(ctrl_mem, 0, ctrl_bytes) != hipSuccess ||
       hipMemset(ctx->s.tb_done, 0, nb * sizeof(int)) != hipSuccess ||
       hipDeviceSynchronize() != hipSuccess) {
@@ -354,6 +352,7 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   if (launch_router(a, logits != nullptr, static_cast<hipStream_t>(stream)) != hipSuccess)
     return MOE_ERR_HIP;
   ctx->routed_T = T;
+  ctx->route_pending = true;
   ctx->routed_plan = a.tile_rows;
   return MOE_OK;
 }
@@ -375,7 +374,7 @@ int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
   if (rc) return rc;
   if (!ctx->weights_set) return MOE_ERR_NOT_READY;
   if (num_tokens == 0) return MOE_OK;
-  if (ctx->routed_T != num_tokens) return MOE_ERR_INVALID_ARG;
+  if (ctx->routed_T != num_tokens || !ctx->route_pending) return MOE_ERR_INVALID_ARG;
   if (!x || !y || !aligned16(x) || !aligned16(y) || (residual && !aligned16(residual)))
     return MOE_ERR_INVALID_ARG;
   if (x == y) return MOE_ERR_INVALID_ARG;
@@ -398,6 +397,9 @@ int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
   const int plan = ctx->routed_plan;
   const int pi = plan_index(plan);
   if (pi < 0) return MOE_ERR_INVALID_ARG;
+  // the routing (and, for the streaming plan, the rows the router prepared)
+  // serve this one launch
+  ctx->route_pending = false;
   if (launch_experts(a, plan, ctx->grid[pi], static_cast<hipStream_t>(stream)) != hipSuccess)
     return MOE_ERR_HIP;
   return MOE_OK;
@@ -477,6 +479,7 @@ int moe_dense_forward(moe_ctx *ctx, const float *x, float *y, const float *resid
   a.max_units = ctx->max_units;
   if (launch_router_dense(a, static_cast<hipStream_t>(stream)) != hipSuccess) return MOE_ERR_HIP;
   ctx->routed_T = num_tokens;
+  ctx->route_pending = true;
   ctx->routed_plan = a.tile_rows;
   return moe_experts(ctx, x, y, residual, num_tokens, stream);
 }

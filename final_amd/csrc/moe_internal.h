@@ -16,10 +16,6 @@ constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
 constexpr int kCombineTokens = 8;  // tokens per combine task
 constexpr int kStreamRows = 16;  // weight rows per streaming-plan task (small batches)
 constexpr int kStreamWideTokens = 32;  // batches from this size use 64-row tasks
-// Streaming-plan blocks each get a private 128-byte line of ready bits (word
-// 0: units whose gate/up tasks are done, word 1: all down tasks done).
-constexpr int kReadyLines = 1024;
-constexpr int kReadyStride = 32;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset
@@ -70,7 +66,6 @@ struct Scratch {
   uint32_t sout_bytes;
   Ctrl *ctrl;
   int *dep;              // [max_units]
-  int *ready;            // [kReadyLines][32]: per-block ready bits, one 128-byte line each
 };
 
 struct RouterArgs {

@@ -113,6 +113,30 @@ __device__ void block_signal(int *p) {
 // Router
 // ---------------------------------------------------------------------------
 
+// Weight-streaming plan: the expert kernel's intermediate rows and expert
+// outputs start every launch as this value, and their readers reload a value
+// until it has been replaced, so a value is its own completion signal.  It is
+// a signalling NaN: arithmetic never produces one (an operation on a NaN
+// returns a quiet NaN), and every value of those rows is computed.
+constexpr uint32_t kUnwritten = 0x7FBADA55u;
+
+// Fill rows [0, 4T) of the intermediate and expert-output buffers with
+// kUnwritten, shared by nthr threads in each of nblk blocks (this thread:
+// thread thr of block blk).  The kernel boundary orders these stores before
+// every store and load of the expert kernel.
+__device__ void fill_unwritten(const RouterArgs &a, int blk, int nblk, int thr, int nthr) {
+  if (a.tile_rows != 0) return;
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  const f32x4 v = __builtin_bit_cast(f32x4, u32x4{kUnwritten, kUnwritten, kUnwritten, kUnwritten});
+  const size_t rows = (size_t)a.T * kTopK;
+  const size_t ni = rows * (size_t)a.inter / 4, ns = rows * (size_t)a.H / 4;
+  const size_t stride = (size_t)nblk * nthr;
+  for (size_t i = (size_t)blk * nthr + thr; i < ni + ns; i += stride) {
+    if (i < ni) st4(a.s.inter + 4 * i, v);
+    else st4(a.s.sout + 4 * (i - ni), v);
+  }
+}
+
 // Exactly layer.cu:434: exp in double, add and IEEE divide in float.
 __device__ __forceinline__ float ref_sigmoid(float x) {
 #pragma clang fp contract(off)
@@ -346,10 +370,6 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
   const int units = min(ps.units, a.max_units);
   for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
   if (a.tile_rows == 0) {
-    for (int i = tid; i < kReadyLines; i += kThreads) {
-      a.s.ready[i * kReadyStride] = 0;
-      a.s.ready[i * kReadyStride + 1] = 0;
-    }
     __syncthreads();  // the block bases above are read back below
     // slot = token block base + in-block rank (stable by token), as the
     // dispatch tasks of the tiled plans compute it
@@ -414,6 +434,7 @@ void router_kernel(RouterArgs a) {
   const int el = tid % EPB, grp = tid / EPB;
   const bool chain_lane = grp * TPL < RT;
   Ctrl *ctrl = a.s.ctrl;
+  fill_unwritten(a, blockIdx.x, gridDim.x, tid, kThreads);
 
   if (!FROM_LOGITS) {
     // staging map: thread -> (row, float4 column) of a KC-wide chunk; the
@@ -685,6 +706,9 @@ void router_decode_kernel(RouterArgs a) {
     const float *xp = xs + min(tl, nt - 1) * P;
     const float acc = chain_dot(gp, xp, H);
     if (tl < nt) st_agent(&a.s.logits[(size_t)(t0 + tl) * kExperts + e0 + el], acc);
+  } else {
+    // waves 1-3, idle during the chains, prepare the expert kernel's rows
+    fill_unwritten(a, blockIdx.x, gridDim.x, tid - 64, kThreads - 64);
   }
   // 3. the last of the token block's 8 blocks finishes it
   __builtin_amdgcn_s_waitcnt(0);  // this block's logits are stored
@@ -775,6 +799,15 @@ __global__ __launch_bounds__(kThreads) void router_dense_kernel(RouterArgs a) {
   __shared__ int s_flag;
   const int tid = threadIdx.x;
   const int T = a.T, t0 = blockIdx.x * RT;
+  // blocks past the token blocks only prepare the expert kernel's rows
+  const int nb = (T + RT - 1) / RT;
+  if ((int)gridDim.x > nb) {
+    if ((int)blockIdx.x >= nb)
+      fill_unwritten(a, blockIdx.x - nb, gridDim.x - nb, tid, kThreads);
+  } else {
+    fill_unwritten(a, blockIdx.x, gridDim.x, tid, kThreads);
+  }
+  if ((int)blockIdx.x >= nb) return;
   const int nt = min(RT, T - t0);
   for (int f = tid; f < nt * kTopK; f += kThreads) {
     const size_t g = (size_t)t0 * kTopK + f;
@@ -784,7 +817,6 @@ __global__ __launch_bounds__(kThreads) void router_dense_kernel(RouterArgs a) {
     st_agent(&a.s.pos[g], f / kTopK);  // every token of the block chose chunk k
   }
   if (tid < kExperts) st_agent(&a.s.blk[(size_t)blockIdx.x * kExperts + tid], tid < kDenseChunks ? nt : 0);
-  const int nb = gridDim.x;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
@@ -1229,23 +1261,28 @@ void expert_mfma_kernel(ExpertArgs a) {
 // f32x4 of token rows per pass of 16 tokens in the same shape, and feeds both
 // to v_mfma_f32_16x16x4f32 (16 rows x 16 tokens, k permuted consistently in
 // the A and B operands).  Loads run kRingDepth steps ahead in a register ring
-// that crosses task boundaries.  The control wave polls the dependency
-// counters, sums the eight k-slice partials a task leaves in LDS, stores the
-// results (SwiGLU applied for gate/up), and signals.
+// that crosses task boundaries.  The control wave sums the eight k-slice
+// partials a task leaves in LDS and stores the results (SwiGLU applied for
+// gate/up) with agent-coherent stores; nothing signals that they are done.
+// The router fills the intermediate and expert-output rows with kUnwritten,
+// and their readers load them coherently (sc1) and reload any value that is
+// still kUnwritten, so a consumer starts as soon as the values it needs have
+// landed, with no store-completion wait, counter or poll in between.
 //
 // Row tasks follow the plan's order: gate/up row blocks expert by expert,
 // then down row blocks.  Block b starts with task b; every later task comes
 // from a queue counter (G + the counter's old value, G = grid), claimed by
 // streaming wave 0 at the first step of the block's current task, so a
-// block that draws cheap tasks takes more of them.  Only down tasks wait
-// (for every gate/up task of their unit), and a gate/up task never waits:
-// while a block runs a gate/up task, its waves do not wait for the inputs of
-// a down task that comes next (those may include the running task, or a
-// gate/up task of a block that is itself waiting); they finish the task
-// first and then wait and refill the ring.  So every gate/up task finishes,
-// and then every down task.  The combine tasks (one per token), which wait
-// for every down task, are dealt round-robin (block b runs tokens b, b + G,
-// ...) after the row tasks.
+// block that draws cheap tasks takes more of them.  The ring issues a down
+// task's loads while the task before it still runs; a down task waits, at
+// the step that consumes them, for intermediate values still unwritten.
+// Only down tasks wait and gate/up tasks never do, and a block claims a down
+// task only after every gate/up task has been claimed (claims follow the
+// order), by a block that runs it to the end: a block's earlier tasks are
+// finished before its streaming waves reach its next task's first step.  So
+// every gate/up task finishes, and then every down task.  The combine tasks
+// (one per token), which wait for their token's expert outputs, are dealt
+// round-robin (block b runs tokens b, b + G, ...) after the row tasks.
 // ---------------------------------------------------------------------------
 
 constexpr int kRingWaves = 8;                       // k-slice streaming waves
@@ -1257,6 +1294,17 @@ constexpr int kRingSlice = kRingSteps * 16;         // floats of k per wave (256
 constexpr int kRingMaxSlots = 4096;                 // slot -> token map kept in LDS
 static_assert(kRingWaves * kRingSlice == 2048, "k slices cover rows of <= 2048 floats");
 static_assert(kRingSteps % kRingDepth == 0, "ring rotation realigns at task boundaries");
+// Token passes per ring step: 1 or 2, the fewest that cover the largest
+// expert's tokens (larger experts run in several groups).  A pass that holds
+// no tokens would still move 1 KiB per wave per step through the CU's
+// load-return path, so the kernel picks the count from the plan at run time.
+constexpr int kRingMaxPasses = 2;
+constexpr int kRingWideGroups = 4;  // row groups of a 64-row task
+// 32-row tasks with 4 passes: batches where every expert holds up to 64
+// tokens (the dense FFN's chunks hold all of them); 64-row tasks with 4
+// passes would need twice the LDS for their partials.
+constexpr int kRingDenseGroups = 2, kRingDensePasses = 4;
+
 // 64-row tasks load 4 weight rows per step: half the depth keeps the bytes in
 // flight per CU about the same and the ring within the register budget.
 constexpr int ring_depth(int rg) { return rg == 1 ? kRingDepth : kRingDepth / 2; }
@@ -1264,8 +1312,6 @@ constexpr int ring_depth(int rg) { return rg == 1 ? kRingDepth : kRingDepth / 2;
 struct RingShared {
   int active[kExperts], counts[kExperts], offsets[kExperts];
   int tok[kRingMaxSlots];  // slot -> token
-  int dep_ok;              // bit u: every gate/up task of unit u is done
-  int p2_ok;               // every down task is done
   int flushed;             // items whose partials the control wave has consumed
   int done[2];             // streaming waves that wrote item i's partials into buffer i & 1
   int abort;
@@ -1303,7 +1349,7 @@ __device__ __forceinline__ bool ring_wait(const int *p, Cond cond, int *abort_fl
   }
   const long long t0 = ring_now();
   while (!cond(__builtin_amdgcn_readfirstlane(lds_load(p)))) {
-    if (lds_load(abort_flag)) return false;
+    if (__builtin_amdgcn_readfirstlane(lds_load(abort_flag))) return false;
     if (ring_now() - t0 > ticks) {
       if ((threadIdx.x & 63) == 0) {
         st_agent(err, 1);
@@ -1319,7 +1365,6 @@ __device__ __forceinline__ bool ring_wait(const int *p, Cond cond, int *abort_fl
 
 struct RingPlan {
   int n1, n2, ncomb, p1u, p2u, grid, rows;
-  uint32_t units;  // bit u for every unit (active expert)
 };
 
 // A row task, wave-uniform.  kind: 1 gate/up rows, 2 down rows, 4 none (the
@@ -1381,7 +1426,7 @@ constexpr uint32_t kRingOff = 0xFFFF0000u;  // lane offset past any buffer: load
 
 // What one streaming lane loads for a group of a task: a weight row byte
 // offset per 16-row group (with this wave's k slice) and a token-row byte
-// offset per pass.
+// offset per pass (token rows for gate/up, intermediate rows for down).
 template <int RG, int P>
 struct RingWork {
   __amdgpu_buffer_rsrc_t wr, xr;
@@ -1448,8 +1493,11 @@ __device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const 
   return r;
 }
 
-// One ring step's loads (each row group's weights + every pass's token rows)
-// into one slot.
+// One ring step's loads (each row group's weights + every pass's token or
+// intermediate rows) into one slot.  The row loads are agent-coherent (sc1):
+// intermediate values that other blocks write during the kernel are read
+// until they have landed (a branch on the task kind to load token rows
+// without sc1 would cost the compiler its exact wait counts).
 template <int RG, int P>
 __device__ __forceinline__ void ring_issue(const RingWork<RG, P> &r, int s, f32x4 (&wt)[RG],
                                            f32x4 (&xv)[P]) {
@@ -1458,7 +1506,56 @@ __device__ __forceinline__ void ring_issue(const RingWork<RG, P> &r, int s, f32x
     wt[gg] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.wr, r.woff[gg] + s * 64, 0, 0));
 #pragma unroll
   for (int p = 0; p < P; ++p)
-    xv[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + s * 64, 0, 0));
+    xv[p] = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + s * 64, 0, kCachePolicySc1));
+}
+
+template <int N>
+__device__ __forceinline__ bool any_unwritten(const f32x4 (&v)[N]) {
+  bool bad = false;
+#pragma unroll
+  for (int n = 0; n < N; ++n)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bad |= __builtin_bit_cast(uint32_t, v[n][i]) == kUnwritten;
+  return __builtin_amdgcn_ballot_w64(bad) != 0;  // wave-uniform
+}
+
+// Step s of a down task read intermediate values not yet written: reload
+// the step's rows (coherently) until every value has landed, then load the
+// rows of the steps already in flight again, since they were issued no later
+// and are likely stale too (their weights are not reloaded).  False if the
+// block aborts; a wait longer than `ticks` reports a device timeout and
+// aborts the block.
+template <int RG, int P, int D>
+__device__ __forceinline__ bool ring_await(const RingWork<RG, P> &r, int s, f32x4 (&wt)[D][RG],
+                                           f32x4 (&xv)[D][P], int *abort_flag, int *err,
+                                           long long ticks) {
+  const long long t0 = ring_now();
+  const int sl = s % D;
+  do {
+    if (__builtin_amdgcn_readfirstlane(lds_load(abort_flag))) return false;
+    if (ring_now() - t0 > ticks) {
+      if ((threadIdx.x & 63) == 0) {
+        st_agent(err, 1);
+        lds_store(abort_flag, 1);
+      }
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      xv[sl][p] = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + s * 64, 0, kCachePolicySc1));
+  } while (any_unwritten<P>(xv[sl]));
+#pragma unroll
+  for (int d = 1; d < D; ++d)
+    if (s + d < kRingSteps) {
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+        xv[(s + d) % D][p] = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + (s + d) * 64, 0, kCachePolicySc1));
+    }
+  return true;
 }
 
 // A token's routing: slots of its four expert rows and their weights.
@@ -1485,19 +1582,44 @@ __device__ __forceinline__ RingRoute ring_route(const ExpertArgs &a, int tok) {
 
 // Combine of token tok by the 512 threads of the streaming waves (thread ts:
 // float4 columns ts, ts + 512, ...), with the arithmetic of combine_task:
-// FMA chain over k ascending, then the residual.  y may alias the residual:
-// each thread reads its columns before it writes them.
-__device__ void ring_combine(const ExpertArgs &a, int tok, const RingRoute &r, int ts) {
+// FMA chain over k ascending, then the residual.  The expert outputs are
+// loaded coherently and reloaded while any is still kUnwritten.  y may alias
+// the residual: each thread reads its columns before it writes them.  False
+// if the block aborts or the wait times out.
+__device__ bool ring_combine(const ExpertArgs &a, int tok, const RingRoute &r, int ts,
+                             int *abort_flag, int *err, long long ticks) {
 #pragma clang fp contract(off)
   const int H4 = a.H >> 2;
-  const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
+  const __amdgpu_buffer_rsrc_t so =
+      __builtin_amdgcn_make_buffer_rsrc(a.s.sout, 0, (int)a.s.sout_bytes, kBufferRsrcWord3);
   const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
   float4 *y4 = reinterpret_cast<float4 *>(a.y);
   for (int c4 = ts; c4 < H4; c4 += kRingWaves * 64) {
-    float4 v[kTopK];
+    f32x4 v[kTopK];
+    uint32_t off[kTopK];
 #pragma unroll
-    for (int k = 0; k < kTopK; ++k) v[k] = so[(size_t)r.slot[k] * H4 + c4];
+    for (int k = 0; k < kTopK; ++k) {
+      off[k] = ((uint32_t)r.slot[k] * (uint32_t)H4 + (uint32_t)c4) * 16u;
+      v[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(so, off[k], 0, kCachePolicySc1));
+    }
     const float4 rv = r4 ? r4[(size_t)tok * H4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    if (any_unwritten<kTopK>(v)) {
+      const long long t0 = ring_now();
+      do {
+        if (__builtin_amdgcn_readfirstlane(lds_load(abort_flag))) return false;
+        if (ring_now() - t0 > ticks) {
+          if ((threadIdx.x & 63) == 0) {
+            st_agent(err, 1);
+            lds_store(abort_flag, 1);
+          }
+          return false;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < kTopK; ++k)
+          v[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(so, off[k], 0, kCachePolicySc1));
+      } while (any_unwritten<kTopK>(v));
+    }
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) {
@@ -1514,6 +1636,7 @@ __device__ void ring_combine(const ExpertArgs &a, int tok, const RingRoute &r, i
     }
     y4[(size_t)tok * H4 + c4] = acc;
   }
+  return true;
 }
 
 // Partials of item i: res[i & 1][wave][row group][pass][row][token], 16 x 16.
@@ -1542,9 +1665,6 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
   RingTask t = ring_seq_task<P>(sh, pl, 0);
   RingWork<RG, P> cur = ring_work<RG, P>(a, sh, rr, t, 0, w);
   bool ok = true;
-  if (t.kind == 2)
-    ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> t.u) & 1; }, &sh.abort, err, ticks);
-  if (!ok) cur = ring_work<RG, P>(a, sh, rr, none, 0, w);
   // in step order: the first step's MFMAs then wait only for the first
   // step's loads (the scheduler would otherwise issue them last)
 #pragma unroll
@@ -1558,19 +1678,17 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
       __builtin_amdgcn_make_buffer_rsrc(a.s.ctrl, 0, (int)sizeof(Ctrl), kBufferRsrcWord3);
   const uint32_t claim_off = lane == 0 ? (uint32_t)offsetof(Ctrl, head) : kRingOff;
   int claimed = 0;
-  bool refill = false;  // the ring holds no loads for task t yet
   while (ok && t.kind != 4) {
-    if (refill) {
-      // a down task whose inputs were not ready when the gate/up task before
-      // it was still running: wait for them now, then fill the ring
-      refill = false;
-      ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> t.u) & 1; }, &sh.abort, err, ticks);
-      cur = ring_work<RG, P>(a, sh, rr, ok ? t : none, 0, w);
-#pragma unroll
-      for (int s = 0; s < D; ++s) {
-        ring_issue<RG, P>(cur, s, wt[s], xv[s]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+    // Issue priority: the control wave's flushes are on every reader's path
+    // (highest, set in ring_role); a gate/up task produces what down tasks
+    // read; and of the two streaming waves that share a SIMD's MFMA unit the
+    // younger would otherwise trail the older by up to a whole task.
+    if (t.kind == 1) {
+      if (w >= kRingWaves / 2) __builtin_amdgcn_s_setprio(2);
+      else __builtin_amdgcn_s_setprio(1);
+    } else {
+      if (w >= kRingWaves / 2) __builtin_amdgcn_s_setprio(1);
+      else __builtin_amdgcn_s_setprio(0);
     }
     // Wave 0 claims the block's next task as this one starts.  Loads
     // complete in issue order, so the reply has arrived by the time step D's
@@ -1591,6 +1709,10 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
 #pragma unroll
     for (int s = 0; s < kRingSteps; ++s) {
       const int sl = s % D;
+      // a down task's intermediate values were loaded up to D steps earlier,
+      // possibly before they had landed
+      if (t.kind == 2 && any_unwritten<P>(xv[sl]) && ok)
+        ok = ring_await<RG, P, D>(cur, s, wt, xv, &sh.abort, err, ticks);
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         if (p < cur.npass) {
@@ -1615,16 +1737,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
           if (ok) ok = ring_wait(&sh.nseq, [&](int v) { return v >= j + 2; }, &sh.abort, err, ticks);
           tn = ok ? ring_seq_task<P>(sh, pl, jn) : none;
         }
-        // a down task needs every gate/up task of its unit done before its
-        // rows are read; a gate/up task does not wait for them
-        if (ok && tn.kind == 2 && gn == 0) {
-          const bool ready = (__builtin_amdgcn_readfirstlane(lds_load(&sh.dep_ok)) >> tn.u) & 1;
-          if (!ready && t.kind == 1)
-            refill = true;
-          else
-            ok = ring_wait(&sh.dep_ok, [&](int v) { return (v >> tn.u) & 1; }, &sh.abort, err, ticks);
-        }
-        nxt = ring_work<RG, P>(a, sh, rr, ok && !refill ? tn : none, gn, w);
+        nxt = ring_work<RG, P>(a, sh, rr, ok ? tn : none, gn, w);
       }
       if (s + D < kRingSteps) ring_issue<RG, P>(cur, s + D, wt[sl], xv[sl]);
       else ring_issue<RG, P>(nxt, s + D - kRingSteps, wt[sl], xv[sl]);
@@ -1658,12 +1771,9 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
     cur = nxt;
   }
   // combine tasks (one token each), after every row task, with the ring's
-  // registers free; the routing is read before the wait
-  for (int tok = blockIdx.x; ok && tok < pl.ncomb; tok += pl.grid) {
-    const RingRoute r = ring_route(a, tok);
-    ok = ring_wait(&sh.p2_ok, [&](int v) { return v != 0; }, &sh.abort, err, ticks);
-    if (ok) ring_combine(a, tok, r, (int)threadIdx.x);
-  }
+  // registers free
+  for (int tok = blockIdx.x; ok && tok < pl.ncomb; tok += pl.grid)
+    ok = ring_combine(a, tok, ring_route(a, tok), (int)threadIdx.x, &sh.abort, err, ticks);
 }
 
 // Control side: sums the 8 k-slice partials of item (t, g) and stores the
@@ -1712,24 +1822,9 @@ __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &
   }
 }
 
-// Control side.  A step issues the stores of every item whose partials are
-// complete and, when one of the next tasks the streaming waves will reach
-// needs an input not yet seen, a poll of the block's own ready line; then it
-// waits once, signals the completed tasks and publishes what the poll found.
-// The block whose signal completes a unit's gate/up tasks (or the down
-// tasks) sets that bit in every block's ready line, so each block polls a
-// line nobody else reads instead of all blocks polling the shared counters.
-// The streaming waves write item i's partials only after item i - 2 is
-// flushed, and while finishing task k they need task k + 1's inputs, so they
-// are never more than 3 tasks past the control wave's flush position.
-constexpr int kRingHorizon = 4;            // tasks (from the flush position) polled for
-constexpr long long kRingPollTicks = 20;   // at most one poll per 200 ns
-// While some expert's gate/up tasks are not known to be done, the line is
-// also polled in the background (every 1 us), so that a down task claimed
-// later rarely waits for a poll that the control wave issues only once it
-// sees that task.
-constexpr long long kRingBgPollTicks = 100;
-
+// Control side: flushes every item whose eight partials are complete, in
+// order, and ends once the block's last row task is flushed.  It never waits
+// for its stores: their readers wait for the values themselves.
 template <int RG, int P>
 __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *res,
                              const RingPlan &pl) {
@@ -1737,42 +1832,10 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
   const int lane = threadIdx.x & 63;
   const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
   const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
-  uint32_t dep_ok = 0;  // units whose gate/up tasks are all done
-  bool p2_ok = false;   // every down task done
   int j = 0, g = 0, it = 0;  // next item to flush
   RingTask t = ring_seq_task<P>(sh, pl, 0);
-  const bool combines = (int)blockIdx.x < pl.ncomb;
-  int sig = 0;
-  long long last = ring_now(), last_poll = 0;
-  while (true) {
-    // inputs one of the next tasks needs and nobody has seen yet
-    int pu = -1;
-    bool pp2 = false;
-    const int ns = __builtin_amdgcn_readfirstlane(lds_load(&sh.nseq));
-    acquire_lds();
-    for (int d = 0; d < kRingHorizon && j + d < ns; ++d) {
-      const RingTask tt = d == 0 ? t : ring_seq_task<P>(sh, pl, j + d);
-      if (tt.kind == 4) {  // the block's last row task: its combine tasks follow
-        pp2 = combines && !p2_ok;
-        break;
-      }
-      if (tt.kind == 2 && !((dep_ok >> tt.u) & 1u)) {
-        pu = tt.u;
-        break;
-      }
-    }
-    // every row task flushed and no input left to poll for: done
-    if (t.kind == 4 && pu < 0 && !pp2) break;
-    bool prog = false;
-    const long long now = ring_now();
-    const bool poll = ((pu >= 0 || pp2) && now - last_poll >= kRingPollTicks) ||
-                      ((dep_ok & pl.units) != pl.units && now - last_poll >= kRingBgPollTicks);
-    int pv = 0;
-    if (poll) {
-      last_poll = now;
-      if (lane < 2) pv = load_relaxed(&a.s.ready[(int)blockIdx.x * kReadyStride + lane]);
-    }
-    // flush every complete item (in order)
+  long long last = ring_now();
+  while (t.kind != 4) {
     int flushed_now = 0;
     while (t.kind != 4) {
       const int b = it & 1;
@@ -1783,7 +1846,6 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
       ++it;
       ++flushed_now;
       if (++g >= t.ngroups) {
-        if ((t.kind == 1 && lane == t.u) || (t.kind == 2 && lane == 32)) ++sig;
         g = 0;
         ++j;
         t = ring_seq_task<P>(sh, pl, j);  // published before task j - 1's partials
@@ -1794,49 +1856,9 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
       // partials are read: the streaming waves may reuse the buffers
       release_lds();
       if (lane == 0) lds_store(&sh.flushed, it);
-      prog = true;
-    }
-    if (poll || flushed_now) {
-      __builtin_amdgcn_s_waitcnt(0);  // poll returned, stores complete
-      bool crossed = false;
-      if (sig) {
-        const int target = lane < kExperts ? pl.p1u : pl.n2;
-        const int old = fetch_add(lane < kExperts ? &a.s.dep[lane] : &c->p2_done, sig);
-        crossed = old < target && old + sig >= target;
-      }
-      sig = 0;
-      const uint64_t cm = __builtin_amdgcn_ballot_w64(crossed);
-      if (cm) {
-        // this block completed units (bits 0..31) and/or the down tasks
-        // (bit 32): tell every block
-        const int ubits = (int)(uint32_t)cm;
-        const bool p2 = (cm >> 32) & 1;
-        for (int bb = lane; bb < pl.grid; bb += 64) {
-          if (ubits) __hip_atomic_fetch_or(&a.s.ready[bb * kReadyStride], ubits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (p2) __hip_atomic_fetch_or(&a.s.ready[bb * kReadyStride + 1], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-      if (poll) {
-        const uint32_t ub = (uint32_t)__builtin_amdgcn_readlane(pv, 0);
-        const bool p2r = __builtin_amdgcn_readlane(pv, 1) != 0;
-        const uint32_t nd = dep_ok | ub;
-        const bool np2 = p2_ok || p2r;
-        if (nd != dep_ok || np2 != p2_ok) {
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");  // inputs those bits publish
-          dep_ok = nd;
-          p2_ok = np2;
-          if (lane == 0) {
-            lds_store(&sh.dep_ok, (int)dep_ok);
-            if (p2_ok) lds_store(&sh.p2_ok, 1);
-          }
-          prog = true;
-        }
-      }
-    }
-    if (prog) {
       last = ring_now();
     } else {
-      if (lds_load(&sh.abort)) break;
+      if (__builtin_amdgcn_readfirstlane(lds_load(&sh.abort))) break;
       if (ring_now() - last > ticks) {
         if (lane == 0) {
           st_agent(&c->err, 1);
@@ -1849,17 +1871,6 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
   }
 }
 
-// Token passes per ring step: 1 or 2, the fewest that cover the largest
-// expert's tokens (larger experts run in several groups).  A pass that holds
-// no tokens would still move 1 KiB per wave per step through the CU's
-// load-return path, so the kernel picks the count from the plan at run time.
-constexpr int kRingMaxPasses = 2;
-constexpr int kRingWideGroups = 4;  // row groups of a 64-row task
-// 32-row tasks with 4 passes: batches where every expert holds up to 64
-// tokens (the dense FFN's chunks hold all of them); 64-row tasks with 4
-// passes would need twice the LDS for their partials.
-constexpr int kRingDenseGroups = 2, kRingDensePasses = 4;
-
 // LDS of the partials: [2][kRingWaves][row groups][passes][16][16]
 constexpr size_t ring_res_bytes(int rg, int p) {
   return (size_t)2 * kRingWaves * rg * p * kRingTokens * kRingTokens * sizeof(float);
@@ -1868,10 +1879,12 @@ constexpr size_t ring_res_bytes(int rg, int p) {
 template <int RG, int P>
 __device__ __forceinline__ void ring_role(const ExpertArgs &a, RingShared &sh, float *res,
                                           const RingPlan &pl, long long ticks) {
-  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == kRingWaves)  // uniform branch per wave
+  if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == kRingWaves) {  // uniform branch per wave
+    __builtin_amdgcn_s_setprio(3);  // above every streaming wave
     ring_control<RG, P>(a, sh, res, pl);
-  else
+  } else {
     ring_streamer<RG, P>(a, sh, res, pl, 2 * ticks);
+  }
 }
 
 template <int KCH1, int KCH2>
@@ -1891,8 +1904,6 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   for (int i = tid; i < nslots; i += kRingThreads) sh.tok[i] = a.s.slot_token[i];
   if (tid < 2) sh.done[tid] = 0;
   if (tid == 0) {
-    sh.dep_ok = 0;
-    sh.p2_ok = 0;
     sh.flushed = 0;
     sh.abort = 0;
     sh.seq[0] = blockIdx.x;  // past the row tasks when the grid is larger
@@ -1906,13 +1917,9 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   pl.p2u = c->p2_per_unit;
   pl.grid = gridDim.x;
   pl.rows = __builtin_amdgcn_readfirstlane(c->stream_rows);
-  {
-    const int na = __builtin_amdgcn_readfirstlane(c->n_active);
-    pl.units = na >= 32 ? 0xFFFFFFFFu : (na > 0 ? (1u << na) - 1u : 0u);
-  }
-  // plans for this kernel take their slots from the router, every block
-  // needs a ready line, and a task covers 16 or 64 rows
-  if (c->n_rblocks != 0 || (int)gridDim.x > kReadyLines ||
+  // plans for this kernel take their slots from the router, and a task
+  // covers 16, 32 or 64 rows
+  if (c->n_rblocks != 0 ||
       (pl.rows != kStreamRows && pl.rows != kStreamRows * kRingWideGroups &&
        pl.rows != kStreamRows * kRingDenseGroups)) {
     if (tid == 0) st_agent(&a.s.ctrl->err, 2);
@@ -1970,8 +1977,10 @@ bool router_fuses_norm(int T) { return T <= 64; }
 
 hipError_t launch_router_dense(const RouterArgs &a, hipStream_t st) {
   if (a.T <= 64) {
+    // the weight-streaming plan adds blocks that prepare its rows
     const int nb = (a.T + kSmallRT - 1) / kSmallRT;
-    hipLaunchKernelGGL(router_dense_kernel<kSmallRT>, dim3(nb), dim3(kThreads), 0, st, a);
+    const int grid = a.tile_rows == 0 ? nb * (1 + kDecES) : nb;
+    hipLaunchKernelGGL(router_dense_kernel<kSmallRT>, dim3(grid), dim3(kThreads), 0, st, a);
   } else {
     const int nb = (a.T + kLargeRT - 1) / kLargeRT;
     hipLaunchKernelGGL(router_dense_kernel<kLargeRT>, dim3(nb), dim3(kThreads), 0, st, a);

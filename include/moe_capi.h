@@ -90,7 +90,9 @@ int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
  * moe_route = gate GEMM + sigmoid/top-4 + per-expert histogram and scan
  * (layer.cu:1438-1464); moe_experts = dispatch + grouped SwiGLU experts +
  * weighted combine (layer.cu:1466-1497).  moe_experts must follow moe_route on
- * the same stream with the same x and num_tokens. */
+ * the same stream with the same x and num_tokens; each moe_route serves one
+ * moe_experts (a second call without a new route returns
+ * MOE_ERR_INVALID_ARG). */
 int moe_route(moe_ctx *ctx, const float *x, int num_tokens, moe_stream_t stream);
 int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
                 int num_tokens, moe_stream_t stream);

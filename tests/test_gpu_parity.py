@@ -199,3 +199,33 @@ def test_forward_norm_in_place(block, real_weights, oracle_mod):
         hip.synchronize()
         block.check_device()
         np.testing.assert_allclose(dh.download(), ref["y"], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [8, 300])
+def test_route_serves_one_experts_launch(T, block, real_weights, oracle_mod):
+    """The weight-streaming plan's readers wait for the rows the router
+    prepared, and every plan's task counters are reset by the router, so one
+    moe_route serves one moe_experts; a second launch without a new route is
+    rejected, and routing again restores the result."""
+    from final_amd import _native, hip
+    from final_amd import workloads as W
+    x = W.gen_x(T, seed=31)
+    ref = oracle_forward(oracle_mod, real_weights, x)
+    dx = hip.DeviceArray.from_numpy(x)
+    dy = hip.DeviceArray((T, W.H))
+    say(f"[one route, one experts] T={T} plan={block.plan(T)}")
+    block.route(dx, T)
+    block.experts(dx, dy, T)
+    with pytest.raises(_native.MoeError) as e:
+        block.experts(dx, dy, T)
+    assert e.value.status == _native.MOE_ERR_INVALID_ARG
+    hip.synchronize()
+    block.check_device()
+    np.testing.assert_allclose(dy.download(), ref["y"], rtol=RTOL, atol=ATOL)
+    dy2 = hip.DeviceArray((T, W.H))
+    block.route(dx, T)
+    block.experts(dx, dy2, T)
+    hip.synchronize()
+    block.check_device()
+    np.testing.assert_allclose(dy2.download(), ref["y"], rtol=RTOL, atol=ATOL)
