@@ -54,10 +54,27 @@ def parse():
     return p.parse_args()
 
 
-def cpu_baseline(w, x, threads: int):
+def host_cpu() -> dict:
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    usable = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None
+    return {"nproc": os.cpu_count(), "usable": usable, "model": model}
+
+
+def cpu_baseline(w, x, threads: int, single_tokens: int = 128):
+    """The oracle over the workload on `threads` OpenMP threads (the reported
+    value), plus one thread over the first `single_tokens` tokens (tokens are
+    independent, so a prefix is a fair sample of the per-token cost)."""
     from oracle import oracle as O
-    O.set_threads(threads)
     T = x.shape[0]
+    O.set_threads(threads)
     times = []
     for _ in range(3):
         t0 = time.perf_counter()
@@ -66,9 +83,18 @@ def cpu_baseline(w, x, threads: int):
         if sum(times) > 30.0:
             break
     med = statistics.median(times)
+    n1 = min(T, single_tokens)
+    O.set_threads(1)
+    t0 = time.perf_counter()
+    O.moe_forward(x[:n1], w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+    t1 = time.perf_counter() - t0
+    O.set_threads(threads)
     return {"value": round(T / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"whole workload ({T} tokens), median of {len(times)} runs, "
-                      f"{med:.3f} s each, OpenMP {threads} threads"}
+                      f"{med:.3f} s each, OpenMP {threads} threads",
+            "single_thread": {"value": round(n1 / t1, 2), "unit": "tokens/s",
+                              "sample": f"first {n1} tokens, one run of {t1:.3f} s, 1 thread"},
+            "host": host_cpu()}
 
 
 def bench_dense(args, wl):
@@ -145,7 +171,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs the MoE block on ONE GPU; multi-GPU runs are not "
-              "part of it (see DESIGN.md for how the block would shard).", file=sys.stderr)
+              "part of it (the design notes describe how the block would shard).", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
