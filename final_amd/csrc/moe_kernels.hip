@@ -1299,15 +1299,22 @@ static_assert(kRingSteps % kRingDepth == 0, "ring rotation realigns at task boun
 // no tokens would still move 1 KiB per wave per step through the CU's
 // load-return path, so the kernel picks the count from the plan at run time.
 constexpr int kRingMaxPasses = 2;
+// 64-row tasks (batches from 32 tokens) share each token-row load across
+// their 4 row groups.  Up to 16 tokens per expert, a wave streams the groups
+// one after another and keeps its token slice in registers: a CU then reads
+// one 16-row block at a time, which streams at ~6.3 TB/s where reading 2 or 4
+// row blocks at once reaches 5.0-5.9 TB/s (measured with a bare load probe).
+// With two token passes the four groups are read at once.
 constexpr int kRingWideGroups = 4;  // row groups of a 64-row task
 // 32-row tasks with 4 passes: batches where every expert holds up to 64
 // tokens (the dense FFN's chunks hold all of them); 64-row tasks with 4
 // passes would need twice the LDS for their partials.
 constexpr int kRingDenseGroups = 2, kRingDensePasses = 4;
 
-// 64-row tasks load 4 weight rows per step: half the depth keeps the bytes in
-// flight per CU about the same and the ring within the register budget.
-constexpr int ring_depth(int rg) { return rg == 1 ? kRingDepth : kRingDepth / 2; }
+// 64-row tasks read at once load 4 weight rows per step; with two token
+// passes half the depth keeps the ring within the register budget of 3 waves
+// per SIMD.
+constexpr int ring_depth(int rg, int p) { return rg == 1 || p == 1 ? kRingDepth : kRingDepth / 2; }
 
 struct RingShared {
   int active[kExperts], counts[kExperts], offsets[kExperts];
@@ -1435,7 +1442,10 @@ struct RingWork {
   int npass;
 };
 
-template <int RG, int P>
+// Item g of a task: token group g / SUB and, for tasks streamed as SUB
+// sequential row sub-groups, sub-group g % SUB.  Only sub-group 0 loads the
+// token rows; the later ones reuse the wave's copy of them.
+template <int RG, int P, int SUB>
 __device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const RingShared &sh,
                                                      const RingRsrc &rr, const RingTask &t, int g,
                                                      int w) {
@@ -1449,7 +1459,8 @@ __device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const 
 #pragma unroll
   for (int p = 0; p < P; ++p) r.xoff[p] = kRingOff;
   if (t.kind != 1 && t.kind != 2) return r;
-  const int m0 = g * kRingTokens * P;
+  const int u = g % SUB;
+  const int m0 = (g / SUB) * kRingTokens * P;
   // every wave writes partials for every pass of the group (zeros from a
   // slice past the end of the rows), so the control wave sums all eight
   r.npass = min(P, (t.cnt - m0 + kRingTokens - 1) / kRingTokens);
@@ -1462,7 +1473,7 @@ __device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const 
     // of the same column, packed [I/32][2][32][H] so the two are 32 rows apart
 #pragma unroll
     for (int gg = 0; gg < RG; ++gg) {
-      const int n = t.col + 8 * gg + (li & 7);
+      const int n = t.col + 8 * (u * RG + gg) + (li & 7);
       const uint32_t prow = (uint32_t)(n >> 5) * 64 + (li >= 8 ? 32 : 0) + (n & 31);
       r.woff[gg] = (((uint32_t)t.e * 2 * a.I + prow) * (uint32_t)a.H + kl) * 4u;
     }
@@ -1481,7 +1492,7 @@ __device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const 
   } else {
 #pragma unroll
     for (int gg = 0; gg < RG; ++gg)
-      r.woff[gg] = (((uint32_t)t.e * a.H + t.col + 16 * gg + li) * (uint32_t)a.I + kl) * 4u;
+      r.woff[gg] = (((uint32_t)t.e * a.H + t.col + 16 * (u * RG + gg) + li) * (uint32_t)a.I + kl) * 4u;
     r.wr = rr.w2;
     r.xr = rr.inter;
 #pragma unroll
@@ -1490,14 +1501,24 @@ __device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const 
       if (m < t.cnt) r.xoff[p] = ((uint32_t)(t.slot0 + m) * a.I + kl) * 4u;
     }
   }
+  if (SUB > 1 && u != 0) {
+    r.xr = rr.none;
+#pragma unroll
+    for (int p = 0; p < P; ++p) r.xoff[p] = kRingOff;
+  }
   return r;
 }
 
 // One ring step's loads (each row group's weights + every pass's token or
-// intermediate rows) into one slot.  The row loads are agent-coherent (sc1):
-// intermediate values that other blocks write during the kernel are read
-// until they have landed (a branch on the task kind to load token rows
-// without sc1 would cost the compiler its exact wait counts).
+// intermediate rows) into one slot.  Both row kinds use the default cache
+// policy, so rows that many tasks share (an expert's tokens or intermediate
+// values) come from the XCD's L2 after the first read.  Intermediate rows are
+// written by other blocks during the kernel, but each of their values is only
+// ever kUnwritten (the router's fill) or final, and caches start the kernel
+// invalidated: a load returns either the final value or kUnwritten, possibly
+// a stale cached kUnwritten, and ring_await then reloads coherently (sc1).
+// Token and intermediate loads are one instruction, so the compiler's wait
+// counts stay exact whichever kind a task is.
 template <int RG, int P>
 __device__ __forceinline__ void ring_issue(const RingWork<RG, P> &r, int s, f32x4 (&wt)[RG],
                                            f32x4 (&xv)[P]) {
@@ -1506,8 +1527,7 @@ __device__ __forceinline__ void ring_issue(const RingWork<RG, P> &r, int s, f32x
     wt[gg] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.wr, r.woff[gg] + s * 64, 0, 0));
 #pragma unroll
   for (int p = 0; p < P; ++p)
-    xv[p] = __builtin_bit_cast(
-        f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + s * 64, 0, kCachePolicySc1));
+    xv[p] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r.xr, r.xoff[p] + s * 64, 0, 0));
 }
 
 template <int N>
@@ -1646,12 +1666,16 @@ __device__ __forceinline__ float *ring_res(float *res, int b, int w, int gg, int
 }
 
 // Streaming side: RG row groups of 16 rows share every token-row load; with
-// one group two accumulators per pass break the MFMA dependency chain.
-template <int RG, int P>
+// one group two accumulators per pass break the MFMA dependency chain.  With
+// SUB > 1 a task's SUB * RG row groups are streamed as SUB items one after
+// another (the access pattern of a 16-row task, which streams faster than
+// several row groups read at once), and each wave keeps the token slice that
+// sub-group 0 loaded in registers (xt) for the later sub-groups.
+template <int RG, int P, int SUB>
 __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, const RingPlan &pl,
                               long long ticks) {
   constexpr int NA = RG == 1 ? 2 : 1;
-  constexpr int D = ring_depth(RG);
+  constexpr int D = ring_depth(RG, P);
   static_assert(kRingSteps % D == 0, "ring rotation realigns at task boundaries");
   static_assert(D < kRingSteps - D - 1, "the next task is published before it is read");
   int *err = &a.s.ctrl->err;
@@ -1661,9 +1685,10 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
   const RingTask none{4, 0, 0, 0, 0, 0, 0, 1};
   f32x4 wt[D][RG];
   f32x4 xv[D][P];
-  int j = 0, g = 0, it = 0;  // task, group within it, item (group) counter
+  f32x4 xt[SUB > 1 ? kRingSteps : 1][P];  // token slice of the task's current group
+  int j = 0, g = 0, it = 0;  // task, item within it, item counter
   RingTask t = ring_seq_task<P>(sh, pl, 0);
-  RingWork<RG, P> cur = ring_work<RG, P>(a, sh, rr, t, 0, w);
+  RingWork<RG, P> cur = ring_work<RG, P, SUB>(a, sh, rr, t, 0, w);
   bool ok = true;
   // in step order: the first step's MFMAs then wait only for the first
   // step's loads (the scheduler would otherwise issue them last)
@@ -1697,6 +1722,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
     const bool claim_now = w == 0 && g == 0;
     if (claim_now) claimed = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, cr, claim_off, 0, 0);
     int jn = j, gn = g + 1;
+    const bool fresh = SUB == 1 || g % SUB == 0;  // this item loads the token rows
     RingTask tn = t;
     RingWork<RG, P> nxt;
     f32x4 acc[RG][P][NA];
@@ -1716,12 +1742,17 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
 #pragma unroll
       for (int p = 0; p < P; ++p) {
         if (p < cur.npass) {
+          f32x4 xo = xv[sl][p];
+          if constexpr (SUB > 1) {
+            xo = fresh ? xo : xt[s][p];
+            xt[s][p] = xo;
+          }
 #pragma unroll
           for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int gg = 0; gg < RG; ++gg)
               acc[gg][p][q % NA] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-                  wt[sl][gg][q], xv[sl][p][q], acc[gg][p][q % NA], 0, 0, 0);
+                  wt[sl][gg][q], xo[q], acc[gg][p][q % NA], 0, 0, 0);
         }
       }
       if (s == D && claim_now) {
@@ -1731,13 +1762,13 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
       }
       if (s == kRingSteps - D - 1) {
         // the next group's rows are about to be issued
-        if (gn >= t.ngroups) {
+        if (gn >= t.ngroups * SUB) {
           jn = j + 1;
           gn = 0;
           if (ok) ok = ring_wait(&sh.nseq, [&](int v) { return v >= j + 2; }, &sh.abort, err, ticks);
           tn = ok ? ring_seq_task<P>(sh, pl, jn) : none;
         }
-        nxt = ring_work<RG, P>(a, sh, rr, ok ? tn : none, gn, w);
+        nxt = ring_work<RG, P, SUB>(a, sh, rr, ok ? tn : none, gn, w);
       }
       if (s + D < kRingSteps) ring_issue<RG, P>(cur, s + D, wt[sl], xv[sl]);
       else ring_issue<RG, P>(nxt, s + D - kRingSteps, wt[sl], xv[sl]);
@@ -1779,12 +1810,13 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
 // Control side: sums the 8 k-slice partials of item (t, g) and stores the
 // outputs with 16-byte agent-scope stores (gate/up: silu(W1 x) * (W3 x) for
 // 8 columns per row group; down: 16 columns per row group).
-template <int RG, int P>
+template <int RG, int P, int SUB>
 __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &t, int g,
                                            const float *res, int b, const AgentOut &inter_out,
                                            const AgentOut &sout_out) {
   const int lane = threadIdx.x & 63;
-  const int m0 = g * kRingTokens * P;
+  const int u = g % SUB;  // row sub-group of the item
+  const int m0 = (g / SUB) * kRingTokens * P;
   const int nt = min(kRingTokens * P, t.cnt - m0);
   // gate/up: lane -> (token, 4 columns): 2 lanes per token and row group;
   // down: 4 lanes
@@ -1816,16 +1848,16 @@ __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &
     }
     const int slot = t.slot0 + m0 + m;
     if (t.kind == 1)
-      inter_out.store((uint32_t)(((size_t)slot * a.I + t.col + 8 * gg + q * 4) * sizeof(float)), o);
+      inter_out.store((uint32_t)(((size_t)slot * a.I + t.col + 8 * (u * RG + gg) + q * 4) * sizeof(float)), o);
     else
-      sout_out.store((uint32_t)(((size_t)slot * a.H + t.col + 16 * gg + q * 4) * sizeof(float)), o);
+      sout_out.store((uint32_t)(((size_t)slot * a.H + t.col + 16 * (u * RG + gg) + q * 4) * sizeof(float)), o);
   }
 }
 
 // Control side: flushes every item whose eight partials are complete, in
 // order, and ends once the block's last row task is flushed.  It never waits
 // for its stores: their readers wait for the values themselves.
-template <int RG, int P>
+template <int RG, int P, int SUB>
 __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *res,
                              const RingPlan &pl) {
   Ctrl *c = a.s.ctrl;
@@ -1841,11 +1873,11 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
       const int b = it & 1;
       if (__builtin_amdgcn_readfirstlane(lds_load(&sh.done[b])) != kRingWaves) break;
       acquire_lds();
-      ring_flush<RG, P>(a, t, g, res, b, inter_out, sout_out);
+      ring_flush<RG, P, SUB>(a, t, g, res, b, inter_out, sout_out);
       lds_store(&sh.done[b], 0);
       ++it;
       ++flushed_now;
-      if (++g >= t.ngroups) {
+      if (++g >= t.ngroups * SUB) {
         g = 0;
         ++j;
         t = ring_seq_task<P>(sh, pl, j);  // published before task j - 1's partials
@@ -1876,14 +1908,14 @@ constexpr size_t ring_res_bytes(int rg, int p) {
   return (size_t)2 * kRingWaves * rg * p * kRingTokens * kRingTokens * sizeof(float);
 }
 
-template <int RG, int P>
+template <int RG, int P, int SUB = 1>
 __device__ __forceinline__ void ring_role(const ExpertArgs &a, RingShared &sh, float *res,
                                           const RingPlan &pl, long long ticks) {
   if (__builtin_amdgcn_readfirstlane(threadIdx.x >> 6) == kRingWaves) {  // uniform branch per wave
     __builtin_amdgcn_s_setprio(3);  // above every streaming wave
-    ring_control<RG, P>(a, sh, res, pl);
+    ring_control<RG, P, SUB>(a, sh, res, pl);
   } else {
-    ring_streamer<RG, P>(a, sh, res, pl, 2 * ticks);
+    ring_streamer<RG, P, SUB>(a, sh, res, pl, 2 * ticks);
   }
 }
 
@@ -1934,7 +1966,7 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     if (maxcnt <= kRingTokens) ring_role<1, 1>(a, sh, res, pl, ticks);
     else ring_role<1, kRingMaxPasses>(a, sh, res, pl, ticks);
   } else if (pl.rows == kStreamRows * kRingWideGroups) {
-    if (maxcnt <= kRingTokens) ring_role<kRingWideGroups, 1>(a, sh, res, pl, ticks);
+    if (maxcnt <= kRingTokens) ring_role<1, 1, kRingWideGroups>(a, sh, res, pl, ticks);
     else ring_role<kRingWideGroups, kRingMaxPasses>(a, sh, res, pl, ticks);
   } else {
     ring_role<kRingDenseGroups, kRingDensePasses>(a, sh, res, pl, ticks);
