@@ -268,6 +268,23 @@ def main():
         achieved = expert_bytes / (exp_avg / 1e3) / 1e9
         roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
+    # near the ridge (fp32 MFMA peak / HBM peak = 19.7 FLOP/B) both bounds
+    # are close: report the other one beside the primary
+    ai = expert_flops / max(expert_bytes, 1)
+    ridge = PEAK_MFMA_F32_TFLOPS * 1e3 / PEAK_HBM_GBS
+    if 0.5 <= ai / ridge <= 2.0:
+        if mfma_bound:
+            other = expert_bytes / (exp_avg / 1e3) / 1e9
+            roof["secondary"] = {"bound": "hbm", "achieved": round(other, 1), "peak": PEAK_HBM_GBS,
+                                 "unit": "GB/s", "frac": round(other / PEAK_HBM_GBS, 4),
+                                 "per_launch": {"bytes": expert_bytes}}
+        else:
+            other = expert_flops / (exp_avg / 1e3) / 1e12
+            roof["secondary"] = {"bound": "mfma", "achieved": round(other, 3),
+                                 "peak": PEAK_MFMA_F32_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(other / PEAK_MFMA_F32_TFLOPS, 4),
+                                 "per_launch": {"flop": expert_flops}}
+        roof["arithmetic_intensity"] = round(ai, 2)
     roof["traffic"] = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:

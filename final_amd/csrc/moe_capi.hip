@@ -83,17 +83,20 @@ static int plan_index(int rows) {
   }
 }
 
+// Crossovers measured on MI355X with the seed-0 workload (whole-step times):
+// weight streaming is fastest up to 96 tokens (420 vs 428 us at 96), 64-row
+// MFMA tiles from 128 to 1024 tokens (527 vs 581 us at 256), 128-row tiles
+// from 1536 (1472 vs 1517 us).
 static int auto_plan(int T, bool stream_ok) {
-  if (T <= 64) return stream_ok ? 0 : 32;
-  if (T < 512) return 32;
-  if (T < 2048) return 64;
+  if (T <= 96 && stream_ok) return 0;
+  if (T < 1536) return 64;
   return 128;
 }
 
 static int ctx_plan(const moe_ctx *ctx, int T) {
   const int p = ctx->tile_override >= 0 ? ctx->tile_override : auto_plan(T, ctx->stream_ok);
   // the streaming plan keeps the batch's slot -> token map in LDS
-  return p == 0 && T > stream_max_tokens() ? 32 : p;
+  return p == 0 && T > stream_max_tokens() ? 64 : p;
 }
 
 template <typename T>

@@ -16,6 +16,13 @@ constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
 constexpr int kCombineTokens = 8;  // tokens per combine task
 constexpr int kStreamRows = 16;  // weight rows per streaming-plan task (small batches)
 constexpr int kStreamWideTokens = 32;  // batches from this size use 64-row tasks
+// Streaming kernel shapes: tokens per MFMA pass; token passes of 16- and
+// 64-row tasks; row groups of 16 in a 64-row task; row groups and passes of a
+// 32-row task (experts of up to 64 tokens).
+constexpr int kRingTokens = 16;
+constexpr int kRingMaxPasses = 2;
+constexpr int kRingWideGroups = 4;
+constexpr int kRingDenseGroups = 2, kRingDensePasses = 4;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset

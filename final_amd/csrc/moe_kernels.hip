@@ -5,7 +5,7 @@
 //      attn_matmul_tiled_kernel, layer.cu:9-141), sigmoid with a double exp,
 //      top-4 (layer.cu:439-499), per-token-block expert histogram and in-block
 //      ranks; the last token block scans the histograms and writes the expert
-//      kernel's task plan.  router_decode_kernel serves T <= 64 (expert-split
+//      kernel's task plan.  router_decode_kernel serves T <= 256 (expert-split
 //      blocks, whole rows staged in LDS), router_kernel larger T (64-token
 //      blocks) and routing from given logits.
 //   2. expert kernel -- persistent, gate/up projection with the SwiGLU
@@ -13,7 +13,8 @@
 //      the weighted top-4 combine with the residual add (layer.cu:695-721,
 //      1860-1880).  Large T: expert_mfma_kernel, MFMA 32x32x2 f32 tiles with
 //      a dispatch phase that assigns slots (replaces moe_scatter_kernel,
-//      layer.cu:501-542, without copying x), one dynamic task queue.  Small T:
+//      layer.cu:501-542, without copying x), one dynamic task queue; 64-row
+//      tiles up to 1535 tokens, 128-row tiles above.  T <= 96:
 //      expert_ring_kernel, weight streaming through MFMA 16x16x4 f32 with
 //      round-robin tasks and slots assigned by the router.
 //
@@ -313,6 +314,9 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
       run += v;
     }
     const int cnt = run;
+    int maxcnt = cnt;
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) maxcnt = max(maxcnt, __shfl_xor(maxcnt, o, 32));
     int total = 0, utotal = 0;
     const int off = lane_scan32(cnt, lane, &total);
     const int tr = a.tile_rows;
@@ -334,10 +338,16 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
       ctrl->unit_off[kExperts] = utotal;
       ctrl->n_active = nact;
       const int units = utotal;
-      // a.bn: columns of an MFMA tile, or weight rows of a streaming task
-      const int p1u = a.inter / (a.bn / 2);
-      const int p2u = a.H / a.bn;
-      ctrl->stream_rows = tr > 0 ? 0 : a.bn;
+      // a.bn: columns of an MFMA tile, or weight rows of a streaming task.
+      // A streaming plan whose largest expert needs more than the two token
+      // passes of a 64-row task takes 32-row tasks with four passes, so
+      // experts of up to 64 tokens read each weight row once.
+      int rows = a.bn;
+      if (tr == 0 && rows == kStreamRows * kRingWideGroups && maxcnt > kRingMaxPasses * kRingTokens)
+        rows = kStreamRows * kRingDenseGroups;
+      const int p1u = a.inter / (rows / 2);
+      const int p2u = a.H / rows;
+      ctrl->stream_rows = tr > 0 ? 0 : rows;
       ctrl->p1_per_unit = p1u;
       ctrl->p2_per_unit = p2u;
       // The streaming plan (small T) gets its slots from this block below, so
@@ -624,7 +634,7 @@ void router_kernel(RouterArgs a) {
   router_plan<RT>(a, nb, T, ps);
 }
 
-// Decode router (T <= 64).  A token block is 8 tokens; its 32 experts are
+// Expert-split router (T <= 256).  A token block is 8 tokens; its 32 experts are
 // split over 8 blocks of 4, so 8x more CUs share the gate.  Each block copies
 // its 4 gate rows and the token rows whole into LDS with direct-to-LDS loads
 // (no chunk loop) and runs one FMA chain per (token, expert) lane (the
@@ -961,7 +971,7 @@ template <> struct TileCfg<128> {
   static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, BK = 32;
 };
 template <> struct TileCfg<64> {
-  static constexpr int WAVES_M = 1, WM = 2, WAVES_N = 4, BK = 16;
+  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, BK = 32;
 };
 template <> struct TileCfg<32> {
   static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, BK = 16;
@@ -1289,7 +1299,6 @@ constexpr int kRingWaves = 8;                       // k-slice streaming waves
 constexpr int kRingThreads = (kRingWaves + 1) * 64; // + the control wave
 constexpr int kRingSteps = 16;                      // 16-float k steps per wave per task
 constexpr int kRingDepth = 4;                       // steps in flight ahead of the MFMAs
-constexpr int kRingTokens = 16;                     // tokens per MFMA pass
 constexpr int kRingSlice = kRingSteps * 16;         // floats of k per wave (256)
 constexpr int kRingMaxSlots = 4096;                 // slot -> token map kept in LDS
 static_assert(kRingWaves * kRingSlice == 2048, "k slices cover rows of <= 2048 floats");
@@ -1298,18 +1307,19 @@ static_assert(kRingSteps % kRingDepth == 0, "ring rotation realigns at task boun
 // expert's tokens (larger experts run in several groups).  A pass that holds
 // no tokens would still move 1 KiB per wave per step through the CU's
 // load-return path, so the kernel picks the count from the plan at run time.
-constexpr int kRingMaxPasses = 2;
+// (kRingMaxPasses, moe_internal.h)
 // 64-row tasks (batches from 32 tokens) share each token-row load across
 // their 4 row groups.  Up to 16 tokens per expert, a wave streams the groups
 // one after another and keeps its token slice in registers: a CU then reads
 // one 16-row block at a time, which streams at ~6.3 TB/s where reading 2 or 4
 // row blocks at once reaches 5.0-5.9 TB/s (measured with a bare load probe).
 // With two token passes the four groups are read at once.
-constexpr int kRingWideGroups = 4;  // row groups of a 64-row task
-// 32-row tasks with 4 passes: batches where every expert holds up to 64
-// tokens (the dense FFN's chunks hold all of them); 64-row tasks with 4
-// passes would need twice the LDS for their partials.
-constexpr int kRingDenseGroups = 2, kRingDensePasses = 4;
+// (kRingWideGroups, moe_internal.h)
+// 32-row tasks with 4 passes: batches whose largest expert holds 33-64
+// tokens (the router picks them from the counts; the dense FFN's chunks hold
+// all tokens), so each weight row is read once; 64-row tasks with 4 passes
+// would need twice the LDS for their partials.
+// (kRingDenseGroups, kRingDensePasses, moe_internal.h)
 
 // 64-row tasks read at once load 4 weight rows per step; with two token
 // passes half the depth keeps the ring within the register budget of 3 waves
@@ -1997,15 +2007,18 @@ __global__ void pack_w13_kernel(float4 *dst, const float4 *w1, const float4 *w3,
 // Launchers
 // ---------------------------------------------------------------------------
 
-// Router shapes: decode (T <= 64) uses 8-token blocks with all 32 experts, so
-// each of the 256 lanes runs one chain and a token block needs no hand-off
-// between blocks; larger T uses 64-token blocks and 8 chains per lane.
+// Router shapes: small T uses 8-token blocks with all 32 experts, so each of
+// the 256 lanes runs one chain and a token block needs no hand-off between
+// blocks; larger T uses 64-token blocks and 8 chains per lane.  The
+// expert-split router (8 blocks per 8 tokens, one block per CU for its LDS)
+// serves batches up to kSplitRouterTokens.
 constexpr int kSmallRT = kDecRT, kSmallKC = 256;
 constexpr int kLargeRT = 64, kLargeES = 1, kLargeKC = 64;
+constexpr int kSplitRouterTokens = 256;  // 505 vs 527 us per step at 256 tokens, 563 vs 545 at 384
 
-int router_tokens_per_block(int T) { return T <= 64 ? kSmallRT : kLargeRT; }
+int router_tokens_per_block(int T) { return T <= kSplitRouterTokens ? kSmallRT : kLargeRT; }
 
-bool router_fuses_norm(int T) { return T <= 64; }
+bool router_fuses_norm(int T) { return T <= kSplitRouterTokens; }
 
 hipError_t launch_router_dense(const RouterArgs &a, hipStream_t st) {
   if (a.T <= 64) {
@@ -2028,7 +2041,7 @@ hipError_t launch_rmsnorm(const float *h, const float *w, float *out, int T, int
 
 hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) {
   const bool small = a.T <= 64;
-  if (small && !from_logits) {
+  if (a.T <= kSplitRouterTokens && !from_logits) {
     const size_t lds = router_decode_lds(a.H);
     if (lds > 65536) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&router_decode_kernel),
