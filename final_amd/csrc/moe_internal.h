@@ -44,7 +44,8 @@ struct Ctrl {
   int p2_per_unit;
   int n_active;     // experts with count > 0
   int rtokens;      // tokens per router block (dispatch task size)
-  int stream_rows;  // streaming plan: weight rows per task (16 or 64)
+  int stream_rows;  // streaming plan: weight rows per task (16, 32 or 64)
+  int max_count;    // tokens of the largest expert
   int counts[kExperts];
   int offsets[kExperts + 1];
   int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)

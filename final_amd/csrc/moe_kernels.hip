@@ -348,6 +348,7 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
       const int p1u = a.inter / (rows / 2);
       const int p2u = a.H / rows;
       ctrl->stream_rows = tr > 0 ? 0 : rows;
+      ctrl->max_count = maxcnt;
       ctrl->p1_per_unit = p1u;
       ctrl->p2_per_unit = p2u;
       // The streaming plan (small T) gets its slots from this block below, so
@@ -1959,6 +1960,7 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   pl.p2u = c->p2_per_unit;
   pl.grid = gridDim.x;
   pl.rows = __builtin_amdgcn_readfirstlane(c->stream_rows);
+  const int maxcnt = __builtin_amdgcn_readfirstlane(c->max_count);
   // plans for this kernel take their slots from the router, and a task
   // covers 16, 32 or 64 rows
   if (c->n_rblocks != 0 ||
@@ -1968,9 +1970,6 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     return;
   }
   __syncthreads();
-  int maxcnt = 0;
-  for (int e = 0; e < kExperts; ++e) maxcnt = max(maxcnt, sh.counts[e]);
-  maxcnt = __builtin_amdgcn_readfirstlane(maxcnt);
   const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
   if (pl.rows == kStreamRows) {
     if (maxcnt <= kRingTokens) ring_role<1, 1>(a, sh, res, pl, ticks);
