@@ -87,14 +87,17 @@ static int plan_index(int rows) {
 // weight streaming is fastest up to 96 tokens (420 vs 428 us at 96), 64-row
 // MFMA tiles from 128 to 1024 tokens (527 vs 581 us at 256), 128-row tiles
 // from 1536 (1472 vs 1517 us).
-static int auto_plan(int T, bool stream_ok) {
-  if (T <= 96 && stream_ok) return 0;
+// The dense FFN's 4 chunk experts each hold every token, so its MFMA plans
+// have few tiles at small T: streaming stays fastest up to ~192 tokens (220
+// vs 284 us at 128), 64-row tiles from 256 (338 vs 365 us).
+static int auto_plan(int T, bool stream_ok, bool dense) {
+  if (T <= (dense ? 192 : 96) && stream_ok) return 0;
   if (T < 1536) return 64;
   return 128;
 }
 
 static int ctx_plan(const moe_ctx *ctx, int T) {
-  const int p = ctx->tile_override >= 0 ? ctx->tile_override : auto_plan(T, ctx->stream_ok);
+  const int p = ctx->tile_override >= 0 ? ctx->tile_override : auto_plan(T, ctx->stream_ok, ctx->dense);
   // the streaming plan keeps the batch's slot -> token map in LDS
   return p == 0 && T > stream_max_tokens() ? 64 : p;
 }
