@@ -966,23 +966,27 @@ __device__ __forceinline__ int unit_expert(const int *unit_off, int u) {
 // ---------------------------------------------------------------------------
 
 template <int BM> struct TileCfg;
-// 4 waves as WAVES_M x WAVES_N; a wave owns WM 32-row blocks x 2 32-column
-// blocks (for the gate/up phase: 32 columns of W1 and the same 32 of W3).
+// 4 waves as WAVES_M x WAVES_N; a wave owns WM 32-row blocks x WN 32-column
+// blocks.  B rows come in groups of 64 (gate/up phase: 32 rows of W1, then
+// the same 32 columns' rows of W3), and the epilogue pairs them through LDS.
 template <> struct TileCfg<128> {
-  static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, BK = 32;
+  static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, WN = 2, BK = 32;
 };
+// 64x128 tiles (128-1535 tokens): 64x256 tiles left 1.4 tiles per block at
+// T=256 (637 us per step, 527 with 64x128); 64x64 tiles balance the blocks
+// better but lose more per tile (537 us at T=256, 1208 vs 1115 at T=1024)
 template <> struct TileCfg<64> {
-  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, BK = 32;
+  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, WN = 2, BK = 32;
 };
 template <> struct TileCfg<32> {
-  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, BK = 16;
+  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 2, BK = 16;
 };
 
 template <int BM> struct Tile {
   using C = TileCfg<BM>;
-  static constexpr int WAVES_M = C::WAVES_M, WM = C::WM, WAVES_N = C::WAVES_N;
+  static constexpr int WAVES_M = C::WAVES_M, WM = C::WM, WAVES_N = C::WAVES_N, WN = C::WN;
   static constexpr int BK = C::BK;
-  static constexpr int BN = WAVES_N * 64;
+  static constexpr int BN = WAVES_N * WN * 32;
   static constexpr int PITCH = BK + 4;           // floats per LDS row
   static constexpr int KV = BK / 4;              // float4 per row per slab
   static constexpr int A_F4 = BM * KV;           // float4 per A slab
@@ -994,6 +998,8 @@ template <int BM> struct Tile {
   static constexpr int EPI_FLOATS = BM * CPITCH;
   static constexpr int LDS_FLOATS = SLAB_FLOATS > EPI_FLOATS ? SLAB_FLOATS : EPI_FLOATS;
   static_assert(BM == WAVES_M * WM * 32, "tile rows");
+  static_assert(WAVES_M * WAVES_N == kThreads / 64, "four waves");
+  static_assert(BN % 64 == 0, "whole W1/W3 row groups");
   static_assert(BK % 8 == 0, "k groups of 8");
 };
 
@@ -1048,7 +1054,7 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
                                           const float *brow0, int K, const AgentOut &out,
                                           int row0, int ldo, int col0) {
   using TL = Tile<BM>;
-  constexpr int WM = TL::WM, BK = TL::BK, PITCH = TL::PITCH, KV = TL::KV;
+  constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH, KV = TL::KV;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
   constexpr int ROWS_PER_PASS = kThreads / KV;  // rows one pass of loads covers
   static_assert(TL::B_F4 % kThreads == 0, "B slab splits evenly");
@@ -1078,11 +1084,11 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
   const int lds_st = lrow * PITCH + lc4;
 
   f32x4 ra[A_PER], rb[B_PER];
-  floatx16 acc[WM][2];
+  floatx16 acc[WM][WN];
 #pragma unroll
   for (int i = 0; i < WM; ++i)
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int c = 0; c < WN; ++c)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.0f;
 
@@ -1108,7 +1114,7 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
   __syncthreads();
   const int lr = lane & 31, lh = (lane >> 5) * 4;
   const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
-  const float *b_rd = Bs + (wn * 64 + lr) * PITCH + lh;
+  const float *b_rd = Bs + (wn * WN * 32 + lr) * PITCH + lh;
   for (int s = 0; s < nslab; s += L) {
 #pragma unroll
     for (int u = 0; u < L; ++u) {
@@ -1125,16 +1131,16 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
       if (wrows > 0) {
 #pragma unroll
         for (int g8 = 0; g8 < BK / 8; ++g8) {
-          f32x4 af[WM], bf[2];
+          f32x4 af[WM], bf[WN];
 #pragma unroll
           for (int i = 0; i < WM; ++i) af[i] = ld4(Ac + i * 32 * PITCH + g8 * 8);
 #pragma unroll
-          for (int c = 0; c < 2; ++c) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
+          for (int c = 0; c < WN; ++c) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
 #pragma unroll
           for (int i = 0; i < WM; ++i) {
             if (i > 0 && wrows <= 32) break;
 #pragma unroll
-            for (int c = 0; c < 2; ++c) {
+            for (int c = 0; c < WN; ++c) {
 #pragma unroll
               for (int q = 0; q < 4; ++q)
                 acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[c][q], acc[i][c], 0, 0, 0);
@@ -1151,9 +1157,10 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
   }
 
   // Epilogue through LDS (the slab buffers are free after the last barrier):
-  // results are written as a [BM][NC] tile, then stored as whole-row float4s.
-  // 32x32 f32 MFMA result layout: lane l holds column l % 32 and rows
-  // 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
+  // the products are written as a [BM][BN] tile in B-row order, then stored
+  // as whole-row float4s; gate/up tiles store silu(W1 x) * (W3 x) of each
+  // 64-row group's two halves.  32x32 f32 MFMA result layout: lane l holds
+  // column l % 32 and rows 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
   constexpr int NC = GATED ? TL::BN / 2 : TL::BN;  // output columns of the tile
   constexpr int CP = TL::CPITCH;
   float *Cs = lds;
@@ -1163,12 +1170,8 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = wrow0 + i * 32 + 8 * (r >> 2) + (lane >> 5) * 4 + (r & 3);
-        if (GATED) {
-          Cs[row * CP + wn * 32 + lr] = silu(acc[i][0][r]) * acc[i][1][r];
-        } else {
-          Cs[row * CP + wn * 64 + lr] = acc[i][0][r];
-          Cs[row * CP + wn * 64 + 32 + lr] = acc[i][1][r];
-        }
+#pragma unroll
+        for (int c = 0; c < WN; ++c) Cs[row * CP + (wn * WN + c) * 32 + lr] = acc[i][c][r];
       }
     }
   }
@@ -1176,9 +1179,18 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
   constexpr int NC4 = NC / 4;
   for (int f = tid; f < BM * NC4; f += kThreads) {
     const int row = f / NC4, c4 = (f % NC4) * 4;
-    if (row < rows_valid)
-      out.store((uint32_t)(((size_t)(row0 + row) * ldo + col0 + c4) * sizeof(float)),
-                ld4(Cs + row * CP + c4));
+    if (row < rows_valid) {
+      f32x4 v;
+      if (GATED) {
+        const float *g = Cs + row * CP + (c4 >> 5) * 64 + (c4 & 31);
+        const f32x4 w1 = ld4(g), w3 = ld4(g + 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = silu(w1[j]) * w3[j];
+      } else {
+        v = ld4(Cs + row * CP + c4);
+      }
+      out.store((uint32_t)(((size_t)(row0 + row) * ldo + col0 + c4) * sizeof(float)), v);
+    }
   }
   __syncthreads();  // Cs aliases the slab buffers of the next tile
 }
