@@ -2024,7 +2024,10 @@ __global__ void pack_w13_kernel(float4 *dst, const float4 *w1, const float4 *w3,
 // expert-split router (8 blocks per 8 tokens, one block per CU for its LDS)
 // serves batches up to kSplitRouterTokens.
 constexpr int kSmallRT = kDecRT, kSmallKC = 256;
-constexpr int kLargeRT = 64, kLargeES = 1, kLargeKC = 64;
+constexpr int kLargeRT = 64, kLargeKC = 64;
+// Larger T: the experts of a 64-token block are split over ES blocks while
+// that keeps the grid within about one block per CU (T=4096: 64 token blocks
+// x 4, router 90 -> 51 us; at T=16384 the unsplit 256 blocks are fastest).
 constexpr int kSplitRouterTokens = 256;  // 505 vs 527 us per step at 256 tokens, 563 vs 545 at 384
 
 int router_tokens_per_block(int T) { return T <= kSplitRouterTokens ? kSmallRT : kLargeRT; }
@@ -2072,8 +2075,15 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
     else
       hipLaunchKernelGGL((router_kernel<true, kLargeRT, 1, kLargeKC>), dim3(nb), dim3(kThreads), 0, st, a);
   } else {
-    hipLaunchKernelGGL((router_kernel<false, kLargeRT, kLargeES, kLargeKC>), dim3(nb * kLargeES),
-                       dim3(kThreads), 0, st, a);
+    if (nb <= 64)
+      hipLaunchKernelGGL((router_kernel<false, kLargeRT, 4, 2 * kLargeKC>), dim3(nb * 4),
+                         dim3(kThreads), 0, st, a);
+    else if (nb <= 128)
+      hipLaunchKernelGGL((router_kernel<false, kLargeRT, 2, kLargeKC>), dim3(nb * 2),
+                         dim3(kThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((router_kernel<false, kLargeRT, 1, kLargeKC>), dim3(nb), dim3(kThreads),
+                         0, st, a);
   }
   return hipGetLastError();
 }
