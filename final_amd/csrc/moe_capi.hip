@@ -179,7 +179,8 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
       (rc = dev_alloc(ctx, &ctx->s.tb_done, nb)) ||
       (rc = dev_alloc(ctx, &ctx->s.slot_token, S)) ||
       (rc = dev_alloc(ctx, &ctx->s.inter, S * I)) ||
-      (rc = dev_alloc(ctx, &ctx->s.sout, S * H))) {
+      (rc = dev_alloc(ctx, &ctx->s.sout, S * H)) ||
+      (rc = dev_alloc(ctx, &ctx->s.ccount, Tm * (H / 64)))) {
     free_all(ctx);
     delete ctx;
     return rc;

@@ -13,7 +13,6 @@ constexpr int kDenseChunks = 4;  // dense FFN: intermediate cut into 4 chunk "ex
 constexpr int kTopK = 4;         // NUM_EXPERTS_PER_TOK, config.h:15
 constexpr int kMinRouterTokens = 8;  // smallest token block of the router
 constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
-constexpr int kCombineTokens = 8;  // tokens per combine task
 constexpr int kStreamRows = 16;  // weight rows per streaming-plan task (small batches)
 constexpr int kStreamWideTokens = 32;  // batches from this size use 64-row tasks
 // Streaming kernel shapes: tokens per MFMA pass; token passes of 16- and
@@ -31,7 +30,6 @@ struct Ctrl {
   int router_done;  // router blocks finished (last-block election)
   int head;         // expert-kernel task queue head
   int assign_done;  // dispatch (slot assignment) tasks finished
-  int p2_done;      // down-projection tasks finished
   int err;          // sticky: 1 = a bounded wait expired
   int num_tokens;
   int tile_rows;    // 0 = streaming kernel, else MFMA rows per tile
@@ -74,6 +72,7 @@ struct Scratch {
   uint32_t sout_bytes;
   Ctrl *ctrl;
   int *dep;              // [max_units]
+  int *ccount;           // [Tmax][H/64]: expert outputs landed per (token, column tile)
 };
 
 struct RouterArgs {

@@ -358,13 +358,14 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
       ctrl->rtokens = RT;
       ctrl->n_p1 = units * p1u;
       ctrl->n_p2 = units * p2u;
-      ctrl->n_comb = (T + kCombineTokens - 1) / kCombineTokens;
+      // the MFMA plans combine inside their down tiles; the streaming kernel
+      // runs one combine task per token
+      ctrl->n_comb = tr > 0 ? 0 : T;
       ctrl->n_total = ndisp + units * p1u + units * p2u + ctrl->n_comb;
       ctrl->num_tokens = T;
       ctrl->tile_rows = tr;
       ctrl->head = 0;
       ctrl->assign_done = 0;
-      ctrl->p2_done = 0;
       ps.units = units;
     }
   }
@@ -866,86 +867,80 @@ __device__ void assign_task(const ExpertArgs &a, int q, int rt) {
   }
 }
 
-// Combine task q: tokens [8q, 8q+8).  y = residual + sum_k w_k * out_k with
-// the reference's order: sum from 0.0f, fma over k ascending
-// (layer.cu:708-720), then the residual add (layer.cu:1866-1871).  The
-// tokens' slots and weights are staged in LDS first (combine_route, after
-// the dispatch and before the wait for the expert outputs), so the output
-// loads of two tokens at a time are all independent.
-struct CombineRoute {
-  int slot[kCombineTokens * kTopK];  // -1: no expert output (skipped)
-  float w[kCombineTokens * kTopK];
-};
-
-__device__ __forceinline__ void combine_route(const ExpertArgs &a, int q, CombineRoute &r) {
-  const int tid = threadIdx.x;
-  if (tid < kCombineTokens * kTopK) {
-    const int tok = q * kCombineTokens + tid / kTopK;
-    int slot = -1;
-    float w = 0.0f;
-    if (tok < a.T) {
-      slot = a.s.pos[(size_t)tok * kTopK + tid % kTopK];
-      w = a.s.wts[(size_t)tok * kTopK + tid % kTopK];
-      if (slot < 0 || slot >= a.T * kTopK) slot = -1;
-    }
-    r.slot[tid] = slot;
-    r.w[tid] = w;
-  }
-}
-
-__device__ void combine_task(const ExpertArgs &a, int q, const CombineRoute &r) {
-#pragma clang fp contract(off)
-  constexpr int TB = 2;  // tokens per batch: 10 loads in flight per thread
-  const int H4 = a.H >> 2;
-  const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
-  const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
-  float4 *y4 = reinterpret_cast<float4 *>(a.y);
-  const int t0 = q * kCombineTokens;
-  const int nt = min(kCombineTokens, a.T - t0);
-  for (int k0 = 0; k0 < nt; k0 += TB) {
-    for (int c4 = threadIdx.x; c4 < H4; c4 += kThreads) {
-      float4 v[TB][kTopK], rv[TB];
-#pragma unroll
-      for (int i = 0; i < TB; ++i) {
-        const int m = min(k0 + i, nt - 1);
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k) {
-          const int slot = r.slot[m * kTopK + k];
-          v[i][k] = so[(size_t)(slot < 0 ? 0 : slot) * H4 + c4];
-        }
-        rv[i] = r4 ? r4[(size_t)(t0 + m) * H4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-#pragma unroll
-      for (int i = 0; i < TB; ++i) {
-        if (k0 + i >= nt) break;
-        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-        for (int k = 0; k < kTopK; ++k) {
-          if (r.slot[(k0 + i) * kTopK + k] < 0) continue;
-          const float wk = r.w[(k0 + i) * kTopK + k];
-          acc.x = __builtin_fmaf(v[i][k].x, wk, acc.x);
-          acc.y = __builtin_fmaf(v[i][k].y, wk, acc.y);
-          acc.z = __builtin_fmaf(v[i][k].z, wk, acc.z);
-          acc.w = __builtin_fmaf(v[i][k].w, wk, acc.w);
-        }
-        if (r4) {
-          acc.x = rv[i].x + acc.x;
-          acc.y = rv[i].y + acc.y;
-          acc.z = rv[i].z + acc.z;
-          acc.w = rv[i].w + acc.w;
-        }
-        y4[(size_t)(t0 + k0 + i) * H4 + c4] = acc;
-      }
-    }
-  }
-}
-
 // Token of a slot, clamped into [0, T) so a bad plan can never address
 // outside x (the dispatch guards flag such plans in ctrl->err).
 __device__ __forceinline__ int slot_tok(const ExpertArgs &a, int slot) {
   const int t = a.s.slot_token[slot];
   return t < 0 ? 0 : (t >= a.T ? a.T - 1 : t);
 }
+
+// Combine inside the down tiles (MFMA plans).  A down tile counts, for each
+// of its rows, one more expert output of that row's token in the tile's
+// column range; the block whose count completes a token's expert outputs
+// computes y for those columns with the reference's order: sum from 0.0f,
+// fma over k ascending (layer.cu:708-720), then the residual add
+// (layer.cu:1866-1871).  The arithmetic is the same whichever block does it.
+// The tile's stores have completed before it counts (agent-scope stores), and
+// the completing block acquires before it reads the other tiles' outputs.
+// y may alias the residual: a thread reads its columns before it writes them.
+template <int BN>
+__device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int ht, int nht,
+                             int *s_list, int *s_n) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  __builtin_amdgcn_s_waitcnt(0);  // this block's expert-output stores have completed
+  if (tid == 0) *s_n = 0;
+  __syncthreads();
+  if (tid < rows) {
+    const int t = slot_tok(a, slot0 + tid);
+    int nvalid = 0;
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) nvalid += a.s.pos[(size_t)t * kTopK + k] >= 0;
+    if (fetch_add(&a.s.ccount[(size_t)t * nht + ht], 1) == nvalid - 1)
+      s_list[atomicAdd(s_n, 1)] = t;
+  }
+  __syncthreads();
+  const int n = *s_n;
+  if (n == 0) return;
+  if (tid == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __syncthreads();
+  constexpr int NC4 = BN / 4;
+  const int H4 = a.H >> 2;
+  const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
+  const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
+  float4 *y4 = reinterpret_cast<float4 *>(a.y);
+  for (int f = tid; f < n * NC4; f += kThreads) {
+    const int t = s_list[f / NC4], c4 = ht * NC4 + f % NC4;
+    float4 v[kTopK];
+    float w[kTopK];
+    bool ok[kTopK];
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+      const int slot = a.s.pos[(size_t)t * kTopK + k];
+      ok[k] = slot >= 0 && slot < a.T * kTopK;
+      w[k] = a.s.wts[(size_t)t * kTopK + k];
+      v[k] = so[(size_t)(ok[k] ? slot : 0) * H4 + c4];
+    }
+    const float4 rv = r4 ? r4[(size_t)t * H4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < kTopK; ++k) {
+      if (!ok[k]) continue;
+      acc.x = __builtin_fmaf(v[k].x, w[k], acc.x);
+      acc.y = __builtin_fmaf(v[k].y, w[k], acc.y);
+      acc.z = __builtin_fmaf(v[k].z, w[k], acc.z);
+      acc.w = __builtin_fmaf(v[k].w, w[k], acc.w);
+    }
+    if (r4) {
+      acc.x = rv.x + acc.x;
+      acc.y = rv.y + acc.y;
+      acc.z = rv.z + acc.z;
+      acc.w = rv.w + acc.w;
+    }
+    y4[(size_t)t * H4 + c4] = acc;
+  }
+}
+
 
 // layer.cu:728 d_silu_opt.
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
@@ -1205,7 +1200,8 @@ void expert_mfma_kernel(ExpertArgs a) {
   __shared__ int s_offsets[kExperts + 1];
   __shared__ int s_counts[kExperts];
   __shared__ int s_aoff[BM];
-  __shared__ CombineRoute s_route;
+  __shared__ int s_comb[BM];
+  __shared__ int s_ncomb;
   Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
   if (tid <= kExperts) {
@@ -1224,7 +1220,13 @@ void expert_mfma_kernel(ExpertArgs a) {
     int next = 0;
     if (tid == 0) next = claim(&c->head);  // claim ahead
     if (task < nb) {
-      assign_task(a, task, c->rtokens);
+      const int rt = c->rtokens;
+      assign_task(a, task, rt);
+      // this router block's tokens start with no expert outputs counted
+      for (int i = tid; i < rt * p2u; i += kThreads) {
+        const int tok = task * rt + i / p2u;
+        if (tok < a.T) st_agent(&a.s.ccount[(size_t)tok * p2u + i % p2u], 0);
+      }
       block_signal(&c->assign_done);
     } else if (task < nb + n1) {
       const int q = task - nb;
@@ -1254,15 +1256,7 @@ void expert_mfma_kernel(ExpertArgs a) {
       mfma_tile<BM, false>(lds, a.s.inter + (size_t)slot0 * I,
                            a.s.inter_bytes - (uint32_t)((size_t)slot0 * I * sizeof(float)), s_aoff,
                            rows, brow0, I, sout_out, slot0, H, ht * TL::BN);
-      block_signal(&c->p2_done);
-    } else {
-      const int q = task - nb - n1 - n2;
-      // slots are final once the dispatch tasks are done (long before the
-      // down tiles): stage them, then wait for the expert outputs
-      block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
-      combine_route(a, q, s_route);
-      block_wait(&c->p2_done, n2, a.wait_limit, &c->err);  // ends with a block barrier
-      combine_task(a, q, s_route);
+      tile_combine<TL::BN>(a, slot0, rows, ht, p2u, s_comb, &s_ncomb);
     }
     __syncthreads();
     if (tid == 0) s_task = next;
@@ -1624,7 +1618,7 @@ __device__ __forceinline__ RingRoute ring_route(const ExpertArgs &a, int tok) {
 }
 
 // Combine of token tok by the 512 threads of the streaming waves (thread ts:
-// float4 columns ts, ts + 512, ...), with the arithmetic of combine_task:
+// float4 columns ts, ts + 512, ...), with the arithmetic of tile_combine:
 // FMA chain over k ascending, then the residual.  The expert outputs are
 // loaded coherently and reloaded while any is still kUnwritten.  y may alias
 // the residual: each thread reads its columns before it writes them.  False
