@@ -13,6 +13,7 @@ constexpr int kDenseChunks = 4;  // dense FFN: intermediate cut into 4 chunk "ex
 constexpr int kTopK = 4;         // NUM_EXPERTS_PER_TOK, config.h:15
 constexpr int kMinRouterTokens = 8;  // smallest token block of the router
 constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
+constexpr int kCombineCols = 64;  // columns per combine counter (MFMA plans)
 constexpr int kStreamRows = 16;  // weight rows per streaming-plan task (small batches)
 constexpr int kStreamWideTokens = 32;  // batches from this size use 64-row tasks
 // Streaming kernel shapes: tokens per MFMA pass; token passes of 16- and
@@ -44,6 +45,7 @@ struct Ctrl {
   int rtokens;      // tokens per router block (dispatch task size)
   int stream_rows;  // streaming plan: weight rows per task (16, 32 or 64)
   int max_count;    // tokens of the largest expert
+  int tail_units;   // last units whose down tiles run as two half-width tiles
   int counts[kExperts];
   int offsets[kExperts + 1];
   int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)
@@ -84,6 +86,7 @@ struct RouterArgs {
   int tile_rows;         // plan: 0 streaming, else MFMA tile rows
   int inter;             // I (for task counts)
   int bn;                // MFMA n-tile width (columns of the B tile)
+  int tail_units;        // MFMA plans: last units whose down tiles run at half width
   int max_units;
   const float *norm_w;   // post-attention RMSNorm weight [H]: x is h, normalise it (T <= 64 only)
   float *xn;             // [T][H]: the normalised rows, for the expert kernel

@@ -356,12 +356,15 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
       const int ndisp = tr > 0 ? nb : 0;
       ctrl->n_rblocks = ndisp;
       ctrl->rtokens = RT;
+      // the last tail units split each down tile in two halves
+      const int tail = tr > 0 ? min(units, a.tail_units) : 0;
+      ctrl->tail_units = tail;
       ctrl->n_p1 = units * p1u;
-      ctrl->n_p2 = units * p2u;
+      ctrl->n_p2 = (units + tail) * p2u;
       // the MFMA plans combine inside their down tiles; the streaming kernel
       // runs one combine task per token
       ctrl->n_comb = tr > 0 ? 0 : T;
-      ctrl->n_total = ndisp + units * p1u + units * p2u + ctrl->n_comb;
+      ctrl->n_total = ndisp + units * p1u + (units + tail) * p2u + ctrl->n_comb;
       ctrl->num_tokens = T;
       ctrl->tile_rows = tr;
       ctrl->head = 0;
@@ -875,19 +878,21 @@ __device__ __forceinline__ int slot_tok(const ExpertArgs &a, int slot) {
 }
 
 // Combine inside the down tiles (MFMA plans).  A down tile counts, for each
-// of its rows, one more expert output of that row's token in the tile's
-// column range; the block whose count completes a token's expert outputs
-// computes y for those columns with the reference's order: sum from 0.0f,
+// of its rows and each kCombineCols-wide column range it covers, one more
+// expert output of that row's token; the block whose count completes a
+// token's expert outputs computes y for those columns with the reference's order: sum from 0.0f,
 // fma over k ascending (layer.cu:708-720), then the residual add
 // (layer.cu:1866-1871).  The arithmetic is the same whichever block does it.
 // The tile's stores have completed before it counts (agent-scope stores), and
 // the completing block acquires before it reads the other tiles' outputs.
 // y may alias the residual: a thread reads its columns before it writes them.
 template <int BN>
-__device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int ht, int nht,
-                             int *s_list, int *s_n) {
+__device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int col0, int *s_list,
+                             int *s_n) {
 #pragma clang fp contract(off)
+  constexpr int NJ = BN / kCombineCols;  // counters the tile's columns cover
   const int tid = threadIdx.x;
+  const int ncc = a.H / kCombineCols, j0 = col0 / kCombineCols;
   __builtin_amdgcn_s_waitcnt(0);  // this block's expert-output stores have completed
   if (tid == 0) *s_n = 0;
   __syncthreads();
@@ -896,21 +901,24 @@ __device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int ht, i
     int nvalid = 0;
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) nvalid += a.s.pos[(size_t)t * kTopK + k] >= 0;
-    if (fetch_add(&a.s.ccount[(size_t)t * nht + ht], 1) == nvalid - 1)
-      s_list[atomicAdd(s_n, 1)] = t;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (fetch_add(&a.s.ccount[(size_t)t * ncc + j0 + j], 1) == nvalid - 1)
+        s_list[atomicAdd(s_n, 1)] = t * ncc + j0 + j;
   }
   __syncthreads();
   const int n = *s_n;
   if (n == 0) return;
   if (tid == 0) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   __syncthreads();
-  constexpr int NC4 = BN / 4;
+  constexpr int NC4 = kCombineCols / 4;
   const int H4 = a.H >> 2;
   const float4 *so = reinterpret_cast<const float4 *>(a.s.sout);
   const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
   float4 *y4 = reinterpret_cast<float4 *>(a.y);
   for (int f = tid; f < n * NC4; f += kThreads) {
-    const int t = s_list[f / NC4], c4 = ht * NC4 + f % NC4;
+    const int item = s_list[f / NC4];
+    const int t = item / ncc, c4 = (item % ncc) * NC4 + f % NC4;
     float4 v[kTopK];
     float w[kTopK];
     bool ok[kTopK];
@@ -977,8 +985,21 @@ template <> struct TileCfg<32> {
   static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 2, BK = 16;
 };
 
-template <int BM> struct Tile {
-  using C = TileCfg<BM>;
+// Half-width down tiles for the last units of a launch (same rows, half the
+// columns), so the last round of tiles is half as long.
+template <int BM> struct TileHalfCfg;
+template <> struct TileHalfCfg<128> {
+  static constexpr int WAVES_M = 4, WM = 1, WAVES_N = 1, WN = 2, BK = 32;
+};
+template <> struct TileHalfCfg<64> {
+  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, WN = 1, BK = 32;
+};
+template <> struct TileHalfCfg<32> {
+  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 1, BK = 16;
+};
+
+template <int BM_, typename C> struct TileT {
+  static constexpr int BM = BM_;
   static constexpr int WAVES_M = C::WAVES_M, WM = C::WM, WAVES_N = C::WAVES_N, WN = C::WN;
   static constexpr int BK = C::BK;
   static constexpr int BN = WAVES_N * WN * 32;
@@ -997,6 +1018,8 @@ template <int BM> struct Tile {
   static_assert(BN % 64 == 0, "whole W1/W3 row groups");
   static_assert(BK % 8 == 0, "k groups of 8");
 };
+template <int BM> using Tile = TileT<BM, TileCfg<BM>>;
+template <int BM> using TileHalf = TileT<BM, TileHalfCfg<BM>>;
 
 // Slab staging of the MFMA tile: buffer float4 loads into registers (A rows
 // gathered; an empty row's offset lies past the buffer, so its loads return
@@ -1043,12 +1066,12 @@ constexpr int kTilePrefetch = 3;
 //
 // Slab pipeline: global loads of slab s+1 are in flight while the MFMAs of
 // slab s run from LDS; one barrier per slab (double-buffered LDS).
-template <int BM, bool GATED>
+template <typename TL, bool GATED>
 __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32_t abytes,
                                           const int *aoff, int rows_valid,
                                           const float *brow0, int K, const AgentOut &out,
                                           int row0, int ldo, int col0) {
-  using TL = Tile<BM>;
+  constexpr int BM = TL::BM;
   constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH, KV = TL::KV;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
   constexpr int ROWS_PER_PASS = kThreads / KV;  // rows one pass of loads covers
@@ -1200,7 +1223,7 @@ void expert_mfma_kernel(ExpertArgs a) {
   __shared__ int s_offsets[kExperts + 1];
   __shared__ int s_counts[kExperts];
   __shared__ int s_aoff[BM];
-  __shared__ int s_comb[BM];
+  __shared__ int s_comb[BM * (Tile<BM>::BN / kCombineCols)];
   __shared__ int s_ncomb;
   Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
@@ -1211,6 +1234,7 @@ void expert_mfma_kernel(ExpertArgs a) {
   if (tid < kExperts) s_counts[tid] = c->counts[tid];
   const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
   const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
+  const int nunits = n1 / p1u, tail = c->tail_units;
   const int H = a.H, I = a.I;
   const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
   if (tid == 0) s_task = claim(&c->head);
@@ -1223,9 +1247,10 @@ void expert_mfma_kernel(ExpertArgs a) {
       const int rt = c->rtokens;
       assign_task(a, task, rt);
       // this router block's tokens start with no expert outputs counted
-      for (int i = tid; i < rt * p2u; i += kThreads) {
-        const int tok = task * rt + i / p2u;
-        if (tok < a.T) st_agent(&a.s.ccount[(size_t)tok * p2u + i % p2u], 0);
+      const int ncc = H / kCombineCols;
+      for (int i = tid; i < rt * ncc; i += kThreads) {
+        const int tok = task * rt + i / ncc;
+        if (tok < a.T) st_agent(&a.s.ccount[(size_t)tok * ncc + i % ncc], 0);
       }
       block_signal(&c->assign_done);
     } else if (task < nb + n1) {
@@ -1239,12 +1264,17 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
       __syncthreads();
       const float *brow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TL::BN) * H;
-      mfma_tile<BM, true>(lds, a.x, (uint32_t)((size_t)a.T * H * sizeof(float)), s_aoff, rows,
+      mfma_tile<Tile<BM>, true>(lds, a.x, (uint32_t)((size_t)a.T * H * sizeof(float)), s_aoff, rows,
                           brow0, H, inter_out, slot0, I, nt * (TL::BN / 2));
       block_signal(&a.s.dep[u]);
     } else if (task < nb + n1 + n2) {
+      // down tiles: full width for the first units, two half-width tiles per
+      // column range for the last tail units
       const int q = task - nb - n1;
-      const int u = q / p2u, ht = q % p2u;
+      const int nfull = (nunits - tail) * p2u;
+      const bool half = q >= nfull;
+      const int u = half ? nunits - tail + (q - nfull) / (2 * p2u) : q / p2u;
+      const int ht = half ? (q - nfull) % (2 * p2u) : q % p2u;
       const int e = unit_expert(s_unit_off, u);
       const int m0 = (u - s_unit_off[e]) * BM;
       const int rows = min(BM, s_counts[e] - m0);
@@ -1252,11 +1282,20 @@ void expert_mfma_kernel(ExpertArgs a) {
       block_wait(&a.s.dep[u], p1u, a.wait_limit, &c->err);
       if (tid < BM) s_aoff[tid] = tid < rows ? tid * I : -1;
       __syncthreads();
-      const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
-      mfma_tile<BM, false>(lds, a.s.inter + (size_t)slot0 * I,
-                           a.s.inter_bytes - (uint32_t)((size_t)slot0 * I * sizeof(float)), s_aoff,
-                           rows, brow0, I, sout_out, slot0, H, ht * TL::BN);
-      tile_combine<TL::BN>(a, slot0, rows, ht, p2u, s_comb, &s_ncomb);
+      const float *abase = a.s.inter + (size_t)slot0 * I;
+      const uint32_t abytes = a.s.inter_bytes - (uint32_t)((size_t)slot0 * I * sizeof(float));
+      if (half) {
+        using TH = TileHalf<BM>;
+        const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TH::BN) * I;
+        mfma_tile<TH, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0, H,
+                             ht * TH::BN);
+        tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb);
+      } else {
+        const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
+        mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0, H,
+                             ht * TL::BN);
+        tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb);
+      }
     }
     __syncthreads();
     if (tid == 0) s_task = next;
