@@ -1066,11 +1066,14 @@ constexpr int kTilePrefetch = 3;
 //
 // Slab pipeline: global loads of slab s+1 are in flight while the MFMAs of
 // slab s run from LDS; one barrier per slab (double-buffered LDS).
+// Thread 0 claims the block's next task from `head` once the MFMAs are done
+// (returned; other threads return 0): the epilogue hides the claim's round
+// trip, and a block commits to its next task only near the end of this one.
 template <typename TL, bool GATED>
-__device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32_t abytes,
-                                          const int *aoff, int rows_valid,
-                                          const float *brow0, int K, const AgentOut &out,
-                                          int row0, int ldo, int col0) {
+__device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_t abytes,
+                                         const int *aoff, int rows_valid,
+                                         const float *brow0, int K, const AgentOut &out,
+                                         int row0, int ldo, int col0, int *head) {
   constexpr int BM = TL::BM;
   constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH, KV = TL::KV;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
@@ -1174,6 +1177,8 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
     }
   }
 
+  const int next = threadIdx.x == 0 ? claim(head) : 0;
+
   // Epilogue through LDS (the slab buffers are free after the last barrier):
   // the products are written as a [BM][BN] tile in B-row order, then stored
   // as whole-row float4s; gate/up tiles store silu(W1 x) * (W3 x) of each
@@ -1211,6 +1216,7 @@ __device__ __forceinline__ void mfma_tile(float *lds, const float *abase, uint32
     }
   }
   __syncthreads();  // Cs aliases the slab buffers of the next tile
+  return next;
 }
 
 template <int BM>
@@ -1241,8 +1247,7 @@ void expert_mfma_kernel(ExpertArgs a) {
   __syncthreads();
   int task = s_task;
   while (task < ntot) {
-    int next = 0;
-    if (tid == 0) next = claim(&c->head);  // claim ahead
+    int next = 0;  // the block's next task (thread 0), claimed near this one's end
     if (task < nb) {
       const int rt = c->rtokens;
       assign_task(a, task, rt);
@@ -1253,6 +1258,7 @@ void expert_mfma_kernel(ExpertArgs a) {
         if (tok < a.T) st_agent(&a.s.ccount[(size_t)tok * ncc + i % ncc], 0);
       }
       block_signal(&c->assign_done);
+      if (tid == 0) next = claim(&c->head);
     } else if (task < nb + n1) {
       const int q = task - nb;
       const int u = q / p1u, nt = q % p1u;
@@ -1264,8 +1270,9 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
       __syncthreads();
       const float *brow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TL::BN) * H;
-      mfma_tile<Tile<BM>, true>(lds, a.x, (uint32_t)((size_t)a.T * H * sizeof(float)), s_aoff, rows,
-                          brow0, H, inter_out, slot0, I, nt * (TL::BN / 2));
+      next = mfma_tile<Tile<BM>, true>(lds, a.x, (uint32_t)((size_t)a.T * H * sizeof(float)), s_aoff,
+                                       rows, brow0, H, inter_out, slot0, I, nt * (TL::BN / 2),
+                                       &c->head);
       block_signal(&a.s.dep[u]);
     } else if (task < nb + n1 + n2) {
       // down tiles: full width for the first units, two half-width tiles per
@@ -1287,13 +1294,13 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (half) {
         using TH = TileHalf<BM>;
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TH::BN) * I;
-        mfma_tile<TH, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0, H,
-                             ht * TH::BN);
+        next = mfma_tile<TH, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
+                                    H, ht * TH::BN, &c->head);
         tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb);
       } else {
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
-        mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0, H,
-                             ht * TL::BN);
+        next = mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
+                                    H, ht * TL::BN, &c->head);
         tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb);
       }
     }
