@@ -73,6 +73,26 @@ def test_every_kernel_plan(plan, block, real_weights, oracle_mod):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("T", [6000, 8200])
+def test_router_block_splits(T, block, real_weights, oracle_mod):
+    """Large batches split each 64-token router block's experts over 4, 2 or 1
+    blocks (6000 tokens: 94 token blocks, split in 2; 8200: 129, unsplit;
+    4096 in test_forward_matches_oracle: split in 4).  Routing checked on
+    every token, y on every 8th."""
+    from final_amd import workloads as W
+    say(f"[router split] T={T} plan={block.plan(T)}")
+    x = W.gen_x(T, seed=5)
+    y = block.forward(x)
+    rt = block.last_routing()
+    mask = np.zeros(T, np.uint8)
+    mask[::8] = 1
+    ref = oracle_forward(oracle_mod, real_weights, x, token_mask=mask)
+    check_routing(rt, ref)
+    sel = mask.astype(bool)
+    np.testing.assert_allclose(y[sel], ref["y"][sel], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
 def test_zipf_skew_t16384(block, real_weights, oracle_mod):
     """Skewed routing: Zipf(1.2) expert frequencies, 3 empty experts, one expert
     taking nearly every token.  Routing checked on all 16384 tokens; y on
