@@ -43,7 +43,7 @@ def check_routing(rt, ref):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T", [1, 8, 64, 100, 256, 1000, 4096])
+@pytest.mark.parametrize("T", [1, 8, 64, 100, 128, 160, 256, 1000, 4096])
 def test_forward_matches_oracle(T, block, real_weights, oracle_mod):
     from final_amd import workloads as W
     say(f"[parity] T={T} plan={block.plan(T)}")
