@@ -37,7 +37,7 @@ struct Ctrl {
   int n_rblocks;    // router blocks = dispatch tasks
   int n_p1;         // gate/up (W1,W3) tasks
   int n_p2;         // down (W2) tasks
-  int n_comb;       // combine tasks
+  int n_comb;       // combine tasks (streaming plan; MFMA plans combine in their down tiles)
   int n_total;      // sum of the four
   int p1_per_unit;  // W1W3 tasks per m-tile (MFMA) or per expert (streaming)
   int p2_per_unit;
