@@ -23,6 +23,10 @@ constexpr int kRingTokens = 16;
 constexpr int kRingMaxPasses = 2;
 constexpr int kRingWideGroups = 4;
 constexpr int kRingDenseGroups = 2, kRingDensePasses = 4;
+// Units (experts) whose down rows the streaming plan splits into 16-row tasks
+// at the end of the queue when its 64-row tasks are streamed in sub-groups
+// (T=64: 277 us with none, 275.7 with 2, 274.4 with 6, 277.4 with 12).
+constexpr int kRingTailUnits = 6;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset

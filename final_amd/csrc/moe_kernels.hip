@@ -357,15 +357,20 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
       const int ndisp = tr > 0 ? nb : 0;
       ctrl->n_rblocks = ndisp;
       ctrl->rtokens = RT;
-      // the last tail units split each down tile in two halves
-      const int tail = tr > 0 ? min(units, a.tail_units) : 0;
+      // MFMA plans: the last tail units split each down tile in two halves;
+      // streaming plan with 64-row tasks of up to 16 tokens: the last units'
+      // down rows run as 16-row tasks (4 per 64-row task)
+      const int tail = tr > 0 ? min(units, a.tail_units)
+                       : (rows == kStreamRows * kRingWideGroups && maxcnt <= kRingTokens
+                              ? min(units, kRingTailUnits) : 0);
+      const int tail_mult = tr > 0 ? 2 : kRingWideGroups;
       ctrl->tail_units = tail;
       ctrl->n_p1 = units * p1u;
-      ctrl->n_p2 = (units + tail) * p2u;
+      ctrl->n_p2 = (units - tail + tail * tail_mult) * p2u;
       // the MFMA plans combine inside their down tiles; the streaming kernel
       // runs one combine task per token
       ctrl->n_comb = tr > 0 ? 0 : T;
-      ctrl->n_total = ndisp + units * p1u + (units + tail) * p2u + ctrl->n_comb;
+      ctrl->n_total = ndisp + ctrl->n_p1 + ctrl->n_p2 + ctrl->n_comb;
       ctrl->num_tokens = T;
       ctrl->tile_rows = tr;
       ctrl->head = 0;
@@ -1436,20 +1441,23 @@ __device__ __forceinline__ bool ring_wait(const int *p, Cond cond, int *abort_fl
 
 struct RingPlan {
   int n1, n2, ncomb, p1u, p2u, grid, rows;
+  int sub;                // row sub-groups streamed one after another per task
+  int tail_q, tail_u0;    // down tasks from tail_q: 16-row tasks of units tail_u0..
 };
 
 // A row task, wave-uniform.  kind: 1 gate/up rows, 2 down rows, 4 none (the
 // queue ran out).  A row task runs in groups of up to 16 * P tokens (one
 // pass of the ring per group).
 struct RingTask {
-  int kind, q, u, e, cnt, slot0, col, ngroups;
+  int kind, q, u, e, cnt, slot0, col, ngroups, nsub;
 };
 
 template <int P>
 __device__ __forceinline__ RingTask ring_task(const RingShared &sh, const RingPlan &pl, int task) {
   task = __builtin_amdgcn_readfirstlane(task);
-  RingTask t{4, 0, 0, 0, 0, 0, 0, 1};
+  RingTask t{4, 0, 0, 0, 0, 0, 0, 1, 1};
   if (task < 0 || task >= pl.n1 + pl.n2) return t;
+  t.nsub = pl.sub;
   if (task < pl.n1) {
     t.kind = 1;
     t.q = task;
@@ -1458,8 +1466,15 @@ __device__ __forceinline__ RingTask ring_task(const RingShared &sh, const RingPl
   } else {
     t.kind = 2;
     t.q = task - pl.n1;
-    t.u = t.q / pl.p2u;
-    t.col = (t.q % pl.p2u) * pl.rows;
+    if (t.q < pl.tail_q) {
+      t.u = t.q / pl.p2u;
+      t.col = (t.q % pl.p2u) * pl.rows;
+    } else {  // the last units' down rows in single 16-row sub-groups
+      const int qq = t.q - pl.tail_q, per = pl.p2u * pl.sub;
+      t.u = pl.tail_u0 + qq / per;
+      t.col = (qq % per) * (pl.rows / pl.sub);
+      t.nsub = 1;
+    }
   }
   t.e = __builtin_amdgcn_readfirstlane(sh.active[t.u]);
   t.cnt = __builtin_amdgcn_readfirstlane(sh.counts[t.e]);
@@ -1523,8 +1538,8 @@ __device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const 
 #pragma unroll
   for (int p = 0; p < P; ++p) r.xoff[p] = kRingOff;
   if (t.kind != 1 && t.kind != 2) return r;
-  const int u = g % SUB;
-  const int m0 = (g / SUB) * kRingTokens * P;
+  const int u = g % t.nsub;
+  const int m0 = (g / t.nsub) * kRingTokens * P;
   // every wave writes partials for every pass of the group (zeros from a
   // slice past the end of the rows), so the control wave sums all eight
   r.npass = min(P, (t.cnt - m0 + kRingTokens - 1) / kRingTokens);
@@ -1565,7 +1580,7 @@ __device__ __forceinline__ RingWork<RG, P> ring_work(const ExpertArgs &a, const 
       if (m < t.cnt) r.xoff[p] = ((uint32_t)(t.slot0 + m) * a.I + kl) * 4u;
     }
   }
-  if (SUB > 1 && u != 0) {
+  if (u != 0) {
     r.xr = rr.none;
 #pragma unroll
     for (int p = 0; p < P; ++p) r.xoff[p] = kRingOff;
@@ -1746,7 +1761,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63, li = lane & 15, lg = lane >> 4;
   const RingRsrc rr = ring_rsrc(a);
-  const RingTask none{4, 0, 0, 0, 0, 0, 0, 1};
+  const RingTask none{4, 0, 0, 0, 0, 0, 0, 1, 1};
   f32x4 wt[D][RG];
   f32x4 xv[D][P];
   f32x4 xt[SUB > 1 ? kRingSteps : 1][P];  // token slice of the task's current group
@@ -1786,7 +1801,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
     const bool claim_now = w == 0 && g == 0;
     if (claim_now) claimed = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(1, cr, claim_off, 0, 0);
     int jn = j, gn = g + 1;
-    const bool fresh = SUB == 1 || g % SUB == 0;  // this item loads the token rows
+    const bool fresh = g % t.nsub == 0;  // this item loads the token rows
     RingTask tn = t;
     RingWork<RG, P> nxt;
     f32x4 acc[RG][P][NA];
@@ -1826,7 +1841,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
       }
       if (s == kRingSteps - D - 1) {
         // the next group's rows are about to be issued
-        if (gn >= t.ngroups * SUB) {
+        if (gn >= t.ngroups * t.nsub) {
           jn = j + 1;
           gn = 0;
           if (ok) ok = ring_wait(&sh.nseq, [&](int v) { return v >= j + 2; }, &sh.abort, err, ticks);
@@ -1879,8 +1894,8 @@ __device__ __forceinline__ void ring_flush(const ExpertArgs &a, const RingTask &
                                            const float *res, int b, const AgentOut &inter_out,
                                            const AgentOut &sout_out) {
   const int lane = threadIdx.x & 63;
-  const int u = g % SUB;  // row sub-group of the item
-  const int m0 = (g / SUB) * kRingTokens * P;
+  const int u = g % t.nsub;  // row sub-group of the item
+  const int m0 = (g / t.nsub) * kRingTokens * P;
   const int nt = min(kRingTokens * P, t.cnt - m0);
   // gate/up: lane -> (token, 4 columns): 2 lanes per token and row group;
   // down: 4 lanes
@@ -1941,7 +1956,7 @@ __device__ void ring_control(const ExpertArgs &a, RingShared &sh, const float *r
       lds_store(&sh.done[b], 0);
       ++it;
       ++flushed_now;
-      if (++g >= t.ngroups * SUB) {
+      if (++g >= t.ngroups * t.nsub) {
         g = 0;
         ++j;
         t = ring_seq_task<P>(sh, pl, j);  // published before task j - 1's partials
@@ -2014,6 +2029,17 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   pl.grid = gridDim.x;
   pl.rows = __builtin_amdgcn_readfirstlane(c->stream_rows);
   const int maxcnt = __builtin_amdgcn_readfirstlane(c->max_count);
+  // 64-row tasks of experts holding at most 16 tokens are streamed as four
+  // 16-row sub-groups; the router then plans the last units' down rows as
+  // 16-row tasks (tail_units), so the last round of tasks is short
+  const bool seq = pl.rows == kStreamRows * kRingWideGroups && maxcnt <= kRingTokens;
+  pl.sub = seq ? kRingWideGroups : 1;
+  {
+    const int units = pl.n1 / max(pl.p1u, 1);
+    const int tail = seq ? __builtin_amdgcn_readfirstlane(c->tail_units) : 0;
+    pl.tail_u0 = units - tail;
+    pl.tail_q = (units - tail) * pl.p2u;
+  }
   // plans for this kernel take their slots from the router, and a task
   // covers 16, 32 or 64 rows
   if (c->n_rblocks != 0 ||
