@@ -32,14 +32,14 @@ def dense_weights():
 @pytest.fixture(scope="module")
 def mlp(dense_weights):
     from final_amd import DenseMLP
-    m = DenseMLP(H, I, max_tokens=1024)
+    m = DenseMLP(H, I, max_tokens=2048)
     m.set_weights(*dense_weights)
     yield m
     m.close()
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T", [1, 8, 31, 32, 48, 64, 100, 150, 192, 256, 1000])
+@pytest.mark.parametrize("T", [1, 8, 31, 32, 48, 64, 100, 150, 192, 256, 1000, 2048])
 def test_dense_matches_oracle(T, mlp, dense_weights, oracle_mod):
     from final_amd import workloads as W
     say(f"[dense] T={T} plan={mlp.plan(T)}")
