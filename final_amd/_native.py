@@ -67,11 +67,11 @@ def lib() -> ctypes.CDLL:
     L.moe_route.argtypes = [_vp, _vp, _i, _vp]
     L.moe_experts.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
     L.moe_route_logits.argtypes = [_vp, _vp, _i, _vp]
-    L.moe_last_routing.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp]
+    L.moe_last_routing.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _vp]
     L.moe_device_status.argtypes = [_vp, _vp]
     L.moe_set_norm_weight.argtypes = [_vp, _vp, _i, _vp]
     L.moe_forward_norm.argtypes = [_vp, _vp, _vp, _i, _vp]
-    L.moe_last_normed.argtypes = [_vp, _vp, _vp]
+    L.moe_last_normed.argtypes = [_vp, _vp, _i, _vp]
     L.moe_dense_create.argtypes = [_i, _i, _i, ctypes.POINTER(_vp)]
     L.moe_dense_set_weights.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
     L.moe_dense_forward.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]

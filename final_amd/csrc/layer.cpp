@@ -250,7 +250,7 @@ void SparseMoeBlock::forward(const Tensor &x, Tensor &y, Tensor &router_logits) 
   check(moe_forward(ctx_, dx.f(), dy.f(), nullptr, (int)T, nullptr), "moe_forward");
   check_hip(hipMemcpy(y.data(), dy.p, T * H * sizeof(float), hipMemcpyDeviceToHost),
             "hipMemcpy");
-  check(moe_last_routing(ctx_, nullptr, nullptr, nullptr, router_logits.data(), nullptr),
+  check(moe_last_routing(ctx_, nullptr, nullptr, nullptr, router_logits.data(), (int)T, nullptr),
         "moe_last_routing");
   check(moe_device_status(ctx_, nullptr), "device status");
 }
@@ -271,6 +271,6 @@ void SparseMoeBlock::route_tokens(const Tensor &router_logits,
             "hipMemcpy");
   check(moe_route_logits(ctx_, dl.f(), (int)T, nullptr), "moe_route_logits");
   check(moe_last_routing(ctx_, top_k_indices.data(), top_k_weights.data(), nullptr,
-                         nullptr, nullptr),
+                         nullptr, (int)T, nullptr),
         "moe_last_routing");
 }

@@ -558,9 +558,10 @@ int moe_forward_norm(moe_ctx *ctx, const float *h, float *out, int num_tokens,
   return moe_experts(ctx, ctx->xn, out, h, num_tokens, stream);
 }
 
-int moe_last_normed(moe_ctx *ctx, float *xn, moe_stream_t stream) {
+int moe_last_normed(moe_ctx *ctx, float *xn, int num_tokens, moe_stream_t stream) {
   if (!ctx || !xn) return MOE_ERR_INVALID_ARG;
   if (ctx->normed_T < 0 || !ctx->xn) return MOE_ERR_NOT_READY;
+  if (num_tokens != ctx->normed_T) return MOE_ERR_INVALID_ARG;  // xn holds another count
   DeviceGuard g(ctx->device);
   if (!g.ok) return MOE_ERR_HIP;
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -572,9 +573,10 @@ int moe_last_normed(moe_ctx *ctx, float *xn, moe_stream_t stream) {
 }
 
 int moe_last_routing(moe_ctx *ctx, int *idx, float *w, int *counts, float *logits,
-                     moe_stream_t stream) {
+                     int num_tokens, moe_stream_t stream) {
   if (!ctx) return MOE_ERR_INVALID_ARG;
   if (ctx->routed_T < 0) return MOE_ERR_NOT_READY;
+  if (num_tokens != ctx->routed_T) return MOE_ERR_INVALID_ARG;  // buffers sized for another T
   DeviceGuard g(ctx->device);
   if (!g.ok) return MOE_ERR_HIP;
   hipStream_t st = static_cast<hipStream_t>(stream);

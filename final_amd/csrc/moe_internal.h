@@ -92,7 +92,7 @@ struct RouterArgs {
   int bn;                // MFMA n-tile width (columns of the B tile)
   int tail_units;        // MFMA plans: last units whose down tiles run at half width
   int max_units;
-  const float *norm_w;   // post-attention RMSNorm weight [H]: x is h, normalise it (T <= 64 only)
+  const float *norm_w;   // post-attention RMSNorm weight [H]: x is h, normalise it (decode router only)
   float *xn;             // [T][H]: the normalised rows, for the expert kernel
 };
 

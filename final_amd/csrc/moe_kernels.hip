@@ -752,9 +752,16 @@ void router_decode_kernel(RouterArgs a) {
     const float p = ref_sigmoid(l);
     s_prob[tl][e] = p;
     s_score[tl][e] = p + (a.w.bias ? a.w.bias[e] : 0.0f);  // layer.cu:462
+    if (e < kTopK) {  // rank slots no expert fills keep the reference's -1 / 0
+      s_ti[tl][e] = -1;
+      s_tp[tl][e] = 0.0f;
+    }
   }
   __syncthreads();
-  // 5. rank of e in the token's order (score descending, lower index first)
+  // 5. rank of e in the token's order (score descending, lower index first).
+  // The insertion only takes a score above its -1e30 sentinel (layer.cu:452,
+  // 465), so NaN and scores <= -1e30 are never selected and never outrank
+  // another expert.
   int sel = -1;
   {
     const float sc = s_score[tl][e];
@@ -762,9 +769,9 @@ void router_decode_kernel(RouterArgs a) {
 #pragma unroll
     for (int j = 0; j < kExperts; ++j) {
       const float sj = s_score[tl][j];
-      r += (sj > sc) || (sj == sc && j < e);
+      r += sj > -1e30f && ((sj > sc) || (sj == sc && j < e));
     }
-    if (tvalid && r < kTopK) sel = r;
+    if (tvalid && sc > -1e30f && r < kTopK) sel = r;
     s_sel[tl][e] = sel;
     if (sel >= 0) {
       s_ti[tl][sel] = e;
@@ -872,6 +879,28 @@ __device__ void assign_task(const ExpertArgs &a, int q, int rt) {
       }
     } else {
       st_agent(&a.s.pos[(size_t)tok * kTopK + k], -1);
+    }
+    // A token none of whose scores is selectable (all NaN or <= -1e30) has no
+    // expert output, so no down tile completes it: its row is written here,
+    // y = residual + 0.0f (the empty sum of layer.cu:708-720, then :1866).
+    bool none = true;
+#pragma unroll
+    for (int kk = 0; kk < kTopK; ++kk) {
+      const int ek = a.s.idx[(size_t)tok * kTopK + kk];
+      none = none && (ek < 0 || ek >= kExperts);
+    }
+    if (none) {
+      const int H4 = a.H >> 2;
+      const float4 *r4 = reinterpret_cast<const float4 *>(a.residual);
+      float4 *y4 = reinterpret_cast<float4 *>(a.y);
+      for (int c4 = k; c4 < H4; c4 += kTopK) {
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (r4) {
+          const float4 rv = r4[(size_t)tok * H4 + c4];
+          v = make_float4(rv.x + 0.0f, rv.y + 0.0f, rv.z + 0.0f, rv.w + 0.0f);
+        }
+        y4[(size_t)tok * H4 + c4] = v;
+      }
     }
   }
 }
@@ -1339,10 +1368,11 @@ void expert_mfma_kernel(ExpertArgs a) {
 // landed, with no store-completion wait, counter or poll in between.
 //
 // Row tasks follow the plan's order: gate/up row blocks expert by expert,
-// then down row blocks.  Block b starts with task b; every later task comes
-// from a queue counter (G + the counter's old value, G = grid), claimed by
-// streaming wave 0 at the first step of the block's current task, so a
-// block that draws cheap tasks takes more of them.  The ring issues a down
+// then down row blocks.  Every task comes from a queue counter: a block's
+// first one is claimed as it starts, each later one by streaming wave 0 at
+// the first step of the block's current task, so a block that draws cheap
+// tasks takes more of them, and a block that is not resident (another
+// kernel holds its CU) owns no task that a running block waits for.  The ring issues a down
 // task's loads while the task before it still runs; a down task waits, at
 // the step that consumes them, for intermediate values still unwritten.
 // Only down tasks wait and gate/up tasks never do, and a block claims a down
@@ -1657,7 +1687,9 @@ __device__ __forceinline__ bool ring_await(const RingWork<RG, P> &r, int s, f32x
   return true;
 }
 
-// A token's routing: slots of its four expert rows and their weights.
+// A token's routing: slots of its four expert rows (-1: no expert in that
+// rank, which a token whose scores are NaN or <= -1e30 leaves empty) and
+// their weights.
 struct RingRoute {
   int slot[kTopK];
   float w[kTopK];
@@ -1670,7 +1702,7 @@ __device__ __forceinline__ RingRoute ring_route(const ExpertArgs &a, int tok) {
     int slot = a.s.pos[(size_t)tok * kTopK + k];
     float w = a.s.wts[(size_t)tok * kTopK + k];
     if (slot < 0 || slot >= a.T * kTopK) {
-      slot = 0;
+      slot = -1;
       w = 0.0f;
     }
     r.slot[k] = slot;
@@ -1698,7 +1730,8 @@ __device__ bool ring_combine(const ExpertArgs &a, int tok, const RingRoute &r, i
     uint32_t off[kTopK];
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) {
-      off[k] = ((uint32_t)r.slot[k] * (uint32_t)H4 + (uint32_t)c4) * 16u;
+      // an empty rank reads past the buffer: zeros, never kUnwritten
+      off[k] = r.slot[k] >= 0 ? ((uint32_t)r.slot[k] * (uint32_t)H4 + (uint32_t)c4) * 16u : kRingOff;
       v[k] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(so, off[k], 0, kCachePolicySc1));
     }
     const float4 rv = r4 ? r4[(size_t)tok * H4 + c4] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1722,6 +1755,7 @@ __device__ bool ring_combine(const ExpertArgs &a, int tok, const RingRoute &r, i
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) {
+      if (r.slot[k] < 0) continue;  // layer.cu:708-720 sums the selected experts only
       acc.x = __builtin_fmaf(v[k].x, r.w[k], acc.x);
       acc.y = __builtin_fmaf(v[k].y, r.w[k], acc.y);
       acc.z = __builtin_fmaf(v[k].z, r.w[k], acc.z);
@@ -1835,7 +1869,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
         }
       }
       if (s == D && claim_now) {
-        if (lane == 0) lds_store(&sh.seq[(j + 1) & 7], pl.grid + claimed);
+        if (lane == 0) lds_store(&sh.seq[(j + 1) & 7], claimed);
         release_lds();
         if (lane == 0) lds_store(&sh.nseq, j + 2);
       }
@@ -2017,7 +2051,10 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   if (tid == 0) {
     sh.flushed = 0;
     sh.abort = 0;
-    sh.seq[0] = blockIdx.x;  // past the row tasks when the grid is larger
+    // every task, the first included, is claimed from the queue, so only a
+    // block that is running owns one (blocks not yet resident own nothing
+    // another block waits for)
+    sh.seq[0] = claim(&a.s.ctrl->head);
     sh.nseq = 1;
   }
   RingPlan pl;

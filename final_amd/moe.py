@@ -44,7 +44,8 @@ class SparseMoeBlock:
         _native.check(L.moe_create(ctypes.byref(self.dims), ctypes.byref(self._ctx)), "moe_create")
         self.hidden, self.inter, self.num_experts = hidden, inter, num_experts
         self.max_tokens = max_tokens
-        self._last_T = -1
+        self._routed_T = -1   # T of the last successful route (C side: routed_T)
+        self._normed_T = -1   # T of the last successful forward_norm (C side: normed_T)
 
     # -- weights ------------------------------------------------------------
     def set_weights(self, gate, bias, w1, w3, w2, stream=None) -> None:
@@ -84,9 +85,11 @@ class SparseMoeBlock:
     # -- forward ------------------------------------------------------------
     def forward_norm_gpu(self, h, out, num_tokens: int, stream=None) -> None:
         """out = h + MoE(rmsnorm(h)) on device buffers; out may be h."""
+        # The read-backs pass these counts to the C side, which rejects a count
+        # other than the one it holds, so a stale value can only fail a call.
         _native.check(_native.lib().moe_forward_norm(self._ctx, _ptr(h), _ptr(out), int(num_tokens),
                                                      _stream(stream)), "moe_forward_norm")
-        self._last_T = int(num_tokens)
+        self._routed_T = self._normed_T = int(num_tokens)
 
     def forward_norm(self, h: np.ndarray) -> np.ndarray:
         """Host convenience for forward_norm_gpu."""
@@ -101,26 +104,25 @@ class SparseMoeBlock:
 
     def last_normed(self, stream=None) -> np.ndarray:
         """Normalised rows of the last forward_norm ([T][H])."""
-        T = max(self._last_T, 0)
+        T = max(self._normed_T, 0)
         out = np.empty((T, self.hidden), np.float32)
-        _native.check(_native.lib().moe_last_normed(self._ctx, out.ctypes.data, _stream(stream)),
+        _native.check(_native.lib().moe_last_normed(self._ctx, out.ctypes.data, T, _stream(stream)),
                       "moe_last_normed")
         return out
 
     def forward_gpu(self, x, y, num_tokens: int, residual=None, stream=None) -> None:
-        _native.check(_native.lib().moe_forward(self._ctx, _ptr(x), _ptr(y), _ptr(residual),
-                                                int(num_tokens), _stream(stream)), "moe_forward")
-        self._last_T = int(num_tokens)
+        self.route(x, num_tokens, stream)
+        self.experts(x, y, num_tokens, residual=residual, stream=stream)
 
     def route(self, x, num_tokens: int, stream=None) -> None:
         _native.check(_native.lib().moe_route(self._ctx, _ptr(x), int(num_tokens), _stream(stream)),
                       "moe_route")
-        self._last_T = int(num_tokens)
+        self._routed_T = int(num_tokens)
 
     def route_logits(self, logits, num_tokens: int, stream=None) -> None:
         _native.check(_native.lib().moe_route_logits(self._ctx, _ptr(logits), int(num_tokens),
                                                      _stream(stream)), "moe_route_logits")
-        self._last_T = int(num_tokens)
+        self._routed_T = int(num_tokens)
 
     def experts(self, x, y, num_tokens: int, residual=None, stream=None) -> None:
         _native.check(_native.lib().moe_experts(self._ctx, _ptr(x), _ptr(y), _ptr(residual),
@@ -140,14 +142,14 @@ class SparseMoeBlock:
 
     # -- inspection ---------------------------------------------------------
     def last_routing(self, stream=None) -> dict:
-        T = max(self._last_T, 0)
+        T = max(self._routed_T, 0)
         idx = np.empty((T, TOPK), np.int32)
         w = np.empty((T, TOPK), np.float32)
         counts = np.empty((self.num_experts,), np.int32)
         logits = np.empty((T, self.num_experts), np.float32)
         _native.check(_native.lib().moe_last_routing(
             self._ctx, idx.ctypes.data, w.ctypes.data, counts.ctypes.data, logits.ctypes.data,
-            _stream(stream)), "moe_last_routing")
+            T, _stream(stream)), "moe_last_routing")
         return {"idx": idx, "w": w, "counts": counts, "logits": logits}
 
     def check_device(self, stream=None) -> None:

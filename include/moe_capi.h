@@ -140,7 +140,7 @@ int moe_set_norm_weight(moe_ctx *ctx, const float *weight, int src_on_device,
  * (layer.cu:144-193, eps 1e-5) and the MoE block of moe_forward.  h, out:
  * device [num_tokens][hidden] fp32, 16-byte aligned; out may alias h (the
  * reference writes the layer output in place, layer.cu:1917).  Needs
- * moe_set_weights and moe_set_norm_weight.  For up to 64 tokens the router
+ * moe_set_weights and moe_set_norm_weight.  For up to 256 tokens the router
  * normalises the rows it already stages (no extra launch); larger batches
  * run one normalisation kernel first.  Asynchronous on `stream`. */
 int moe_forward_norm(moe_ctx *ctx, const float *h, float *out, int num_tokens,
@@ -148,15 +148,19 @@ int moe_forward_norm(moe_ctx *ctx, const float *h, float *out, int num_tokens,
 
 /* Copies the normalised rows of the last moe_forward_norm ([T][hidden]) to
  * host memory (parity tests: the reference's normed_hidden_gpu_,
- * layer.cu:1904-1905).  Synchronises `stream`. */
-int moe_last_normed(moe_ctx *ctx, float *xn, moe_stream_t stream);
+ * layer.cu:1904-1905).  num_tokens is the row count xn holds and must equal
+ * that call's T (else MOE_ERR_INVALID_ARG, nothing copied).  Synchronises
+ * `stream`. */
+int moe_last_normed(moe_ctx *ctx, float *xn, int num_tokens, moe_stream_t stream);
 
 /* Copies the routing of the last moe_route/moe_forward to host memory:
  * idx [T][4] (rank order, -1 = none), w [T][4], counts [E], logits [T][E]
- * (any may be NULL).  Synchronises `stream`.  The topk_indices_gpu_,
- * topk_weights_gpu_ and expert_counts_gpu_ of the reference (layer.h:99-107). */
+ * (any may be NULL).  num_tokens is the T the buffers are sized for and must
+ * equal the routed T (else MOE_ERR_INVALID_ARG, nothing copied).
+ * Synchronises `stream`.  The topk_indices_gpu_, topk_weights_gpu_ and
+ * expert_counts_gpu_ of the reference (layer.h:99-107). */
 int moe_last_routing(moe_ctx *ctx, int *idx, float *w, int *counts,
-                     float *logits, moe_stream_t stream);
+                     float *logits, int num_tokens, moe_stream_t stream);
 
 /* Reads and clears the device status word: MOE_ERR_DEVICE_TIMEOUT if a
  * kernel's bounded dependency wait expired since the last call,

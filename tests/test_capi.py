@@ -87,7 +87,7 @@ def test_argument_validation_before_any_gpu_call(L):
     assert L.moe_route(None, None, 4, None) == _native.MOE_ERR_INVALID_ARG
     assert L.moe_experts(None, None, None, None, 4, None) == _native.MOE_ERR_INVALID_ARG
     assert L.moe_route_logits(None, None, 4, None) == _native.MOE_ERR_INVALID_ARG
-    assert L.moe_last_routing(None, None, None, None, None, None) == _native.MOE_ERR_INVALID_ARG
+    assert L.moe_last_routing(None, None, None, None, None, 0, None) == _native.MOE_ERR_INVALID_ARG
     assert L.moe_device_status(None, None) == _native.MOE_ERR_INVALID_ARG
     assert L.moe_set_weights(None, None, None, None, None, None, 0, None) == _native.MOE_ERR_INVALID_ARG
     assert L.moe_plan_tile_rows(None, 64) == -1

@@ -285,3 +285,35 @@ def test_route_serves_one_experts_launch(T, block, real_weights, oracle_mod):
     hip.synchronize()
     block.check_device()
     np.testing.assert_allclose(dy2.download(), ref["y"], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+def test_readback_checks_token_count(block, real_weights):
+    """moe_last_normed / moe_last_routing copy the rows of the call that
+    produced them and take the caller's row count: a count other than the
+    stored one is rejected (nothing is copied), so a buffer sized for another
+    batch can never be overrun.  Sequences: forward_norm(300) then forward(8)
+    then the normalised rows; a route that succeeded followed by an experts
+    call that failed (x aliasing y) then the routing."""
+    from final_amd import _native, hip
+    from final_amd import workloads as W
+    L = _native.lib()
+    block.set_norm_weight(_norm_weight(W.H))
+    h = W.gen_x(300, seed=91)
+    block.forward_norm(h)
+    x8 = W.gen_x(8, seed=92)
+    block.forward(x8)
+    assert block.last_normed().shape == (300, W.H)
+    small = np.empty((8, W.H), np.float32)
+    assert L.moe_last_normed(block._ctx, small.ctypes.data, 8, None) == _native.MOE_ERR_INVALID_ARG
+    assert block.last_routing()["idx"].shape == (8, 4)
+    idx = np.empty((300, 4), np.int32)
+    assert L.moe_last_routing(block._ctx, idx.ctypes.data, None, None, None, 300,
+                              None) == _native.MOE_ERR_INVALID_ARG
+    dx = hip.DeviceArray.from_numpy(W.gen_x(40, seed=93))
+    with pytest.raises(_native.MoeError):
+        block.forward_gpu(dx, dx, 40)  # route succeeds, experts rejects x == y
+    hip.synchronize()
+    assert block.last_routing()["idx"].shape == (40, 4)
+    assert L.moe_last_routing(block._ctx, idx.ctypes.data, None, None, None, 8,
+                              None) == _native.MOE_ERR_INVALID_ARG
