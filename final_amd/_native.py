@@ -26,6 +26,7 @@ CAPI_SYMBOLS = (
     "moe_plan_tile_rows", "moe_force_tile_rows", "moe_set_wait_divisor",
     "moe_strerror", "moe_version", "moe_set_norm_weight", "moe_forward_norm",
     "moe_last_normed", "moe_dense_create", "moe_dense_set_weights", "moe_dense_forward",
+    "moe_forward_noalloc",
 )
 SYNTH_SYMBOLS = (
     "moe_synth_normal", "moe_synth_stream_gate", "moe_synth_stream_bias",
@@ -64,6 +65,7 @@ def lib() -> ctypes.CDLL:
     L.moe_destroy.argtypes = [_vp]
     L.moe_set_weights.argtypes = [_vp, _vp, _vp, _vp, _vp, _vp, _i, _vp]
     L.moe_forward.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
+    L.moe_forward_noalloc.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
     L.moe_route.argtypes = [_vp, _vp, _i, _vp]
     L.moe_experts.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
     L.moe_route_logits.argtypes = [_vp, _vp, _i, _vp]

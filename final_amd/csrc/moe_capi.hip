@@ -9,6 +9,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <new>
 #include <vector>
 
@@ -42,6 +43,90 @@ struct DeviceGuard {
 bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
+
+// ---------------------------------------------------------------------------
+// Scratch of moe_forward_noalloc: one file-scope device array per GPU, for
+// callers that cannot allocate (code under HIP graph capture, serving loops).
+// Layout: a fixed header whose counters must start at zero (Ctrl + dep, then
+// the router's per-token-block counters), cleared once per device at set-up
+// and returned to zero by every forward that completes (the router resets the
+// counters it and the expert kernel use; it never waits, so it always ends);
+// then the data regions of one call, laid out for that call's token count.
+// In host code `scratch` names a host-side stand-in: kernels and copies use
+// the device address hipGetSymbolAddress returned for the current device.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kNoAllocBytes = (size_t)8 << 20;  // 8 MiB per GPU
+constexpr int kNoAllocMaxTokens = 128;
+constexpr size_t kNoAllocHeader = 8192;   // Ctrl + dep[], then tb_done[]
+constexpr size_t kNoAllocTbDone = 4096;   // offset of tb_done in the header
+constexpr int kNoAllocMaxUnits = kNoAllocMaxTokens * kTopK / 32 + kExperts + 1;
+constexpr int kMaxDevices = 64;
+static_assert(sizeof(Ctrl) + sizeof(int) * kNoAllocMaxUnits <= kNoAllocTbDone, "ctrl + dep fit");
+static_assert(kNoAllocTbDone + sizeof(int) * (kNoAllocMaxTokens / kMinRouterTokens) <=
+                  kNoAllocHeader, "tb_done fits");
+
+std::mutex g_noalloc_mu;
+char *g_noalloc_ptr[kMaxDevices] = {};  // device address of `scratch` per device
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocBytes];
+
+// Once per device, with that device current (from moe_create): the device
+// address of `scratch` and a cleared header.  MOE_OK or MOE_ERR_HIP.
+static int noalloc_setup(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return MOE_OK;  // moe_forward_noalloc then reports not ready
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (g_noalloc_ptr[dev]) return MOE_OK;
+  void *p = nullptr;
+  if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+    (void)hipGetLastError();
+    return MOE_ERR_HIP;
+  }
+  if (hipMemset(p, 0, kNoAllocHeader) != hipSuccess || hipDeviceSynchronize() != hipSuccess)
+    return MOE_ERR_HIP;
+  g_noalloc_ptr[dev] = static_cast<char *>(p);
+  return MOE_OK;
+}
+
+static char *noalloc_ptr(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return nullptr;
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  return g_noalloc_ptr[dev];
+}
+
+// The call's Scratch inside the device array at `base`, for T tokens of a
+// context with hidden H and intermediate I.  False if it does not fit.
+static bool noalloc_layout(char *base, int T, int H, int I, Scratch *s, int *max_units) {
+  const size_t S = (size_t)T * kTopK, E = kExperts;
+  const size_t nb = (T + kMinRouterTokens - 1) / kMinRouterTokens;
+  size_t off = kNoAllocHeader;
+  auto take = [&](size_t bytes) {
+    const size_t o = off;
+    off = align256(off + bytes);
+    return base + o;
+  };
+  s->ctrl = reinterpret_cast<Ctrl *>(base);
+  s->dep = reinterpret_cast<int *>(base + sizeof(Ctrl));
+  s->tb_done = reinterpret_cast<int *>(base + kNoAllocTbDone);
+  s->logits = reinterpret_cast<float *>(take(T * E * sizeof(float)));
+  s->idx = reinterpret_cast<int *>(take(S * sizeof(int)));
+  s->wts = reinterpret_cast<float *>(take(S * sizeof(float)));
+  s->pos = reinterpret_cast<int *>(take(S * sizeof(int)));
+  s->blk = reinterpret_cast<int *>(take(nb * E * sizeof(int)));
+  s->slot_token = reinterpret_cast<int *>(take(S * sizeof(int)));
+  s->ccount = reinterpret_cast<int *>(take((size_t)T * (H / kCombineCols) * sizeof(int)));
+  s->inter = reinterpret_cast<float *>(take(S * I * sizeof(float)));
+  s->sout = reinterpret_cast<float *>(take(S * H * sizeof(float)));
+  s->inter_bytes = (uint32_t)(S * I * sizeof(float));
+  s->sout_bytes = (uint32_t)(S * H * sizeof(float));
+  *max_units = (int)(S / 32 + E + 1);
+  return off <= kNoAllocBytes;
+}
 
 struct moe_ctx {
   moe_dims d{};
@@ -219,6 +304,11 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
   for (int p = 0; p < 4; ++p) {
     static const int rows[4] = {0, 32, 64, 128};
     ctx->grid[p] = ctx->cus * expert_blocks_per_cu(rows[p]);
+  }
+  if ((rc = noalloc_setup(ctx->device))) {
+    free_all(ctx);
+    delete ctx;
+    return rc;
   }
   *out = ctx;
   return MOE_OK;
@@ -432,6 +522,58 @@ int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
   return moe_experts(ctx, x, y, residual, num_tokens, stream);
 }
 
+int moe_forward_noalloc(moe_ctx *ctx, const float *x, float *y, const float *residual,
+                        int num_tokens, moe_stream_t stream) {
+  if (!ctx || ctx->dense) return MOE_ERR_INVALID_ARG;
+  const int T = num_tokens;
+  if (T < 0) return MOE_ERR_INVALID_ARG;
+  if (T > kNoAllocMaxTokens) return MOE_ERR_TOO_MANY_TOKENS;
+  if (!ctx->weights_set) return MOE_ERR_NOT_READY;
+  if (T == 0) return MOE_OK;
+  if (!x || !y || !aligned16(x) || !aligned16(y) || (residual && !aligned16(residual)) || x == y)
+    return MOE_ERR_INVALID_ARG;
+  char *base = noalloc_ptr(ctx->device);
+  if (!base) return MOE_ERR_NOT_READY;
+  Scratch s{};
+  int max_units = 0;
+  if (!noalloc_layout(base, T, ctx->d.hidden, ctx->d.inter, &s, &max_units))
+    return MOE_ERR_TOO_MANY_TOKENS;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // same plan, kernels and arithmetic as moe_forward, on the device array
+  RouterArgs ra{};
+  ra.x = x;
+  ra.w.gate = ctx->gate;
+  ra.w.bias = ctx->has_bias ? ctx->bias : nullptr;
+  ra.w.w13 = ctx->w13;
+  ra.w.w2 = ctx->w2;
+  ra.s = s;
+  ra.T = T;
+  ra.H = ctx->d.hidden;
+  ra.inter = ctx->d.inter;
+  ra.tile_rows = ctx_plan(ctx, T);
+  ra.bn = expert_bn(ra.tile_rows, T);
+  ra.tail_units = tail_units(ctx, ra.tile_rows, ra.bn);
+  ra.max_units = max_units;
+  const int pi = plan_index(ra.tile_rows);
+  if (pi < 0) return MOE_ERR_INVALID_ARG;
+  if (launch_router(ra, false, st) != hipSuccess) return MOE_ERR_HIP;
+  ExpertArgs ea{};
+  ea.x = x;
+  ea.y = y;
+  ea.residual = residual;
+  ea.w = ra.w;
+  ea.s = s;
+  ea.T = T;
+  ea.H = ctx->d.hidden;
+  ea.I = ctx->d.inter;
+  ea.wait_limit = kDefaultWaitLimit / (ctx->wait_div > 0 ? ctx->wait_div : 1);
+  if (ea.wait_limit < 1) ea.wait_limit = 1;
+  if (launch_experts(ea, ra.tile_rows, ctx->grid[pi], st) != hipSuccess) return MOE_ERR_HIP;
+  return MOE_OK;
+}
+
 int moe_dense_set_weights(moe_ctx *ctx, const float *w1, const float *w3, const float *w2,
                           int src_on_device, moe_stream_t stream) {
   if (!ctx || !ctx->dense || !w1 || !w3 || !w2) return MOE_ERR_INVALID_ARG;
@@ -601,24 +743,33 @@ int moe_last_routing(moe_ctx *ctx, int *idx, float *w, int *counts, float *logit
   return MOE_OK;
 }
 
+// Reads and clears one status word (device int) on `st`; 0 when clear.
+static int take_status(int *word, hipStream_t st, int *err) {
+  *err = 0;
+  if (hipMemcpyAsync(err, word, sizeof(int), hipMemcpyDeviceToHost, st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return MOE_ERR_HIP;
+  if (*err) {
+    const int zero = 0;
+    if (hipMemcpyAsync(word, &zero, sizeof(int), hipMemcpyHostToDevice, st) != hipSuccess ||
+        hipStreamSynchronize(st) != hipSuccess)
+      return MOE_ERR_HIP;
+  }
+  return MOE_OK;
+}
+
 int moe_device_status(moe_ctx *ctx, moe_stream_t stream) {
   if (!ctx) return MOE_ERR_INVALID_ARG;
   DeviceGuard g(ctx->device);
   if (!g.ok) return MOE_ERR_HIP;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  int err = 0;
-  if (hipMemcpyAsync(&err, &ctx->s.ctrl->err, sizeof(int), hipMemcpyDeviceToHost, st) !=
-          hipSuccess ||
-      hipStreamSynchronize(st) != hipSuccess)
-    return MOE_ERR_HIP;
-  if (err) {
-    const int zero = 0;
-    if (hipMemcpyAsync(&ctx->s.ctrl->err, &zero, sizeof(int), hipMemcpyHostToDevice, st) !=
-            hipSuccess ||
-        hipStreamSynchronize(st) != hipSuccess)
-      return MOE_ERR_HIP;
-    return err == 1 ? MOE_ERR_DEVICE_TIMEOUT : MOE_ERR_INTERNAL;
-  }
+  int err = 0, err_na = 0;
+  if (take_status(&ctx->s.ctrl->err, st, &err)) return MOE_ERR_HIP;
+  // the status word of the device's moe_forward_noalloc scratch
+  if (char *base = noalloc_ptr(ctx->device))
+    if (take_status(&reinterpret_cast<Ctrl *>(base)->err, st, &err_na)) return MOE_ERR_HIP;
+  const int e = err ? err : err_na;
+  if (e) return e == 1 ? MOE_ERR_DEVICE_TIMEOUT : MOE_ERR_INTERNAL;
   return MOE_OK;
 }
 

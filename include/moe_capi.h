@@ -86,6 +86,21 @@ int moe_set_weights(moe_ctx *ctx, const float *gate, const float *bias,
 int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
                 int num_tokens, moe_stream_t stream);
 
+/* moe_forward without allocating: no counterpart in the reference.  For
+ * callers that cannot allocate device memory during a forward (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * kernels, plan and results as moe_forward (bit for bit), but the routing,
+ * intermediate and expert-output scratch is one file-scope device array per
+ * GPU (8 MiB, set up by moe_create on that GPU) instead of the context's.
+ * num_tokens <= 128 (and the rows must fit the array: 128 tokens at hidden
+ * 2048 / inter 1792); larger returns MOE_ERR_TOO_MANY_TOKENS.  Calls no
+ * hipMalloc/hipFree.  Every call on a GPU shares that GPU's array: calls that
+ * overlap on one GPU (two streams, or two contexts) race; calls ordered on
+ * one stream do not.  Its device status is reported by moe_device_status of
+ * any context on that GPU.  moe_last_routing does not see its routing. */
+int moe_forward_noalloc(moe_ctx *ctx, const float *x, float *y, const float *residual,
+                        int num_tokens, moe_stream_t stream);
+
 /* The two halves of moe_forward, for callers that time or inspect them:
  * moe_route = gate GEMM + sigmoid/top-4 + per-expert histogram and scan
  * (layer.cu:1438-1464); moe_experts = dispatch + grouped SwiGLU experts +

@@ -1,0 +1,71 @@
+"""moe_forward_noalloc (the entry point that allocates nothing) against
+moe_forward through the C-ABI.
+
+Same kernels and plan on a per-GPU device array instead of the context's
+scratch, so y must equal moe_forward's bit for bit.  Two calls in a row, the
+second with fewer tokens (the array keeps the first call's contents), and the
+size limit.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from conftest import bits
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.mark.gpu
+def test_noalloc_matches_forward(real_weights):
+    from final_amd import SparseMoeBlock, _native, hip
+    from final_amd import workloads as W
+    L = _native.lib()
+    w = real_weights
+    blk = SparseMoeBlock(max_tokens=256)
+    try:
+        blk.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+        for T in (128, 8, 1):
+            say(f"[noalloc] T={T} plan={blk.plan(T)}")
+            x = W.gen_x(T, seed=300 + T)
+            r = W.gen_x(T, seed=400 + T)
+            dx = hip.DeviceArray.from_numpy(x)
+            dr = hip.DeviceArray.from_numpy(r)
+            dy = hip.DeviceArray((T, W.H))
+            dz = hip.DeviceArray((T, W.H))
+            blk.forward_gpu(dx, dy, T, residual=dr)
+            _native.check(L.moe_forward_noalloc(blk._ctx, dx.ptr, dz.ptr, dr.ptr, T, None),
+                          "moe_forward_noalloc")
+            hip.synchronize()
+            blk.check_device()
+            y, z = dy.download(), dz.download()
+            assert np.isfinite(z).all()
+            assert np.array_equal(bits(z), bits(y)), f"T={T}: noalloc y differs from moe_forward"
+        # a forced MFMA plan on the same array, after the streaming calls
+        blk.force_tile_rows(64)
+        try:
+            T = 100
+            say(f"[noalloc] T={T} plan={blk.plan(T)}")
+            x = W.gen_x(T, seed=500)
+            dx = hip.DeviceArray.from_numpy(x)
+            dy = hip.DeviceArray((T, W.H))
+            dz = hip.DeviceArray((T, W.H))
+            blk.forward_gpu(dx, dy, T)
+            _native.check(L.moe_forward_noalloc(blk._ctx, dx.ptr, dz.ptr, None, T, None),
+                          "moe_forward_noalloc")
+            hip.synchronize()
+            blk.check_device()
+            assert np.array_equal(bits(dz.download()), bits(dy.download()))
+        finally:
+            blk.force_tile_rows(-1)
+        big = hip.DeviceArray((129, W.H))
+        out = hip.DeviceArray((129, W.H))
+        assert L.moe_forward_noalloc(blk._ctx, big.ptr, out.ptr, None, 129,
+                                     None) == _native.MOE_ERR_TOO_MANY_TOKENS
+        assert L.moe_forward_noalloc(blk._ctx, big.ptr, big.ptr, None, 4,
+                                     None) == _native.MOE_ERR_INVALID_ARG
+    finally:
+        blk.close()
