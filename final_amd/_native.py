@@ -26,7 +26,15 @@ CAPI_SYMBOLS = (
     "moe_plan_tile_rows", "moe_force_tile_rows", "moe_set_wait_divisor",
     "moe_strerror", "moe_version", "moe_set_norm_weight", "moe_forward_norm",
     "moe_last_normed", "moe_dense_create", "moe_dense_set_weights", "moe_dense_forward",
-    "moe_forward_noalloc",
+    "moe_forward_noalloc", "moe_create_shared", "moe_dense_create_shared",
+)
+LFM_SYMBOLS = (
+    "lfm_gemm_nt", "lfm_embed", "lfm_rmsnorm", "lfm_qk_norm_rope", "lfm_attention",
+    "lfm_shortconv", "lfm_rope_tables", "lfm_synth_normal", "lfm_fill", "lfm_synth_stream_of",
+    "lfm_synth_is_norm", "lfm_synth_tensor", "lfm_model_create_synthetic",
+    "lfm_model_create_from_file", "lfm_model_destroy", "lfm_model_forward", "lfm_model_embed",
+    "lfm_model_layer_forward", "lfm_model_head", "lfm_model_moe", "lfm_model_info",
+    "lfm_model_status",
 )
 SYNTH_SYMBOLS = (
     "moe_synth_normal", "moe_synth_stream_gate", "moe_synth_stream_bias",
@@ -39,6 +47,13 @@ class MoeDims(ctypes.Structure):
     _fields_ = [("hidden", ctypes.c_int), ("inter", ctypes.c_int),
                 ("num_experts", ctypes.c_int), ("top_k", ctypes.c_int),
                 ("max_tokens", ctypes.c_int)]
+
+
+class LfmModelConfig(ctypes.Structure):
+    _fields_ = [("num_layers", ctypes.c_int), ("layer_types", ctypes.c_void_p),
+                ("num_dense_layers", ctypes.c_int), ("max_batch", ctypes.c_int),
+                ("max_seq", ctypes.c_int), ("seed", ctypes.c_uint64),
+                ("weight_std", ctypes.c_float)]
 
 
 class MoeError(RuntimeError):
@@ -92,6 +107,33 @@ def lib() -> ctypes.CDLL:
         f.argtypes = [_i]
         f.restype = ctypes.c_uint64
     L.moe_synth_set_threads.argtypes = [_i]
+    L.moe_create_shared.argtypes = [ctypes.POINTER(MoeDims), _vp, ctypes.POINTER(_vp)]
+    L.moe_dense_create_shared.argtypes = [_i, _i, _i, _vp, ctypes.POINTER(_vp)]
+    _ll, _sz, _u64, _f = ctypes.c_longlong, ctypes.c_size_t, ctypes.c_uint64, ctypes.c_float
+    L.lfm_gemm_nt.argtypes = [_vp, _vp, _vp, _vp, _i, _i, _i, _vp]
+    L.lfm_embed.argtypes = [_vp, _vp, _vp, _i, _i, _i, _vp, _vp]
+    L.lfm_rmsnorm.argtypes = [_vp, _ll, _vp, _vp, _ll, _i, _i, _vp]
+    L.lfm_qk_norm_rope.argtypes = [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]
+    L.lfm_attention.argtypes = [_vp, _i, _vp, _i, _i, _i, _i, _i, _i, _vp]
+    L.lfm_shortconv.argtypes = [_vp, _vp, _vp, _i, _i, _i, _i, _vp]
+    L.lfm_rope_tables.argtypes = [_vp, _vp, _i, _i, _f]
+    L.lfm_synth_normal.argtypes = [_vp, _sz, _u64, _u64, _f, _u64, _vp]
+    L.lfm_fill.argtypes = [_vp, _sz, _f, _vp]
+    L.lfm_synth_stream_of.argtypes = [ctypes.c_char_p]
+    L.lfm_synth_stream_of.restype = _u64
+    L.lfm_synth_is_norm.argtypes = [ctypes.c_char_p]
+    L.lfm_synth_tensor.argtypes = [_u64, ctypes.c_char_p, _f, _vp, _sz]
+    L.lfm_model_create_synthetic.argtypes = [ctypes.POINTER(LfmModelConfig), ctypes.POINTER(_vp)]
+    L.lfm_model_create_from_file.argtypes = [ctypes.c_char_p, _i, _i, ctypes.POINTER(_vp)]
+    L.lfm_model_destroy.argtypes = [_vp]
+    L.lfm_model_forward.argtypes = [_vp, _vp, _i, _i, _vp, _vp]
+    L.lfm_model_embed.argtypes = [_vp, _vp, _i, _i, _vp, _vp]
+    L.lfm_model_layer_forward.argtypes = [_vp, _i, _vp, _i, _i, _vp]
+    L.lfm_model_head.argtypes = [_vp, _vp, _i, _i, _vp, _vp]
+    L.lfm_model_moe.argtypes = [_vp, _i, ctypes.POINTER(_vp)]
+    L.lfm_model_info.argtypes = [_vp, ctypes.POINTER(_i), ctypes.POINTER(_i), ctypes.POINTER(_i),
+                                 ctypes.POINTER(_i)]
+    L.lfm_model_status.argtypes = [_vp, _vp]
     _lib = L
     return L
 

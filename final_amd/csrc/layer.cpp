@@ -52,12 +52,19 @@ MLP::MLP(const std::string &w1_file, const std::string &w2_file,
 MLP::MLP(Tensor w1, Tensor w2, Tensor w3)
     : w1_(std::move(w1)), w3_(std::move(w3)), w2_(std::move(w2)) {}
 
+MLP::MLP(int layer_idx, int hidden, int inter, const SyntheticWeights &s)
+    : synth_(true), syn_(s), layer_idx_(layer_idx), syn_hidden_(hidden), syn_inter_(inter) {
+  if (hidden <= 0 || inter <= 0) throw std::invalid_argument("MLP: hidden and inter must be > 0");
+}
+
 MLP::~MLP() { release_gpu(); }
 
 MLP::MLP(MLP &&o) noexcept
     : w1_gpu_(o.w1_gpu_), w3_gpu_(o.w3_gpu_), w2_gpu_(o.w2_gpu_),
       temp_buf_gpu_(o.temp_buf_gpu_), w1_(std::move(o.w1_)), w3_(std::move(o.w3_)),
-      w2_(std::move(o.w2_)), dense_ctx_(o.dense_ctx_), max_tokens_(o.max_tokens_) {
+      w2_(std::move(o.w2_)), dense_ctx_(o.dense_ctx_), donor_(o.donor_),
+      max_tokens_(o.max_tokens_), synth_(o.synth_), syn_(o.syn_), layer_idx_(o.layer_idx_),
+      syn_hidden_(o.syn_hidden_), syn_inter_(o.syn_inter_) {
   o.w1_gpu_ = o.w3_gpu_ = o.w2_gpu_ = o.temp_buf_gpu_ = nullptr;
   o.dense_ctx_ = nullptr;
 }
@@ -73,7 +80,13 @@ MLP &MLP::operator=(MLP &&o) noexcept {
     w3_gpu_ = o.w3_gpu_;
     temp_buf_gpu_ = o.temp_buf_gpu_;
     dense_ctx_ = o.dense_ctx_;
+    donor_ = o.donor_;
     max_tokens_ = o.max_tokens_;
+    synth_ = o.synth_;
+    syn_ = o.syn_;
+    layer_idx_ = o.layer_idx_;
+    syn_hidden_ = o.syn_hidden_;
+    syn_inter_ = o.syn_inter_;
     o.w1_gpu_ = o.w3_gpu_ = o.w2_gpu_ = o.temp_buf_gpu_ = nullptr;
     o.dense_ctx_ = nullptr;
   }
@@ -95,29 +108,66 @@ void MLP::set_max_tokens(int n) {
   max_tokens_ = n;
 }
 
+void MLP::share_scratch_with(moe_ctx *donor) {
+  if (dense_ctx_) throw std::logic_error("MLP::share_scratch_with after init_gpu");
+  donor_ = donor;
+}
+
 void MLP::init_gpu() {
   release_gpu();
-  if (w1_.ndim() != 2 || w3_.shape() != w1_.shape() || w2_.ndim() != 2 ||
-      w2_.shape()[0] != w1_.shape()[1] || w2_.shape()[1] != w1_.shape()[0])
-    throw std::invalid_argument("MLP::init_gpu: w1/w3 must be [I][H] and w2 [H][I]");
-  const int I = (int)w1_.shape()[0], H = (int)w1_.shape()[1];
-  check(moe_dense_create(H, I, max_tokens_, &dense_ctx_), "moe_dense_create");
-  check(moe_dense_set_weights(dense_ctx_, w1_.data(), w3_.data(), w2_.data(), 0, nullptr),
+  int I, H;
+  if (synth_) {
+    I = syn_inter_;
+    H = syn_hidden_;
+  } else {
+    if (w1_.ndim() != 2 || w3_.shape() != w1_.shape() || w2_.ndim() != 2 ||
+        w2_.shape()[0] != w1_.shape()[1] || w2_.shape()[1] != w1_.shape()[0])
+      throw std::invalid_argument("MLP::init_gpu: w1/w3 must be [I][H] and w2 [H][I]");
+    I = (int)w1_.shape()[0];
+    H = (int)w1_.shape()[1];
+  }
+  if (donor_)
+    check(moe_dense_create_shared(H, I, max_tokens_, donor_, &dense_ctx_), "moe_dense_create_shared");
+  else
+    check(moe_dense_create(H, I, max_tokens_, &dense_ctx_), "moe_dense_create");
+  if (!synth_) {
+    check(moe_dense_set_weights(dense_ctx_, w1_.data(), w3_.data(), w2_.data(), 0, nullptr),
+          "moe_dense_set_weights");
+    return;
+  }
+  // synthetic: draw the three matrices on the device under their names
+  const size_t n = (size_t)I * H;
+  DevBuf stage(3 * n * sizeof(float));
+  const char *names[3] = {"w1", "w3", "w2"};
+  for (int k = 0; k < 3; ++k) {
+    std::ostringstream ss;
+    ss << "layers." << layer_idx_ << ".feed_forward." << names[k] << ".weight";
+    check(lfm_synth_normal(stage.f() + k * n, n, syn_.seed, lfm_synth_stream_of(ss.str().c_str()),
+                           syn_.std_dev, 0, nullptr),
+          "lfm_synth_normal");
+  }
+  check(moe_dense_set_weights(dense_ctx_, stage.f(), stage.f() + n, stage.f() + 2 * n, 1, nullptr),
         "moe_dense_set_weights");
 }
 
 void MLP::forward_gpu(float *x, float *y, int batch, int seq_len, int hidden_size,
                       hipStream_t stream) {
+  forward_gpu(x, y, nullptr, batch, seq_len, hidden_size, stream);
+}
+
+void MLP::forward_gpu(float *x, float *y, const float *residual, int batch, int seq_len,
+                      int hidden_size, hipStream_t stream) {
   if (!dense_ctx_) throw std::logic_error("MLP::forward_gpu before init_gpu");
-  if ((size_t)hidden_size != w1_.shape()[1])
+  if (hidden_size != (synth_ ? syn_hidden_ : (int)w1_.shape()[1]))
     throw std::invalid_argument("MLP::forward_gpu: hidden_size mismatch");
   if (batch < 0 || seq_len < 0) throw std::invalid_argument("negative batch/seq_len");
-  check(moe_dense_forward(dense_ctx_, x, y, nullptr, batch * seq_len, stream), "moe_dense_forward");
+  check(moe_dense_forward(dense_ctx_, x, y, residual, batch * seq_len, stream),
+        "moe_dense_forward");
 }
 
 void MLP::forward(const Tensor &x, Tensor &y) {
   if (!dense_ctx_) throw std::logic_error("MLP::forward before init_gpu");
-  const size_t H = w1_.shape()[1];
+  const size_t H = synth_ ? (size_t)syn_hidden_ : w1_.shape()[1];
   if (x.ndim() < 1 || x.size() % H != 0)
     throw std::invalid_argument("MLP::forward: x must be [T][H]");
   const size_t T = x.size() / H;
@@ -156,9 +206,59 @@ SparseMoeBlock::SparseMoeBlock(int layer_idx, Tensor gate, std::vector<MLP> expe
   check_shapes();
 }
 
+SparseMoeBlock::SparseMoeBlock(int layer_idx, int hidden, int inter, const SyntheticWeights &s)
+    : layer_idx_(layer_idx), synth_(true), syn_(s), syn_hidden_(hidden), syn_inter_(inter) {
+  if (hidden <= 0 || inter <= 0)
+    throw std::invalid_argument("SparseMoeBlock: hidden and inter must be > 0");
+}
+
 SparseMoeBlock::~SparseMoeBlock() { moe_destroy(ctx_); }
 
+int SparseMoeBlock::hidden() const { return synth_ ? syn_hidden_ : (int)gate_.shape()[1]; }
+
+int SparseMoeBlock::inter() const {
+  return synth_ ? syn_inter_ : (int)experts_[0].w1().shape()[0];
+}
+
+void SparseMoeBlock::share_scratch_with(moe_ctx *donor) {
+  if (ctx_) throw std::logic_error("SparseMoeBlock::share_scratch_with after init_gpu");
+  donor_ = donor;
+}
+
+// Draws the block's tensors on the device under the reference's names
+// (layer.cu:1277-1298) and packs them into the context.
+void SparseMoeBlock::upload_synthetic() {
+  const size_t H = syn_hidden_, I = syn_inter_, E = NUM_EXPERTS;
+  const size_t ng = E * H, nw = I * H;
+  DevBuf stage((ng + E + 3 * E * nw) * sizeof(float));
+  float *gate = stage.f(), *bias = gate + ng, *w = bias + E;
+  auto draw = [&](float *dst, size_t n, const std::string &name) {
+    check(lfm_synth_normal(dst, n, syn_.seed, lfm_synth_stream_of(name.c_str()), syn_.std_dev, 0,
+                           nullptr),
+          "lfm_synth_normal");
+  };
+  std::ostringstream sg, sb;
+  sg << "layers." << layer_idx_ << ".feed_forward.gate.weight";
+  sb << "layers." << layer_idx_ << ".feed_forward.expert_bias";
+  draw(gate, ng, sg.str());
+  draw(bias, E, sb.str());
+  std::vector<const float *> w1(E), w2(E), w3(E);
+  for (size_t e = 0; e < E; ++e) {
+    float *b = w + 3 * e * nw;
+    draw(b, nw, expert_name(layer_idx_, e, "w1"));
+    draw(b + nw, nw, expert_name(layer_idx_, e, "w3"));
+    draw(b + 2 * nw, nw, expert_name(layer_idx_, e, "w2"));
+    w1[e] = b;
+    w3[e] = b + nw;
+    w2[e] = b + 2 * nw;
+  }
+  check(moe_set_weights(ctx_, gate, USE_EXPERT_BIAS ? bias : nullptr, w1.data(), w3.data(),
+                        w2.data(), 1, nullptr),
+        "moe_set_weights");
+}
+
 void SparseMoeBlock::check_shapes() const {
+  if (synth_) return;
   if (gate_.ndim() != 2 || gate_.shape()[0] != NUM_EXPERTS)
     throw std::invalid_argument("SparseMoeBlock: gate must be [32][hidden]");
   const size_t H = gate_.shape()[1];
@@ -187,12 +287,19 @@ void SparseMoeBlock::init_gpu() {
     ctx_ = nullptr;
   }
   moe_dims d{};
-  d.hidden = (int)gate_.shape()[1];
-  d.inter = (int)experts_[0].w1().shape()[0];
+  d.hidden = hidden();
+  d.inter = inter();
   d.num_experts = (int)NUM_EXPERTS;
   d.top_k = (int)NUM_EXPERTS_PER_TOK;
   d.max_tokens = max_tokens_;
-  check(moe_create(&d, &ctx_), "moe_create");
+  if (donor_)
+    check(moe_create_shared(&d, donor_, &ctx_), "moe_create_shared");
+  else
+    check(moe_create(&d, &ctx_), "moe_create");
+  if (synth_) {
+    upload_synthetic();
+    return;
+  }
   std::vector<const float *> w1(NUM_EXPERTS), w2(NUM_EXPERTS), w3(NUM_EXPERTS);
   for (size_t e = 0; e < NUM_EXPERTS; ++e) {
     w1[e] = experts_[e].w1().data();
@@ -213,7 +320,7 @@ void SparseMoeBlock::forward_gpu(float *x, float *y, int batch, int seq_len,
 void SparseMoeBlock::forward_gpu(float *x, float *y, const float *residual, int batch,
                                  int seq_len, int hidden_size, hipStream_t stream) {
   if (!ctx_) throw std::logic_error("SparseMoeBlock::forward_gpu before init_gpu");
-  if ((size_t)hidden_size != gate_.shape()[1])
+  if (hidden_size != hidden())
     throw std::invalid_argument("SparseMoeBlock::forward_gpu: hidden_size mismatch");
   if (batch < 0 || seq_len < 0) throw std::invalid_argument("negative batch/seq_len");
   check(moe_forward(ctx_, x, y, residual, batch * seq_len, stream), "moe_forward");
@@ -221,15 +328,20 @@ void SparseMoeBlock::forward_gpu(float *x, float *y, const float *residual, int 
 
 void SparseMoeBlock::set_post_attention_norm(const Tensor &weight) {
   if (!ctx_) throw std::logic_error("SparseMoeBlock::set_post_attention_norm before init_gpu");
-  if (weight.size() != gate_.shape()[1])
+  if (weight.size() != (size_t)hidden())
     throw std::invalid_argument("SparseMoeBlock::set_post_attention_norm: weight must have H entries");
   check(moe_set_norm_weight(ctx_, weight.data(), 0, nullptr), "moe_set_norm_weight");
+}
+
+void SparseMoeBlock::set_post_attention_norm_gpu(const float *weight) {
+  if (!ctx_) throw std::logic_error("SparseMoeBlock::set_post_attention_norm_gpu before init_gpu");
+  check(moe_set_norm_weight(ctx_, weight, 1, nullptr), "moe_set_norm_weight");
 }
 
 void SparseMoeBlock::forward_gpu_norm(float *h, float *out, int batch, int seq_len,
                                       int hidden_size, hipStream_t stream) {
   if (!ctx_) throw std::logic_error("SparseMoeBlock::forward_gpu_norm before init_gpu");
-  if ((size_t)hidden_size != gate_.shape()[1])
+  if (hidden_size != hidden())
     throw std::invalid_argument("SparseMoeBlock::forward_gpu_norm: hidden_size mismatch");
   if (batch < 0 || seq_len < 0) throw std::invalid_argument("negative batch/seq_len");
   check(moe_forward_norm(ctx_, h, out, batch * seq_len, stream), "moe_forward_norm");
@@ -237,7 +349,7 @@ void SparseMoeBlock::forward_gpu_norm(float *h, float *out, int batch, int seq_l
 
 void SparseMoeBlock::forward(const Tensor &x, Tensor &y, Tensor &router_logits) {
   if (!ctx_) throw std::logic_error("SparseMoeBlock::forward before init_gpu");
-  const size_t H = gate_.shape()[1];
+  const size_t H = (size_t)hidden();
   if (x.ndim() < 1 || x.size() % H != 0)
     throw std::invalid_argument("SparseMoeBlock::forward: x must be [T][hidden]");
   const size_t T = x.size() / H;

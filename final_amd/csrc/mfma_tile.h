@@ -1,0 +1,266 @@
+// MFMA tile of the grouped and dense GEMMs: C = A . B^T on
+// v_mfma_f32_32x32x2_f32, LDS double-buffered slabs with global loads three
+// slabs ahead.
+#pragma once
+
+#include "gpu_common.h"
+
+namespace moe {
+
+// ---------------------------------------------------------------------------
+// MFMA grouped GEMM tile
+// ---------------------------------------------------------------------------
+
+template <int BM> struct TileCfg;
+// 4 waves as WAVES_M x WAVES_N; a wave owns WM 32-row blocks x WN 32-column
+// blocks.  B rows come in groups of 64 (gate/up phase: 32 rows of W1, then
+// the same 32 columns' rows of W3), and the epilogue pairs them through LDS.
+template <> struct TileCfg<128> {
+  static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, WN = 2, BK = 32;
+};
+// 64x128 tiles (128-1535 tokens): 64x256 tiles left 1.4 tiles per block at
+// T=256 (637 us per step, 527 with 64x128); 64x64 tiles balance the blocks
+// better but lose more per tile (537 us at T=256, 1208 vs 1115 at T=1024)
+template <> struct TileCfg<64> {
+  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, WN = 2, BK = 32;
+};
+template <> struct TileCfg<32> {
+  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 2, BK = 16;
+};
+
+// Half-width down tiles for the last units of a launch (same rows, half the
+// columns), so the last round of tiles is half as long.
+template <int BM> struct TileHalfCfg;
+template <> struct TileHalfCfg<128> {
+  static constexpr int WAVES_M = 4, WM = 1, WAVES_N = 1, WN = 2, BK = 32;
+};
+template <> struct TileHalfCfg<64> {
+  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, WN = 1, BK = 32;
+};
+template <> struct TileHalfCfg<32> {
+  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 1, BK = 16;
+};
+
+template <int BM_, typename C> struct TileT {
+  static constexpr int BM = BM_;
+  static constexpr int WAVES_M = C::WAVES_M, WM = C::WM, WAVES_N = C::WAVES_N, WN = C::WN;
+  static constexpr int BK = C::BK;
+  static constexpr int BN = WAVES_N * WN * 32;
+  static constexpr int PITCH = BK + 4;           // floats per LDS row
+  static constexpr int KV = BK / 4;              // float4 per row per slab
+  static constexpr int A_F4 = BM * KV;           // float4 per A slab
+  static constexpr int B_F4 = BN * KV;
+  static constexpr int A_PER = (A_F4 + kThreads - 1) / kThreads;
+  static constexpr int B_PER = (B_F4 + kThreads - 1) / kThreads;
+  static constexpr int CPITCH = BN + 8;          // epilogue tile row pitch
+  static constexpr int SLAB_FLOATS = 2 * (BM + BN) * PITCH;
+  static constexpr int EPI_FLOATS = BM * CPITCH;
+  static constexpr int LDS_FLOATS = SLAB_FLOATS > EPI_FLOATS ? SLAB_FLOATS : EPI_FLOATS;
+  static_assert(BM == WAVES_M * WM * 32, "tile rows");
+  static_assert(WAVES_M * WAVES_N == kThreads / 64, "four waves");
+  static_assert(BN % 64 == 0, "whole W1/W3 row groups");
+  static_assert(BK % 8 == 0, "k groups of 8");
+};
+template <int BM> using Tile = TileT<BM, TileCfg<BM>>;
+template <int BM> using TileHalf = TileT<BM, TileHalfCfg<BM>>;
+
+// Slab staging of the MFMA tile: buffer float4 loads into registers (A rows
+// gathered; an empty row's offset lies past the buffer, so its loads return
+// zeros without a branch; B rows contiguous with stride K), then LDS stores.
+// Every load is unconditional, so the compiler's count of loads in flight
+// stays exact and a slab's LDS stores wait only for that slab.  Fully
+// unrolled with compile-time indices so the arrays stay in registers while
+// the loads are in flight.
+constexpr uint32_t kTileOOB = 0xFF000000u;  // past every A buffer (moe_create bounds them)
+
+template <int A_PER, int B_PER, int RPP>
+__device__ __forceinline__ void slab_load(f32x4 (&ra)[A_PER], f32x4 (&rb)[B_PER],
+                                          const uint32_t (&a_off)[A_PER],
+                                          __amdgpu_buffer_rsrc_t ar, uint32_t b_off,
+                                          __amdgpu_buffer_rsrc_t br, int K, int k0) {
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i)
+    ra[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, a_off[i] + k0 * 4u, 0, 0));
+#pragma unroll
+  for (int i = 0; i < B_PER; ++i)
+    rb[i] = __builtin_bit_cast(
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(br, b_off + (uint32_t)(i * RPP * K + k0) * 4u, 0, 0));
+}
+
+template <int BM, int A_PER, int B_PER, int RPP, int PITCH>
+__device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4 (&rb)[B_PER],
+                                           float *As, float *Bs, int lds_st, int lrow) {
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i)
+    if (A_PER * RPP <= BM || lrow + i * RPP < BM)  // rows past BM: threads of a partial pass
+      st4(As + lds_st + i * RPP * PITCH, ra[i]);
+#pragma unroll
+  for (int i = 0; i < B_PER; ++i) st4(Bs + lds_st + i * RPP * PITCH, rb[i]);
+}
+
+// Slabs of global loads in flight ahead of the MFMAs (register sets).
+constexpr int kTilePrefetch = 3;
+
+// One output tile of C[rows][cols] = A[rows][K] . B[cols][K]^T.
+// A rows are gathered: row r starts at abase + aoff[r] (aoff in LDS; rows at
+// or past rows_valid are zero; abytes = bytes readable from abase).  B rows
+// are contiguous with stride K from brow0.  GATED: per wave the B tile holds 32 rows of W1 then the same 32 of
+// W3 and the epilogue writes silu(W1 x) * (W3 x); otherwise the product.
+//
+// Slab pipeline: global loads of slab s+1 are in flight while the MFMAs of
+// slab s run from LDS; one barrier per slab (double-buffered LDS).
+// Thread 0 claims the block's next task from `head` once the MFMAs are done
+// (returned; other threads return 0): the epilogue hides the claim's round
+// trip, and a block commits to its next task only near the end of this one.
+// head == nullptr: no claim (grids of one tile per block).  `out` stores the
+// epilogue's float4s: out.store(byte offset into [rows][ldo], value).
+template <typename TL, bool GATED, typename Out = AgentOut>
+__device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_t abytes,
+                                         const int *aoff, int rows_valid,
+                                         const float *brow0, int K, const Out &out,
+                                         int row0, int ldo, int col0, int *head) {
+  constexpr int BM = TL::BM;
+  constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH, KV = TL::KV;
+  constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
+  constexpr int ROWS_PER_PASS = kThreads / KV;  // rows one pass of loads covers
+  static_assert(TL::B_F4 % kThreads == 0, "B slab splits evenly");
+  float *As = lds;                      // [2][BM][PITCH]
+  float *Bs = lds + 2 * BM * PITCH;     // [2][BN][PITCH]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave % TL::WAVES_M, wn = wave / TL::WAVES_M;
+  const int lrow = tid / KV, lc4 = (tid % KV) * 4;
+
+  uint32_t a_src[A_PER];  // byte offset of this thread's A float4 (kTileOOB: zero row)
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i) {
+    const int r = lrow + i * ROWS_PER_PASS;
+    a_src[i] = (r < BM && r < rows_valid) ? (uint32_t)(aoff[r] + lc4) * 4u : kTileOOB;
+  }
+  const __amdgpu_buffer_rsrc_t abase_r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(abase), 0, (int)abytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t bsrc_r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(brow0), 0, (int)((uint32_t)TL::BN * K * 4u), kBufferRsrcWord3);
+  // loads past the last slab use descriptors of size 0 (zeros, no traffic):
+  // every load and LDS store of the loop is unconditional, which keeps the
+  // compiler's count of loads in flight exact across the loop
+  const __amdgpu_buffer_rsrc_t none_r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(brow0), 0, 0, kBufferRsrcWord3);
+  const uint32_t bsrc = (uint32_t)(lrow * K + lc4) * 4u;
+  const int lds_st = lrow * PITCH + lc4;
+
+  floatx16 acc[WM][WN];
+#pragma unroll
+  for (int i = 0; i < WM; ++i)
+#pragma unroll
+    for (int c = 0; c < WN; ++c)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.0f;
+
+  // Rows of this wave that hold data: 0 = skip the MFMAs, <= 32 with WM == 2
+  // = only the first row block (wave-uniform branches).
+  const int wrow0 = wm * WM * 32;
+  const int wrows = min(max(rows_valid - wrow0, 0), WM * 32);
+
+  const int nslab = K / BK;
+  // Global loads run kPrefetch slabs ahead in kPrefetch register sets: slab
+  // t + kPrefetch is loaded while slab t's MFMAs run, and slab t + 1 (loaded
+  // kPrefetch - 1 slabs earlier) is written to LDS after them.
+  constexpr int NS = kTilePrefetch;
+  constexpr int L = NS % 2 == 0 ? NS : 2 * NS;  // steps per unrolled round
+  f32x4 sa[NS][A_PER], sb[NS][B_PER];
+#pragma unroll
+  for (int j = 0; j < NS; ++j) {
+    const bool in = j < nslab;
+    slab_load<A_PER, B_PER, ROWS_PER_PASS>(sa[j], sb[j], a_src, in ? abase_r : none_r, bsrc,
+                                           in ? bsrc_r : none_r, K, in ? j * BK : 0);
+  }
+  slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(sa[0], sb[0], As, Bs, lds_st, lrow);
+  __syncthreads();
+  const int lr = lane & 31, lh = (lane >> 5) * 4;
+  const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
+  const float *b_rd = Bs + (wn * WN * 32 + lr) * PITCH + lh;
+  for (int s = 0; s < nslab; s += L) {
+#pragma unroll
+    for (int u = 0; u < L; ++u) {
+      const int t = s + u;
+      if (t >= nslab) break;
+      // the set of slab t is free (written to LDS a step ago): slab t + NS
+      {
+        const bool in = t + NS < nslab;
+        slab_load<A_PER, B_PER, ROWS_PER_PASS>(sa[u % NS], sb[u % NS], a_src, in ? abase_r : none_r,
+                                               bsrc, in ? bsrc_r : none_r, K, in ? (t + NS) * BK : 0);
+      }
+      const float *Ac = a_rd + (u & 1) * BM * PITCH;
+      const float *Bc = b_rd + (u & 1) * TL::BN * PITCH;
+      if (wrows > 0) {
+#pragma unroll
+        for (int g8 = 0; g8 < BK / 8; ++g8) {
+          f32x4 af[WM], bf[WN];
+#pragma unroll
+          for (int i = 0; i < WM; ++i) af[i] = ld4(Ac + i * 32 * PITCH + g8 * 8);
+#pragma unroll
+          for (int c = 0; c < WN; ++c) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
+#pragma unroll
+          for (int i = 0; i < WM; ++i) {
+            if (i > 0 && wrows <= 32) break;
+#pragma unroll
+            for (int c = 0; c < WN; ++c) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q)
+                acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[c][q], acc[i][c], 0, 0, 0);
+            }
+          }
+        }
+      }
+      // slab t + 1 (past the end: zeros into a buffer nobody reads again)
+      slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(
+          sa[(u + 1) % NS], sb[(u + 1) % NS], As + ((u + 1) & 1) * BM * PITCH,
+          Bs + ((u + 1) & 1) * TL::BN * PITCH, lds_st, lrow);
+      __syncthreads();
+    }
+  }
+
+  const int next = threadIdx.x == 0 && head ? claim(head) : 0;
+
+  // Epilogue through LDS (the slab buffers are free after the last barrier):
+  // the products are written as a [BM][BN] tile in B-row order, then stored
+  // as whole-row float4s; gate/up tiles store silu(W1 x) * (W3 x) of each
+  // 64-row group's two halves.  32x32 f32 MFMA result layout: lane l holds
+  // column l % 32 and rows 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
+  constexpr int NC = GATED ? TL::BN / 2 : TL::BN;  // output columns of the tile
+  constexpr int CP = TL::CPITCH;
+  float *Cs = lds;
+  if (wrows > 0) {
+#pragma unroll
+    for (int i = 0; i < WM; ++i) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int row = wrow0 + i * 32 + 8 * (r >> 2) + (lane >> 5) * 4 + (r & 3);
+#pragma unroll
+        for (int c = 0; c < WN; ++c) Cs[row * CP + (wn * WN + c) * 32 + lr] = acc[i][c][r];
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int NC4 = NC / 4;
+  for (int f = tid; f < BM * NC4; f += kThreads) {
+    const int row = f / NC4, c4 = (f % NC4) * 4;
+    if (row < rows_valid) {
+      f32x4 v;
+      if (GATED) {
+        const float *g = Cs + row * CP + (c4 >> 5) * 64 + (c4 & 31);
+        const f32x4 w1 = ld4(g), w3 = ld4(g + 32);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = silu(w1[j]) * w3[j];
+      } else {
+        v = ld4(Cs + row * CP + c4);
+      }
+      out.store((uint32_t)(((size_t)(row0 + row) * ldo + col0 + c4) * sizeof(float)), v);
+    }
+  }
+  __syncthreads();  // Cs aliases the slab buffers of the next tile
+  return next;
+}
+
+}  // namespace moe

@@ -155,6 +155,7 @@ struct moe_ctx {
   float *xn = nullptr;      // [max_tokens][H]: normalised rows
   int normed_T = -1;
   Scratch s{};
+  moe_ctx *donor = nullptr;  // context whose scratch this one uses (moe_create_shared)
   std::vector<void *> allocs;
 };
 
@@ -236,8 +237,11 @@ const char *moe_strerror(int status) {
 const char *moe_version(void) { return "final_amd-moe 0.1.0 gfx950"; }
 
 // A context with expert weights for e_alloc experts (all kExperts for the
-// MoE block, kDenseChunks for the dense FFN, which has no gate).
-static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **out) {
+// MoE block, kDenseChunks for the dense FFN, which has no gate).  With a
+// donor the context allocates only its weights and runs on the donor's
+// scratch (same hidden and per-expert inter, max_tokens <= the donor's).
+static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **out,
+                      moe_ctx *donor = nullptr) {
   moe_ctx *ctx = new (std::nothrow) moe_ctx();
   if (!ctx) return MOE_ERR_OUT_OF_MEMORY;
   ctx->d = d;
@@ -264,6 +268,28 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
     return MOE_ERR_UNSUPPORTED;
   }
   int rc = MOE_OK;
+  if (donor) {
+    while (donor->donor) donor = donor->donor;
+    if (donor->d.hidden != d.hidden || donor->d.inter != d.inter ||
+        donor->d.max_tokens < d.max_tokens || donor->device != ctx->device) {
+      delete ctx;
+      return MOE_ERR_INVALID_ARG;
+    }
+    if ((!dense && (rc = dev_alloc(ctx, &ctx->gate, E * H))) ||
+        (!dense && (rc = dev_alloc(ctx, &ctx->bias, E))) ||
+        (rc = dev_alloc(ctx, &ctx->w13, e_alloc * 2 * I * H)) ||
+        (rc = dev_alloc(ctx, &ctx->w2, e_alloc * H * I))) {
+      free_all(ctx);
+      delete ctx;
+      return rc;
+    }
+    ctx->donor = donor;
+    ctx->s = donor->s;
+    ctx->max_units = donor->max_units;
+    for (int p = 0; p < 4; ++p) ctx->grid[p] = donor->grid[p];
+    *out = ctx;
+    return MOE_OK;
+  }
   if ((!dense && (rc = dev_alloc(ctx, &ctx->gate, E * H))) ||
       (!dense && (rc = dev_alloc(ctx, &ctx->bias, E))) ||
       (rc = dev_alloc(ctx, &ctx->w13, e_alloc * 2 * I * H)) ||
@@ -327,7 +353,25 @@ int moe_create(const moe_dims *dims, moe_ctx **out) {
   return create_ctx(d, kExperts, false, out);
 }
 
+int moe_create_shared(const moe_dims *dims, moe_ctx *donor, moe_ctx **out) {
+  if (!dims || !donor || !out) return MOE_ERR_INVALID_ARG;
+  *out = nullptr;
+  const moe_dims d = *dims;
+  if (d.hidden <= 0 || d.inter <= 0 || d.max_tokens <= 0 || d.max_tokens > kMaxTokensLimit)
+    return MOE_ERR_INVALID_ARG;
+  if (d.num_experts != kExperts || d.top_k != kTopK || d.hidden % 256 != 0 || d.inter % 256 != 0)
+    return MOE_ERR_UNSUPPORTED;
+  DeviceGuard g(donor->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  return create_ctx(d, kExperts, false, out, donor);
+}
+
 int moe_dense_create(int hidden, int inter, int max_tokens, moe_ctx **out) {
+  return moe_dense_create_shared(hidden, inter, max_tokens, nullptr, out);
+}
+
+int moe_dense_create_shared(int hidden, int inter, int max_tokens, moe_ctx *donor,
+                            moe_ctx **out) {
   if (!out) return MOE_ERR_INVALID_ARG;
   *out = nullptr;
   if (hidden <= 0 || inter <= 0 || max_tokens <= 0 || max_tokens > kMaxTokensLimit)
@@ -339,7 +383,14 @@ int moe_dense_create(int hidden, int inter, int max_tokens, moe_ctx **out) {
   d.num_experts = kExperts;
   d.top_k = kTopK;
   d.max_tokens = max_tokens;
-  const int rc = create_ctx(d, kDenseChunks, true, out);
+  int rc;
+  if (donor) {
+    DeviceGuard g(donor->device);
+    if (!g.ok) return MOE_ERR_HIP;
+    rc = create_ctx(d, kDenseChunks, true, out, donor);
+  } else {
+    rc = create_ctx(d, kDenseChunks, true, out);
+  }
   if (rc == MOE_OK) (*out)->dense_inter = inter;
   return rc;
 }
@@ -658,8 +709,19 @@ int moe_set_norm_weight(moe_ctx *ctx, const float *weight, int src_on_device,
     float *nw = nullptr, *xn = nullptr;
     int rc = dev_alloc(ctx, &nw, H);
     if (rc) return rc;
-    rc = dev_alloc(ctx, &xn, (size_t)ctx->d.max_tokens * H);
-    if (rc) return rc;
+    if (ctx->donor) {
+      // the normalised rows are scratch too: the donor's serve every sharer
+      if (!ctx->donor->xn) {
+        rc = dev_alloc(ctx->donor, &ctx->donor->xn, (size_t)ctx->donor->d.max_tokens * H);
+        if (rc) return rc;
+      }
+      xn = ctx->donor->xn;
+    } else if (ctx->xn) {
+      xn = ctx->xn;  // allocated for the context's sharers already
+    } else {
+      rc = dev_alloc(ctx, &xn, (size_t)ctx->d.max_tokens * H);
+      if (rc) return rc;
+    }
     ctx->norm_w = nw;
     ctx->xn = xn;
   }

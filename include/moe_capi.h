@@ -131,6 +131,21 @@ int moe_route_logits(moe_ctx *ctx, const float *logits, int num_tokens,
  * with moe_destroy.  moe_forward / moe_route / moe_set_weights reject a dense
  * context and moe_dense_* reject a MoE context. */
 int moe_dense_create(int hidden, int inter, int max_tokens, moe_ctx **out);
+
+/* A context that owns only its weights and runs on the scratch of `donor`
+ * (routing, plan, intermediate and expert-output rows, normalised rows):
+ * the decoder layers of one model run one after another on one stream, so
+ * they need one scratch between them, not one each (the reference gives
+ * every layer its own, layer.cu:1399-1425).  Replaces moe_create /
+ * moe_dense_create for such layers: hidden and the per-expert intermediate
+ * (inter, or inter / 4 for the dense FFN) must equal the donor's, max_tokens
+ * must not exceed it, same device.  The donor must outlive the context, and
+ * every context sharing a scratch must be used on one stream, one call after
+ * another; moe_last_routing / moe_last_normed on any of them read the last
+ * forward of any of them.  Released with moe_destroy. */
+int moe_create_shared(const moe_dims *dims, moe_ctx *donor, moe_ctx **out);
+int moe_dense_create_shared(int hidden, int inter, int max_tokens, moe_ctx *donor,
+                            moe_ctx **out);
 /* w1, w3 [inter][hidden], w2 [hidden][inter] (MLP's w1/w3/w2 tensors,
  * layer.cu:1199-1204); host memory when src_on_device == 0.  Synchronises
  * `stream`. */

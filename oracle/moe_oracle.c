@@ -413,11 +413,83 @@ void orc_rmsnorm(const float *h, const float *weight, int64_t T, int H, float *o
 /* whole block                                                               */
 /* ------------------------------------------------------------------------ */
 
+#define ORC_MAX_EXPERTS 256
+
+/* Adopts guide[] (another implementation's top-4 of one token, rank order)
+ * in place of the oracle's own when it is a top-4 of the oracle's scores up
+ * to eps: four distinct experts, each scoring at least the best excluded
+ * expert minus eps, in non-increasing score order up to eps.  The weights
+ * are then the reference's renormalisation (layer.cu:480-491) of the
+ * oracle's own probabilities in the guide's order.  Returns 0 when the guide
+ * equals the own choice, 1 when adopted, -1 when it is not a near-tie. */
+static int adopt_guide(const float *lg, const float *bias, int E, const int *guide,
+                       float eps, int *idx, float *w) {
+  int same = 1;
+  for (int k = 0; k < ORC_TOPK; ++k) same &= guide[k] == idx[k];
+  if (same) return 0;
+  float sc[ORC_MAX_EXPERTS], pr[ORC_MAX_EXPERTS];
+  if (E > ORC_MAX_EXPERTS) return -1;
+  for (int e = 0; e < E; ++e) {
+    pr[e] = orc_sigmoid(lg[e]);
+    sc[e] = pr[e] + (bias ? bias[e] : 0.0f);
+  }
+  int in[ORC_MAX_EXPERTS] = {0};
+  for (int k = 0; k < ORC_TOPK; ++k) {
+    const int e = guide[k];
+    if (e < 0 || e >= E || in[e]) return -1;
+    in[e] = 1;
+    if (sc[e] != sc[e]) return -1; /* never a NaN score */
+    if (k > 0 && sc[e] > sc[guide[k - 1]] + eps) return -1;
+  }
+  float lo = sc[guide[0]], hi = -INFINITY;
+  for (int k = 1; k < ORC_TOPK; ++k) lo = fminf(lo, sc[guide[k]]);
+  for (int e = 0; e < E; ++e)
+    if (!in[e] && sc[e] == sc[e]) hi = fmaxf(hi, sc[e]);
+  if (lo < hi - eps) return -1;
+  float sum = 0.0f;
+  for (int k = 0; k < ORC_TOPK; ++k) sum += pr[guide[k]];
+  const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;
+  for (int k = 0; k < ORC_TOPK; ++k) {
+    idx[k] = guide[k];
+    w[k] = pr[guide[k]] * scale * 1.0f;
+  }
+  return 1;
+}
+
+static int moe_forward_impl(const float *x, const float *gate, const float *bias,
+                            const float *w1, const float *w3, const float *w2,
+                            const float *residual, int64_t T, int H, int I, int E,
+                            const uint8_t *token_mask, float *y, float *logits_out,
+                            int *idx_out, float *w_out, int *counts_out,
+                            const int *guide, float eps, int64_t *n_adopted,
+                            int64_t *n_hard);
+
 int orc_moe_forward(const float *x, const float *gate, const float *bias,
                     const float *w1, const float *w3, const float *w2,
                     const float *residual, int64_t T, int H, int I, int E,
                     const uint8_t *token_mask, float *y, float *logits_out,
                     int *idx_out, float *w_out, int *counts_out) {
+  return moe_forward_impl(x, gate, bias, w1, w3, w2, residual, T, H, I, E, token_mask, y,
+                          logits_out, idx_out, w_out, counts_out, NULL, 0.0f, NULL, NULL);
+}
+
+int orc_moe_forward_guided(const float *x, const float *gate, const float *bias,
+                           const float *w1, const float *w3, const float *w2,
+                           const float *residual, int64_t T, int H, int I, int E,
+                           const int *guide, float eps, float *y, int *idx_out,
+                           int64_t *n_adopted, int64_t *n_hard) {
+  if (!guide || !n_adopted || !n_hard) return -1;
+  return moe_forward_impl(x, gate, bias, w1, w3, w2, residual, T, H, I, E, NULL, y, NULL,
+                          idx_out, NULL, NULL, guide, eps, n_adopted, n_hard);
+}
+
+static int moe_forward_impl(const float *x, const float *gate, const float *bias,
+                            const float *w1, const float *w3, const float *w2,
+                            const float *residual, int64_t T, int H, int I, int E,
+                            const uint8_t *token_mask, float *y, float *logits_out,
+                            int *idx_out, float *w_out, int *counts_out,
+                            const int *guide, float eps, int64_t *n_adopted,
+                            int64_t *n_hard) {
   if (T < 0 || H <= 0 || I <= 0 || E < ORC_TOPK) return -1;
   const int64_t S = T * ORC_TOPK;
   int rc = -1;
@@ -436,6 +508,20 @@ int orc_moe_forward(const float *x, const float *gate, const float *bias,
 
   orc_gate_logits(x, gate, T, H, E, logits);
   orc_route(logits, bias, T, E, idx, w, counts);
+  if (guide) {
+    int64_t na = 0, nh = 0;
+    for (int64_t t = 0; t < T; ++t) {
+      const int r = adopt_guide(logits + t * E, bias, E, guide + t * ORC_TOPK, eps,
+                                idx + t * ORC_TOPK, w + t * ORC_TOPK);
+      na += r == 1;
+      nh += r < 0;
+    }
+    *n_adopted = na;
+    *n_hard = nh;
+    for (int e = 0; e < E; ++e) counts[e] = 0;
+    for (int64_t t = 0; t < T * ORC_TOPK; ++t)
+      if (idx[t] >= 0 && idx[t] < E) counts[idx[t]]++;
+  }
   orc_dispatch(idx, T, E, offsets, pos, slot_token);
 
   /* slots whose token is selected get a compact row in outc */

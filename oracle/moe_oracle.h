@@ -129,6 +129,24 @@ int orc_moe_forward(const float *x, const float *gate, const float *bias,
                     const uint8_t *token_mask, float *y, float *logits, int *idx,
                     float *w, int *counts);
 
+/* orc_moe_forward for all T tokens with the routing of another
+ * implementation as a guide: where guide [T][4] (rank order) differs from the
+ * oracle's own top-4 of a token but is a top-4 of the oracle's scores up to
+ * eps (four distinct experts, none scoring more than eps below an excluded
+ * expert, in non-increasing order up to eps), the oracle adopts it, with the
+ * weights renormalised from its own probabilities in that order
+ * (layer.cu:480-491); otherwise it keeps its own.  n_adopted counts adopted
+ * tokens, n_hard the tokens whose guide is not a near-tie.  Used where the
+ * oracle runs on inputs that differ from the other implementation's by
+ * rounding only (a decoder's later layers), so that a near-tie decided the
+ * other way is followed instead of diverging.  idx_out (may be NULL) gets the
+ * routing used.  Returns 0, or -1 on bad arguments. */
+int orc_moe_forward_guided(const float *x, const float *gate, const float *bias,
+                           const float *w1, const float *w3, const float *w2,
+                           const float *residual, int64_t T, int H, int I, int E,
+                           const int *guide, float eps, float *y, int *idx_out,
+                           int64_t *n_adopted, int64_t *n_hard);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,8 +5,10 @@ __graft_entry__.py and by the cpu_baseline leg of bench.py, always as the
 checker.  The product package (final_amd) never imports this module.
 
 The oracle restates the reference's MoE arithmetic (risepower20/final,
-src/layer.cu:9-141, 434-542, 695-1126, 1428-1498, 1860-1880); each C function
-cites the lines it follows.
+src/layer.cu:9-141, 434-542, 695-1126, 1428-1498, 1860-1880) and the decoder
+around it (layer.cu:144-429, 1508-1922; model.cu:18-116, 469-559); each C
+function cites the lines it follows, and decoder_layer / model_head below
+compose them in DecoderLayer::forward_gpu's and worker_stage's order.
 """
 from __future__ import annotations
 
@@ -65,6 +67,20 @@ def lib():
                                       _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                       _u8p, _f32p, _f32p, _i32p, _f32p, _i32p]
         L.orc_moe_forward.restype = ctypes.c_int
+        L.orc_moe_forward_guided.argtypes = [_f32p, _f32p, _f32p, _f32p, _f32p, _f32p, _f32p,
+                                             _i64, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                             _i32p, ctypes.c_float, _f32p, _i32p,
+                                             ctypes.POINTER(_i64), ctypes.POINTER(_i64)]
+        L.orc_moe_forward_guided.restype = ctypes.c_int
+        L.orc_embed.argtypes = [_i32p, _i64, _f32p, ctypes.c_int, ctypes.c_int, _f32p]
+        L.orc_rope_tables.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        L.orc_qk_norm_rope.argtypes = [_f32p, ctypes.c_int, _i64, ctypes.c_int, ctypes.c_int,
+                                       ctypes.c_int, ctypes.c_int, _f32p, _f32p, _f32p, _f32p]
+        L.orc_attention.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p]
+        L.orc_shortconv.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, _f32p]
+        L.orc_add.argtypes = [_f32p, _f32p, _i64, _f32p]
         _lib = L
     return _lib
 
@@ -229,3 +245,135 @@ def moe_forward(x, gate, bias, w1, w3, w2, residual=None, token_mask=None):
     if rc != 0:
         raise RuntimeError("orc_moe_forward failed")
     return {"y": y, "logits": logits, "idx": idx, "w": w, "counts": counts}
+
+
+# ---------------------------------------------------------------------------
+# Decoder model around the block (lfm_oracle.c)
+# ---------------------------------------------------------------------------
+
+HEADS, KV_HEADS, HEAD_DIM, CONV_L = 32, 8, 64, 3  # config.h:8-9,28-29
+Q_COLS, KV_COLS = HEADS * HEAD_DIM, KV_HEADS * HEAD_DIM
+ROPE_THETA = 1000000.0
+
+
+def _c32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def embed(ids, table):
+    """embedding_lookup_kernel (model.cu:18-32)."""
+    ids = np.ascontiguousarray(ids, dtype=np.int32).reshape(-1)
+    V, H = table.shape
+    h = np.empty((ids.size, H), np.float32)
+    lib().orc_embed(_i(ids), ids.size, _f(_c32(table)), H, V, _f(h))
+    return h
+
+
+def rope_tables(max_pos, head_dim=HEAD_DIM, theta=ROPE_THETA):
+    """RotaryEmbedding::init_gpu's cos/sin tables [max_pos][head_dim]."""
+    c = np.empty((max_pos, head_dim), np.float32)
+    s_ = np.empty((max_pos, head_dim), np.float32)
+    lib().orc_rope_tables(_f(c), _f(s_), max_pos, head_dim, theta)
+    return c, s_
+
+
+def qk_norm_rope(qkv, seq, q_weight, k_weight, cos, sin, heads=HEADS, kv_heads=KV_HEADS,
+                 k_col=Q_COLS):
+    """Returns a copy of qkv [T][ld] with its q/k heads normalised and rotated."""
+    out = np.array(qkv, dtype=np.float32, order="C", copy=True)
+    T, ld = out.shape
+    lib().orc_qk_norm_rope(_f(out), ld, T, seq, heads, kv_heads, k_col, _f(_c32(q_weight)),
+                           _f(_c32(k_weight)), _f(_c32(cos)), _f(_c32(sin)))
+    return out
+
+
+def attention(qkv, batch, seq, heads=HEADS, kv_heads=KV_HEADS, k_col=Q_COLS,
+              v_col=Q_COLS + KV_COLS):
+    """Causal GQA attention (fused_attn_gqa_kernel, any seq) -> [T][heads*64]."""
+    qkv = _c32(qkv)
+    out = np.empty((batch * seq, heads * HEAD_DIM), np.float32)
+    lib().orc_attention(_f(qkv), qkv.shape[1], batch, seq, heads, kv_heads, k_col, v_col, _f(out))
+    return out
+
+
+def shortconv(bcg, conv_w, batch, seq, L=CONV_L):
+    """ShortConv's mix (layer.cu:360-429): bcg [T][3H] -> [T][H]."""
+    bcg = _c32(bcg)
+    H = bcg.shape[1] // 3
+    y = np.empty((batch * seq, H), np.float32)
+    lib().orc_shortconv(_f(bcg), _f(_c32(conv_w).reshape(H, L)), batch, seq, H, L, _f(y))
+    return y
+
+
+def add(a, b):
+    """add_kernel (layer.cu:1860-1880)."""
+    a, b = _c32(a), _c32(b)
+    out = np.empty_like(a)
+    lib().orc_add(_f(a), _f(b), a.size, _f(out))
+    return out
+
+
+def moe_forward_guided(x, gate, bias, w1, w3, w2, residual, guide, eps):
+    """moe_forward over all tokens, following guide [T][4] where it is a
+    near-tie of the oracle's scores (orc_moe_forward_guided).  Returns
+    (y, idx used, adopted count, count of guides that are not near-ties)."""
+    T, H = x.shape
+    E, I, _ = w1.shape
+    y = np.empty((T, H), np.float32)
+    idx = np.empty((T, TOPK), np.int32)
+    na, nh = _i64(0), _i64(0)
+    rc = lib().orc_moe_forward_guided(
+        _f(_c32(x)), _f(gate), _f(bias), _f(w1), _f(w3), _f(w2), _f(_c32(residual)), T, H, I, E,
+        _i(np.ascontiguousarray(guide, dtype=np.int32)), float(eps), _f(y), _i(idx),
+        ctypes.byref(na), ctypes.byref(nh))
+    if rc != 0:
+        raise RuntimeError("orc_moe_forward_guided failed")
+    return y, idx, int(na.value), int(nh.value)
+
+
+def decoder_layer(h, w, batch, seq, cos, sin, guide=None, eps=0.0):
+    """DecoderLayer::forward_gpu (layer.cu:1882-1919) on h [T][H] (T = batch*seq):
+    operator norm; attention (q|k|v projections, q/k norm + rotation, causal
+    GQA attention, out_proj) or short conv (in_proj, mix, out_proj); residual;
+    FFN norm; MoE block (or dense FFN); residual.  w: dict of the layer's
+    tensors under the reference's short names (op_norm, ffn_norm, q, k, v, o,
+    q_norm, k_norm | conv, in_proj, out_proj; gate, bias, w1, w3, w2 for a MoE
+    FFN with w1/w3 [E][I][H] and w2 [E][H][I], or dense_w1/w3/w2).  guide:
+    routing of another implementation to follow on near-ties (MoE only).
+    Returns (h', info) with the routing used and the near-tie counts."""
+    h = _c32(h)
+    xn = rmsnorm(h, w["op_norm"])
+    if "q" in w:
+        heads, kvh = w["q"].shape[0] // HEAD_DIM, w["k"].shape[0] // HEAD_DIM
+        qc, kc = heads * HEAD_DIM, kvh * HEAD_DIM
+        wqkv = np.ascontiguousarray(np.concatenate([w["q"], w["k"], w["v"]], axis=0))
+        qkv = gemm_nt_chain(xn, wqkv)
+        qkv = qk_norm_rope(qkv, seq, w["q_norm"], w["k_norm"], cos, sin, heads, kvh, qc)
+        att = attention(qkv, batch, seq, heads, kvh, qc, qc + kc)
+        op = gemm_nt_chain(att, _c32(w["o"]))
+    else:
+        bcg = gemm_nt_chain(xn, _c32(w["in_proj"]))
+        mix = shortconv(bcg, w["conv"], batch, seq)
+        op = gemm_nt_chain(mix, _c32(w["out_proj"]))
+    h = add(h, op)
+    info = {}
+    if "gate" in w:
+        x2 = rmsnorm(h, w["ffn_norm"])
+        if guide is None:
+            r = moe_forward(x2, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"], residual=h)
+            h, info["idx"], info["adopted"], info["hard"] = r["y"], r["idx"], 0, 0
+        else:
+            h, info["idx"], info["adopted"], info["hard"] = moe_forward_guided(
+                x2, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"], h, guide, eps)
+    else:
+        x2 = rmsnorm(h, w["ffn_norm"])
+        h = dense_mlp(x2, w["dense_w1"], w["dense_w3"], w["dense_w2"], residual=h)
+    return h, info
+
+
+def model_head(h, norm_weight, head, batch, seq):
+    """Final RMSNorm of each sequence's last token and the LM head
+    (model.cu:481-536, lm_head_gemm_kernel's FMA chains) -> [batch][vocab]."""
+    H = h.shape[1]
+    last = np.ascontiguousarray(_c32(h).reshape(batch, seq, H)[:, seq - 1, :])
+    return gemm_nt_chain(rmsnorm(last, norm_weight), _c32(head))

@@ -15,10 +15,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 INCLUDE = os.path.join(ROOT, "include")
 
 
-def declared_c_functions(header):
+def declared_c_functions(header, prefix="moe_"):
     text = open(os.path.join(INCLUDE, header)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(moe_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(" + prefix + r"\w+)\s*\(", text)))
 
 
 @pytest.fixture(scope="module")
@@ -35,6 +35,11 @@ def test_c_symbols_exported(L):
         assert hasattr(L, n), f"{n} declared in include/ but not exported"
     assert set(declared_c_functions("moe_capi.h")) == set(_native.CAPI_SYMBOLS)
     assert set(declared_c_functions("moe_synth.h")) == set(_native.SYNTH_SYMBOLS)
+    lfm = declared_c_functions("lfm_capi.h", "lfm_")
+    assert len(lfm) >= 20
+    for n in lfm:
+        assert hasattr(L, n), f"{n} declared in include/lfm_capi.h but not exported"
+    assert set(lfm) == set(_native.LFM_SYMBOLS)
 
 
 def test_cpp_interface_exported():
@@ -53,6 +58,18 @@ def test_cpp_interface_exported():
         "ModelLoader::ModelLoader(",
         "ModelLoader::load_tensor(",
         "g_model_loader",
+        "RMSNorm::forward_gpu(float*, float*, int, int, ihipStream_t*)",
+        "RotaryEmbedding::init_gpu()",
+        "Attention::Attention(int)",
+        "Attention::forward_gpu(float*, float*, float*, float*, int, int, int, ihipStream_t*)",
+        "ShortConv::ShortConv(int)",
+        "ShortConv::forward_gpu(float*, float*, int, int, int, ihipStream_t*)",
+        "DecoderLayer::DecoderLayer(int, bool)",
+        "DecoderLayer::init_gpu(int)",
+        "DecoderLayer::forward_gpu(float*, float*, float*, float*, int, int, int, ihipStream_t*)",
+        "LFM2Model::LFM2Model(std::__cxx11::basic_string<char, std::char_traits<char>, std::allocator<char> > const&)",
+        "LFM2Model::forward(int, int, int const*, unsigned long, float*)",
+        "LFM2Model::sync()",
     ):
         assert sig in out, sig
 
@@ -101,3 +118,31 @@ def test_error_raises_with_status():
         _native.check(_native.MOE_ERR_TOO_MANY_TOKENS, "moe_forward")
     assert ei.value.status == _native.MOE_ERR_TOO_MANY_TOKENS
     assert "max_tokens" in str(ei.value)
+
+
+def test_lfm_argument_validation_before_any_gpu_call(L):
+    from final_amd import _native
+    INV, UNS = _native.MOE_ERR_INVALID_ARG, _native.MOE_ERR_UNSUPPORTED
+    a = 4096  # a 16-byte-aligned non-null address the checks never dereference
+    assert L.lfm_gemm_nt(None, a, a + 64, None, 4, 128, 32, None) == INV
+    assert L.lfm_gemm_nt(a, a, a + 64, None, -1, 128, 32, None) == INV
+    assert L.lfm_gemm_nt(a, a + 64, a, None, 4, 128, 32, None) == INV      # C aliases A
+    assert L.lfm_gemm_nt(a, a + 64, a + 128, None, 4, 100, 32, None) == UNS  # N % 128
+    assert L.lfm_gemm_nt(a, a + 64, a + 128, None, 4, 128, 48, None) == UNS  # K % 32
+    assert L.lfm_gemm_nt(a + 4, a + 64, a + 128, None, 4, 128, 32, None) == INV  # misaligned
+    assert L.lfm_gemm_nt(None, None, None, None, 0, 128, 32, None) == _native.MOE_OK
+    assert L.lfm_embed(None, a, a, 4, 2048, 100, None, None) == INV
+    assert L.lfm_embed(a, a, a, 4, 2050, 100, None, None) == UNS
+    assert L.lfm_rmsnorm(a, 10, a, a, 64, 2, 64, None) == INV             # stride < dim
+    assert L.lfm_qk_norm_rope(a, 3072, a, a, a, a, 1, 4, 32, 8, 1024, None) == INV  # k_col overlaps q
+    assert L.lfm_attention(a, 3072, a + 4096 * 16, 1, 4, 32, 4, 2048, 2560, None) == UNS  # 8 groups
+    assert L.lfm_attention(a, 3072, a, 1, 4, 32, 8, 2048, 2560, None) == INV  # out aliases qkv
+    assert L.lfm_shortconv(a, a, a + 64, 1, 4, 2050, 3, None) == UNS
+    assert L.lfm_shortconv(a, a, a, 1, 4, 2048, 3, None) == INV
+    assert L.lfm_model_forward(None, a, 1, 1, a, None) == INV
+    assert L.lfm_model_destroy(None) == _native.MOE_OK
+    assert L.lfm_model_create_synthetic(None, None) == INV
+    assert L.lfm_rope_tables(None, None, 4, 64, 1e6) == INV
+    assert L.lfm_synth_is_norm(b"layers.0.ffn_norm.weight") == 1
+    assert L.lfm_synth_is_norm(b"layers.0.conv.in_proj.weight") == 0
+    assert L.lfm_synth_stream_of(b"a") == 0xAF63DC4C8601EC8C  # FNV-1a 64 of "a"
