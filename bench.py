@@ -14,6 +14,14 @@ Prints ONE JSON line on stdout (progress goes to stderr):
                 pass of the same steps after the timed ones
   cpu_baseline  the CPU oracle (a restatement of the reference's arithmetic)
                 on this host, median of a few runs
+  sweep         the other configurations measured the same way in the same
+                run: the decode shapes T = 1, 8, 64, 256 (four weight copies
+                cycled so the 256 MB Infinity Cache cannot serve them; T=64 is
+                also the reference's CPU-runnable case and carries its CPU
+                baseline), the skewed-routing T=16384 case, and the whole
+                24-layer decoder forward at batch 64 x seq 512 (embedding, 6
+                attention + 18 short-conv layers, each with the MoE FFN, final
+                norm and LM head)
 """
 from __future__ import annotations
 
@@ -31,6 +39,11 @@ METRIC = "MoE-block tokens/sec at T=4096 fp32, 1 GPU; % of MFMA / HBM roofline"
 PEAK_MFMA_F32_TFLOPS = 157.3   # MI355X dense fp32 matrix
 PEAK_HBM_GBS = 8000.0          # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+TRAFFIC_SOURCE = ("profiles/traffic.json: rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of the same "
+                  "workload in an earlier run, scaled by a copy kernel of known size; not counted "
+                  "in this run")
+SWEEP_MOE = ("decode_t1", "decode_t8", "decode_t64", "decode_t256", "zipf_t16384")
+DATA = "synthetic (seeded N(0,0.02) weights, N(0,1) tokens)"
 
 
 def log(*a):
@@ -42,11 +55,14 @@ def parse():
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=20)
     p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="prefill_t4096")
+    p.add_argument("--workload", default="prefill_t4096",
+                   help="headline workload (final_amd.workloads.WORKLOADS, or lfm2_b64_s512)")
     p.add_argument("--weight-sets", type=int, default=0,
                    help="distinct weight copies cycled per step (0 = auto: enough to "
                         "exceed the 256 MB Infinity Cache for small T)")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-sweep", action="store_true", help="headline workload only")
+    p.add_argument("--model-steps", type=int, default=3, help="timed forwards of the model")
     p.add_argument("--cpu-threads", type=int, default=0)
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run device-to-device copies of MIB MiB (the runtime's copy "
@@ -68,19 +84,20 @@ def host_cpu() -> dict:
     return {"nproc": os.cpu_count(), "usable": usable, "model": model}
 
 
-def cpu_baseline(w, x, threads: int, single_tokens: int = 128):
+def cpu_baseline(w, x, threads: int, single_tokens: int = 128, min_s: float = 0.0):
     """The oracle over the workload on `threads` OpenMP threads (the reported
-    value), plus one thread over the first `single_tokens` tokens (tokens are
+    value; repeated until min_s seconds of work, at most 3 runs above it),
+    plus one thread over the first `single_tokens` tokens (tokens are
     independent, so a prefix is a fair sample of the per-token cost)."""
     from oracle import oracle as O
     T = x.shape[0]
     O.set_threads(threads)
     times = []
-    for _ in range(3):
+    while True:
         t0 = time.perf_counter()
         O.moe_forward(x, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
         times.append(time.perf_counter() - t0)
-        if sum(times) > 30.0:
+        if sum(times) > 30.0 or (len(times) >= 3 and sum(times) >= min_s):
             break
     med = statistics.median(times)
     n1 = min(T, single_tokens)
@@ -91,10 +108,202 @@ def cpu_baseline(w, x, threads: int, single_tokens: int = 128):
     O.set_threads(threads)
     return {"value": round(T / med, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"whole workload ({T} tokens), median of {len(times)} runs, "
-                      f"{med:.3f} s each, OpenMP {threads} threads",
+                      f"{med:.4f} s each, OpenMP {threads} threads",
             "single_thread": {"value": round(n1 / t1, 2), "unit": "tokens/s",
                               "sample": f"first {n1} tokens, one run of {t1:.3f} s, 1 thread"},
             "host": host_cpu()}
+
+
+def roofline(plan, flops, nbytes, ms, name):
+    """Primary bound of the expert kernel for its plan; the other bound too
+    when the arithmetic intensity is within 2x of the ridge (157.3/8 FLOP/B)."""
+    mfma_bound = plan != 0
+    if mfma_bound:
+        a = flops / (ms / 1e3) / 1e12
+        roof = {"bound": "mfma", "achieved": round(a, 3), "peak": PEAK_MFMA_F32_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(a / PEAK_MFMA_F32_TFLOPS, 4)}
+    else:
+        a = nbytes / (ms / 1e3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(a, 1), "peak": PEAK_HBM_GBS,
+                "unit": "GB/s", "frac": round(a / PEAK_HBM_GBS, 4)}
+    ai = flops / max(nbytes, 1)
+    ridge = PEAK_MFMA_F32_TFLOPS * 1e3 / PEAK_HBM_GBS
+    if 0.5 <= ai / ridge <= 2.0:
+        if mfma_bound:
+            o = nbytes / (ms / 1e3) / 1e9
+            roof["secondary"] = {"bound": "hbm", "achieved": round(o, 1), "peak": PEAK_HBM_GBS,
+                                 "unit": "GB/s", "frac": round(o / PEAK_HBM_GBS, 4),
+                                 "per_launch": {"bytes": nbytes}}
+        else:
+            o = flops / (ms / 1e3) / 1e12
+            roof["secondary"] = {"bound": "mfma", "achieved": round(o, 3),
+                                 "peak": PEAK_MFMA_F32_TFLOPS, "unit": "TFLOP/s",
+                                 "frac": round(o / PEAK_MFMA_F32_TFLOPS, 4),
+                                 "per_launch": {"flop": flops}}
+        roof["arithmetic_intensity"] = round(ai, 2)
+    roof["traffic"] = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            tr = json.load(f).get(name)
+        if tr:
+            roof["traffic"] = tr.get("bytes_per_launch")
+            roof["traffic_source"] = TRAFFIC_SOURCE
+    roof["kernel"] = "expert_mfma_kernel<%d>" % plan if mfma_bound else "expert_ring_kernel"
+    roof["kernel_ms"] = round(ms, 4)
+    roof["per_launch"] = {"flop": flops} if mfma_bound else {"bytes": nbytes}
+    return roof
+
+
+def measure_moe(name, w, x, steps, warmup, nsets):
+    """Times `steps` back-to-back forwards of workload `name` (weights w,
+    tokens x) cycling nsets device copies of the weights, then the same steps
+    with events around the router and expert launches."""
+    from final_amd import SparseMoeBlock, hip
+    from final_amd import workloads as W
+    T = x.shape[0]
+    blocks = []
+    for _ in range(nsets):
+        b = SparseMoeBlock(max_tokens=max(T, 64))
+        b.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+        blocks.append(b)
+    stream = hip.Stream()
+    dx = hip.DeviceArray.from_numpy(x)
+    dy = hip.DeviceArray((T, W.H))
+    plan = blocks[0].plan(T)
+    log(f"[bench] {name}: T={T} plan={plan} (0 = weight streaming, else MFMA tile rows), "
+        f"weight sets={nsets}")
+    for i in range(warmup):
+        blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream)
+    stream.synchronize()
+    blocks[0].check_device(stream)
+    start, stop = hip.Event(), hip.Event()
+    hip.synchronize()
+    t_wall = time.perf_counter()
+    start.record(stream)
+    for i in range(steps):
+        blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream)
+    stop.record(stream)
+    stop.synchronize()
+    wall = time.perf_counter() - t_wall
+    hip.synchronize()
+    total_ms = start.elapsed_ms(stop)
+    # the same steps with events around each launch, for the per-kernel times
+    # (events between launches add a few microseconds per step, so they stay
+    # out of the timed steps)
+    ev = [(hip.Event(), hip.Event(), hip.Event()) for _ in range(steps)]
+    for i in range(steps):
+        b = blocks[i % nsets]
+        e0, e1, e2 = ev[i]
+        e0.record(stream)
+        b.route(dx, T, stream=stream)
+        e1.record(stream)
+        b.experts(dx, dy, T, stream=stream)
+        e2.record(stream)
+    ev[-1][2].synchronize()
+    hip.synchronize()
+    route_ms = statistics.mean(e0.elapsed_ms(e1) for e0, e1, _ in ev)
+    exp_ms = statistics.mean(e1.elapsed_ms(e2) for _, e1, e2 in ev)
+    for b in blocks:
+        b.check_device(stream)
+    counts = blocks[0].last_routing()["counts"]
+    for b in blocks:
+        b.close()
+    ms_step = total_ms / steps
+    flops = T * (W.flops_per_token() - 2 * W.H * W.E)  # W1, W3, W2 of 4 slots per token
+    nbytes = W.algorithmic_bytes(counts, T) - (W.E * W.H * 4 + W.E * 4)
+    roof = roofline(plan, flops, nbytes, exp_ms, name)
+    roof["router_ms"] = round(route_ms, 4)
+    return {"workload": name, "tokens": T, "ms_per_step": round(ms_step, 4),
+            "tokens_per_s": round(T * steps / (total_ms / 1e3), 1), "steps": steps,
+            "plan_tile_rows": plan, "weight_sets": nsets,
+            "active_experts": int((counts > 0).sum()), "zero_token_experts": int((counts == 0).sum()),
+            "max_expert_tokens": int(counts.max()), "counts": [int(c) for c in counts],
+            "wall_s": round(wall, 4), "roofline": roof}
+
+
+def model_flops(batch, seq, layer_types, vocab=65536):
+    """Algorithmic FLOPs of one forward: every projection and expert GEMM
+    (2 per multiply-add), the causal attention products over the keys each
+    query sees, the gate, and the LM head on the last tokens."""
+    H, I, E, K, HD, NH, NKV = 2048, 1792, 32, 4, 64, 32, 8
+    T = batch * seq
+    moe = 2 * H * E + K * 3 * 2 * H * I
+    attn_proj = 2 * H * (NH + 2 * NKV) * HD + 2 * NH * HD * H
+    attn_core = batch * NH * (seq * (seq + 1) // 2) * HD * 2 * 2
+    conv = 2 * H * 3 * H + 2 * H * H
+    n_attn = sum(1 for t in layer_types if t == 0)
+    n_conv = len(layer_types) - n_attn
+    return (T * (len(layer_types) * moe + n_attn * attn_proj + n_conv * conv)
+            + n_attn * attn_core + batch * 2 * H * vocab)
+
+
+def measure_model(steps, warmup, batch=64, seq=512):
+    """The whole decoder forward on one GPU: 24 layers of the reference's
+    layer types, every FFN the MoE block (as the benchmark config specifies;
+    the reference's own model has dense FFNs in layers 0-1), synthetic
+    N(0, 0.02) weights drawn on the device, uniform random token ids."""
+    import numpy as np
+
+    from final_amd import hip, lfm
+    log(f"[bench] lfm2 model: batch={batch} seq={seq}: building 24 synthetic layers on the device")
+    t0 = time.perf_counter()
+    model = lfm.LFM2Model(num_layers=24, num_dense_layers=0, max_batch=batch, max_seq=seq, seed=0)
+    build_s = time.perf_counter() - t0
+    ids = np.random.default_rng(0).integers(0, lfm.VOCAB, (batch, seq)).astype(np.int32)
+    d_ids = hip.DeviceArray.from_numpy(ids)
+    logits = hip.DeviceArray((batch, lfm.VOCAB))
+    stream = hip.Stream()
+    for _ in range(warmup):
+        model.forward(d_ids, batch, seq, logits, stream=stream)
+    stream.synchronize()
+    start, stop = hip.Event(), hip.Event()
+    t_wall = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        model.forward(d_ids, batch, seq, logits, stream=stream)
+    stop.record(stream)
+    stop.synchronize()
+    wall = time.perf_counter() - t_wall
+    ms = start.elapsed_ms(stop) / steps
+    # one more forward in pieces with events between them: per-layer times
+    T = batch * seq
+    h = hip.DeviceArray((T, lfm.HIDDEN))
+    ev = [hip.Event() for _ in range(model.num_layers + 3)]
+    ev[0].record(stream)
+    model.embed(d_ids, batch, seq, h, stream=stream)
+    ev[1].record(stream)
+    for i in range(model.num_layers):
+        model.layer_forward(i, h, batch, seq, stream=stream)
+        ev[i + 2].record(stream)
+    model.head(h, batch, seq, logits, stream=stream)
+    ev[-1].record(stream)
+    ev[-1].synchronize()
+    per_layer = [ev[i + 1].elapsed_ms(ev[i + 2]) for i in range(model.num_layers)]
+    attn = [t for i, t in enumerate(per_layer) if model.is_attention(i)]
+    conv = [t for i, t in enumerate(per_layer) if not model.is_attention(i)]
+    status = model.status(stream)
+    if status != 0:
+        raise RuntimeError(f"model device status {status}")
+    lg = logits.download()
+    if not np.all(np.isfinite(lg)):
+        raise RuntimeError("non-finite logits")
+    model.close()
+    flops = model_flops(batch, seq, model.layer_types)
+    a = flops / (ms / 1e3) / 1e12
+    return {"workload": "lfm2_b64_s512", "tokens": T, "batch": batch, "seq_len": seq,
+            "layers": 24, "ms_per_step": round(ms, 3),
+            "tokens_per_s": round(T / (ms / 1e3), 1), "steps": steps, "warmup": warmup,
+            "wall_s": round(wall, 3), "build_s": round(build_s, 2),
+            "layer_ms": {"attention_avg": round(statistics.mean(attn), 3),
+                         "conv_avg": round(statistics.mean(conv), 3),
+                         "embed": round(ev[0].elapsed_ms(ev[1]), 3),
+                         "head": round(ev[-2].elapsed_ms(ev[-1]), 3)},
+            "roofline": {"bound": "mfma", "achieved": round(a, 3), "peak": PEAK_MFMA_F32_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(a / PEAK_MFMA_F32_TFLOPS, 4),
+                         "scope": "whole forward (every GEMM, attention and the MoE experts)",
+                         "per_launch": {"flop": flops}, "traffic": None},
+            "data": "synthetic (seeded N(0,0.02) weights on the device, RMSNorm weights 1, "
+                    "uniform random token ids)"}
 
 
 def bench_dense(args, wl):
@@ -157,7 +366,7 @@ def bench_dense(args, wl):
         "value": round(T * K / (ms_step * K / 1e3), 1), "unit": "tokens/s", "n_gpus": 1,
         "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) tokens)",
+        "data": DATA,
         "config": {"workload": wl.name, "tokens": T, "hidden": W.H, "inter": I,
                    "plan_tile_rows": plan, "weight_sets": nsets, "wall_s": round(wall, 4)},
         "roofline": roof, "cpu_baseline": None,
@@ -167,6 +376,12 @@ def bench_dense(args, wl):
     print(json.dumps(out), flush=True)
 
 
+def weight_sets_for(T, requested):
+    # a set's active experts for small T can sit in the 256 MB Infinity Cache;
+    # cycle copies so every step streams its weights from HBM
+    return requested if requested > 0 else (1 if T >= 512 else 4)
+
+
 def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -174,9 +389,7 @@ def main():
               "part of it (the design notes describe how the block would shard).", file=sys.stderr)
         sys.exit(2)
 
-    import numpy as np
-
-    from final_amd import SparseMoeBlock, hip
+    from final_amd import hip
     from final_amd import workloads as W
 
     if args.copy_calibration:
@@ -187,134 +400,65 @@ def main():
         hip.synchronize()
         print(json.dumps({"copy_calibration_bytes": n, "copies": 3}), flush=True)
         return
-
-    wl = W.WORKLOADS[args.workload]
-    T = wl.T
     if hip.device_count() < 1:
         raise RuntimeError("no HIP device visible")
+
+    threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+    if args.workload == "lfm2_b64_s512":
+        e = measure_model(args.model_steps, 1)
+        out = {"metric": "LFM2-style decoder forward tokens/sec (batch 64 x seq 512) fp32, 1 GPU",
+               "value": e["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+               "steps": args.model_steps, "warmup": 1, "ms_per_step": e["ms_per_step"],
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+               "data": e["data"], "config": {k: e[k] for k in ("workload", "tokens", "batch",
+                                                               "seq_len", "layers")},
+               "roofline": e["roofline"], "cpu_baseline": None, "detail": e}
+        print(json.dumps(out), flush=True)
+        return
+
+    wl = W.WORKLOADS[args.workload]
     if wl.kind == "dense":
         return bench_dense(args, wl)
-    log(f"[bench] workload={wl.name} T={T}: generating weights")
+    log(f"[bench] generating seed-{wl.seed} weights")
     w = W.gen_weights(wl.seed, bias=wl.bias)
-    x = W.gen_x(T, wl.seed)
-
-    nsets = args.weight_sets
-    if nsets <= 0:
-        # a set's active experts for small T can sit in the 256 MB Infinity
-        # Cache; cycle copies so every step streams its weights from HBM
-        nsets = 1 if T >= 512 else 4
-    blocks = []
-    for i in range(nsets):
-        b = SparseMoeBlock(max_tokens=max(T, 64))
-        b.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
-        blocks.append(b)
-    stream = hip.Stream()
-    dx = hip.DeviceArray.from_numpy(x)
-    dy = hip.DeviceArray((T, W.H))
-    plan = blocks[0].plan(T)
-    log(f"[bench] plan={plan} (0 = weight streaming, else MFMA tile rows), weight sets={nsets}")
-
-    for i in range(args.warmup):
-        blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream)
-    stream.synchronize()
-    blocks[0].check_device(stream)
-
-    K = args.steps
-    # timed steps: back-to-back forwards, nothing recorded between them
-    start, stop = hip.Event(), hip.Event()
-    hip.synchronize()
-    t_wall = time.perf_counter()
-    start.record(stream)
-    for i in range(K):
-        blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream)
-    stop.record(stream)
-    stop.synchronize()
-    wall = time.perf_counter() - t_wall
-    hip.synchronize()
-    total_ms = start.elapsed_ms(stop)
-    # then the same steps with events around each launch, for the per-kernel
-    # times of the roofline (events between launches add a few microseconds
-    # per step, so they stay out of the timed steps)
-    ev = [(hip.Event(), hip.Event(), hip.Event()) for _ in range(K)]
-    for i in range(K):
-        b = blocks[i % nsets]
-        e0, e1, e2 = ev[i]
-        e0.record(stream)
-        b.route(dx, T, stream=stream)
-        e1.record(stream)
-        b.experts(dx, dy, T, stream=stream)
-        e2.record(stream)
-    ev[-1][2].synchronize()
-    hip.synchronize()
-    route_ms = [e0.elapsed_ms(e1) for e0, e1, _ in ev]
-    exp_ms = [e1.elapsed_ms(e2) for _, e1, e2 in ev]
-    for b in blocks:
-        b.check_device(stream)
-    rt = blocks[0].last_routing()
-    counts = rt["counts"]
-
-    ms_step = total_ms / K
-    value = T * K / (total_ms / 1e3)
-    exp_avg = statistics.mean(exp_ms)
-    route_avg = statistics.mean(route_ms)
-    expert_flops = T * (W.flops_per_token() - 2 * W.H * W.E)  # W1, W3, W2 of 4 slots/token
-    expert_bytes = W.algorithmic_bytes(counts, T) - (W.E * W.H * 4 + W.E * 4)
-    mfma_bound = plan != 0
-    if mfma_bound:
-        achieved = expert_flops / (exp_avg / 1e3) / 1e12
-        roof = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_F32_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_F32_TFLOPS, 4)}
-    else:
-        achieved = expert_bytes / (exp_avg / 1e3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4)}
-    # near the ridge (fp32 MFMA peak / HBM peak = 19.7 FLOP/B) both bounds
-    # are close: report the other one beside the primary
-    ai = expert_flops / max(expert_bytes, 1)
-    ridge = PEAK_MFMA_F32_TFLOPS * 1e3 / PEAK_HBM_GBS
-    if 0.5 <= ai / ridge <= 2.0:
-        if mfma_bound:
-            other = expert_bytes / (exp_avg / 1e3) / 1e9
-            roof["secondary"] = {"bound": "hbm", "achieved": round(other, 1), "peak": PEAK_HBM_GBS,
-                                 "unit": "GB/s", "frac": round(other / PEAK_HBM_GBS, 4),
-                                 "per_launch": {"bytes": expert_bytes}}
-        else:
-            other = expert_flops / (exp_avg / 1e3) / 1e12
-            roof["secondary"] = {"bound": "mfma", "achieved": round(other, 3),
-                                 "peak": PEAK_MFMA_F32_TFLOPS, "unit": "TFLOP/s",
-                                 "frac": round(other / PEAK_MFMA_F32_TFLOPS, 4),
-                                 "per_launch": {"flop": expert_flops}}
-        roof["arithmetic_intensity"] = round(ai, 2)
-    roof["traffic"] = None
-    if os.path.exists(TRAFFIC_FILE):
-        with open(TRAFFIC_FILE) as f:
-            tr = json.load(f).get(wl.name)
-        if tr:
-            roof["traffic"] = tr.get("bytes_per_launch")
-    roof["kernel"] = "expert_mfma_kernel<%d>" % plan if mfma_bound else "expert_ring_kernel"
-    roof["kernel_ms"] = round(exp_avg, 4)
-    roof["router_ms"] = round(route_avg, 4)
-    roof["per_launch"] = ({"flop": expert_flops} if mfma_bound else {"bytes": expert_bytes})
-
+    x = W.gen_x(wl.T, wl.seed)
+    head = measure_moe(wl.name, w, x, args.steps, args.warmup,
+                       weight_sets_for(wl.T, args.weight_sets))
     out = {
-        "metric": METRIC, "value": round(value, 1), "unit": "tokens/s", "n_gpus": 1,
-        "steps": K, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "metric": METRIC, "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": head["ms_per_step"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-        "data": "synthetic (seeded N(0,0.02) weights, N(0,1) tokens)",
-        "config": {"workload": wl.name, "tokens": T, "hidden": W.H, "inter": W.I,
-                   "experts": W.E, "top_k": W.K, "plan_tile_rows": plan,
-                   "active_experts": int((counts > 0).sum()), "weight_sets": nsets,
-                   "wall_s": round(wall, 4)},
-        "roofline": roof,
+        "data": DATA,
+        "config": {"workload": wl.name, "tokens": wl.T, "hidden": W.H, "inter": W.I,
+                   "experts": W.E, "top_k": W.K, "plan_tile_rows": head["plan_tile_rows"],
+                   "active_experts": head["active_experts"], "weight_sets": head["weight_sets"],
+                   "wall_s": head["wall_s"]},
+        "roofline": head["roofline"],
     }
     if not args.no_cpu:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
         log(f"[bench] CPU oracle baseline, {threads} threads")
-        out["cpu_baseline"] = cpu_baseline(w, x, threads)
+        out["cpu_baseline"] = cpu_baseline(w, x, threads, min_s=10.0)
     else:
         out["cpu_baseline"] = None
-    for b in blocks:
-        b.close()
+
+    if not args.no_sweep:
+        sweep = {}
+        for name in SWEEP_MOE:
+            if name == wl.name:
+                continue
+            s = W.WORKLOADS[name]
+            ws = w if s.bias == wl.bias else dict(w, bias=W.zipf_bias() if s.bias == "zipf"
+                                                   else W.gen_weights(s.seed)["bias"])
+            xs = W.gen_x(s.T, s.seed)
+            e = measure_moe(name, ws, xs, args.steps, args.warmup,
+                            weight_sets_for(s.T, args.weight_sets))
+            if name == "decode_t64" and not args.no_cpu:
+                # the reference's CPU-runnable case (T=64): about 10 s of oracle work
+                log(f"[bench] CPU oracle baseline at T=64, {threads} threads")
+                e["cpu_baseline"] = cpu_baseline(ws, xs, threads, single_tokens=64, min_s=10.0)
+            sweep[name] = e
+        sweep["lfm2_b64_s512"] = measure_model(args.model_steps, 1)
+        out["sweep"] = sweep
     print(json.dumps(out), flush=True)
 
 
