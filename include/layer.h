@@ -229,7 +229,7 @@ public:
                    int seq_len, int hidden_size, hipStream_t stream);
 
   // The decoder layer's post-attention RMSNorm weight [H] (RMSNorm,
-  // layer.h:10-24, loaded as layers.{i}.ffn_norm.weight at layer.cu:1792).
+  // layer.h:10-24, loaded as layers.{i}.ffn_norm.weight at layer.cu:1790-1793).
   // After init_gpu.  The device-pointer form takes a device copy.
   void set_post_attention_norm(const Tensor &weight);
   void set_post_attention_norm_gpu(const float *weight);

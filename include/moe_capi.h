@@ -157,8 +157,8 @@ int moe_dense_forward(moe_ctx *ctx, const float *x, float *y, const float *resid
                       int num_tokens, moe_stream_t stream);
 
 /* The post-attention RMSNorm weight [hidden] of the decoder layer that owns
- * this block (RMSNorm post_attention_layernorm_, layer.cu:1793, weight
- * layers.{i}.post_attention_layernorm.weight; RMSNorm::init_gpu uploads it,
+ * this block (RMSNorm post_attention_layernorm_, layer.cu:1790-1793, weight
+ * layers.{i}.ffn_norm.weight; RMSNorm::init_gpu uploads it,
  * layer.cu:1128-1142).  Host memory when src_on_device == 0.  Allocates the
  * normalised-row scratch ([max_tokens][hidden]) on first use.  Synchronises
  * `stream`. */
