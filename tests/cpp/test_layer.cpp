@@ -20,7 +20,9 @@
 #include <vector>
 
 #include "layer.h"
+#include "model.h"
 #include "model_loader.h"
+#include "moe_synth.h"
 #include "tensor.h"
 
 extern "C" {
@@ -312,13 +314,116 @@ void gpu_tests() {
   CHECK(std::memcmp(wt.data(), wref.data(), wref.size() * 4) == 0);
 }
 
+// The block at the reference's shapes (hidden 2048, inter 1792), in-memory
+// weights: small batches reach the weight-streaming kernel.
+void gpu_full_shape_tests() {
+  constexpr int H = 2048, I = 1792;
+  std::vector<float> gate((size_t)kE * H), bias(kE), w1((size_t)kE * I * H), w3(w1.size()),
+      w2((size_t)kE * H * I);
+  moe_synth_normal(3, 0, 0.02f, 0, gate.data(), gate.size());
+  moe_synth_normal(3, 1, 0.02f, 0, bias.data(), bias.size());
+  moe_synth_normal(3, 2, 0.02f, 0, w1.data(), w1.size());
+  moe_synth_normal(3, 3, 0.02f, 0, w3.data(), w3.size());
+  moe_synth_normal(3, 4, 0.02f, 0, w2.data(), w2.size());
+  std::vector<MLP> experts;
+  for (int e = 0; e < kE; ++e)
+    experts.emplace_back(Tensor({(size_t)I, (size_t)H}, w1.data() + (size_t)e * I * H, true),
+                         Tensor({(size_t)H, (size_t)I}, w2.data() + (size_t)e * H * I, true),
+                         Tensor({(size_t)I, (size_t)H}, w3.data() + (size_t)e * I * H, true));
+  SparseMoeBlock blk(kLayer, Tensor({(size_t)kE, (size_t)H}, gate.data(), true), std::move(experts),
+                     Tensor({(size_t)kE}, bias.data(), true));
+  blk.set_max_tokens(256);
+  blk.init_gpu();
+  CHECK(moe_plan_tile_rows(blk.context(), 8) == 0 && moe_plan_tile_rows(blk.context(), 64) == 0);
+  for (int T : {8, 64, 200}) {
+    std::vector<float> x((size_t)T * H), yref((size_t)T * H);
+    moe_synth_normal(3, 99, 1.0f, 0, x.data(), x.size());
+    std::vector<int> iref((size_t)T * 4), cref(kE);
+    CHECK(orc_moe_forward(x.data(), gate.data(), bias.data(), w1.data(), w3.data(), w2.data(),
+                          nullptr, T, H, I, kE, nullptr, yref.data(), nullptr, iref.data(),
+                          nullptr, cref.data()) == 0);
+    Tensor tx({(size_t)T, (size_t)H}, x.data(), true), ty, tl;
+    blk.forward(tx, ty, tl);
+    std::vector<int> idx((size_t)T * 4), cnt(kE);
+    CHECK(moe_last_routing(blk.context(), idx.data(), nullptr, cnt.data(), nullptr, T, nullptr) == 0);
+    CHECK(idx == iref && cnt == cref);
+    int bad = 0;
+    for (size_t i = 0; i < yref.size(); ++i) bad += !close(ty.data()[i], yref[i]);
+    CHECK(bad == 0);
+    std::printf("gpu full-shape T=%d plan=%d ok\n", T, moe_plan_tile_rows(blk.context(), T));
+  }
+}
+
+// The model through the reference's own entry points: LFM2Model::forward
+// (sample_idx, batch, host ids, seq_len, host logits) + sync() equals the
+// device-pointer forward bit for bit; DecoderLayer::forward on host tensors
+// equals forward_gpu.
+void gpu_model_tests() {
+  LFM2Config cfg;
+  cfg.num_layers = 2;
+  cfg.layer_types = {1, 0};
+  cfg.num_dense_layers = 1;  // one dense FFN, one MoE block
+  cfg.max_batch = 2;
+  cfg.max_seq = 40;
+  SyntheticWeights s;
+  s.seed = 5;
+  LFM2Model model(cfg, s);
+  const int B = 2, S = 40, V = model.vocab();
+  std::vector<int> ids((size_t)B * S);
+  for (size_t i = 0; i < ids.size(); ++i) ids[i] = (int)((i * 2654435761u) % (unsigned)V);
+  std::vector<float> logits((size_t)B * V);
+  model.forward(0, B, ids.data(), S, logits.data());
+  model.sync();
+  int *dids = nullptr;
+  float *dlog = nullptr;
+  CHECK(hipMalloc(&dids, ids.size() * 4) == hipSuccess && hipMalloc(&dlog, logits.size() * 4) == hipSuccess);
+  CHECK(hipMemcpy(dids, ids.data(), ids.size() * 4, hipMemcpyHostToDevice) == hipSuccess);
+  model.forward_gpu(dids, B, S, dlog, nullptr);
+  std::vector<float> l2(logits.size());
+  CHECK(hipDeviceSynchronize() == hipSuccess);
+  CHECK(hipMemcpy(l2.data(), dlog, l2.size() * 4, hipMemcpyDeviceToHost) == hipSuccess);
+  CHECK(std::memcmp(l2.data(), logits.data(), l2.size() * 4) == 0);
+  bool finite = true;
+  for (float v : logits) finite = finite && std::isfinite(v);
+  CHECK(finite);
+  CHECK(model.status(nullptr) == MOE_OK);
+  CHECK(throws([&] { model.forward(0, 3, ids.data(), S, logits.data()); }));  // beyond max_batch
+  // DecoderLayer on host tensors vs on device buffers (attention layer 1)
+  DecoderLayer &layer = model.layer(1);
+  const size_t n = (size_t)S * HIDDEN_SIZE;
+  std::vector<float> h(n);
+  moe_synth_normal(5, 7, 1.0f, 0, h.data(), n);
+  RotaryEmbedding rope((size_t)S);
+  Tensor c, sn;
+  rope.forward(S, c, sn);
+  Tensor th({(size_t)S, HIDDEN_SIZE}, h.data(), true), tout;
+  layer.forward(th, c, sn, nullptr, tout);
+  rope.init_gpu();
+  float *dh = nullptr;
+  CHECK(hipMalloc(&dh, n * 4) == hipSuccess);
+  CHECK(hipMemcpy(dh, h.data(), n * 4, hipMemcpyHostToDevice) == hipSuccess);
+  layer.forward_gpu(dh, rope.cos_gpu_, rope.sin_gpu_, dh, 1, S, (int)HIDDEN_SIZE, nullptr);
+  std::vector<float> hd(n);
+  CHECK(hipDeviceSynchronize() == hipSuccess);
+  CHECK(hipMemcpy(hd.data(), dh, n * 4, hipMemcpyDeviceToHost) == hipSuccess);
+  CHECK(std::memcmp(hd.data(), tout.data(), n * 4) == 0);
+  (void)hipFree(dids);
+  (void)hipFree(dlog);
+  (void)hipFree(dh);
+  std::printf("gpu model ok\n");
+}
+
 }  // namespace
 
 int main(int argc, char **argv) {
   const std::string mode = argc > 1 ? argv[1] : "cpu";
   try {
     if (mode == "cpu") cpu_tests();
-    else if (mode == "gpu") gpu_tests();
+    else if (mode == "gpu") {
+      gpu_tests();
+      gpu_full_shape_tests();
+      gpu_model_tests();
+    }
     else {
       std::fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
       return 2;

@@ -566,3 +566,100 @@ def test_dense_mlp_is_chained_gemms(oracle_mod):
                       for gr, ur in zip(gate, up)], np.float32)
     want = oracle_mod.gemm_nt_chain(inter, w2)
     assert np.array_equal(bits(oracle_mod.dense_mlp(x, w1, w3, w2)), bits(want))
+
+
+# ---------------------------------------------------------------------------
+# Exact rounding sequences of the activations, from decimal arithmetic
+# ---------------------------------------------------------------------------
+
+def _dec_exp_to_double(v: float) -> float:
+    """exp(v) correctly rounded to double, from 60-digit decimal arithmetic
+    (independent of the host's libm)."""
+    import decimal
+    with decimal.localcontext() as c:
+        c.prec = 60
+        return float(decimal.Decimal(v).exp())  # Decimal -> float rounds to nearest
+
+
+def _dec_exp_to_float(v: float) -> np.float32:
+    """exp(v) correctly rounded to float (one rounding from the exact value)."""
+    import decimal
+    with decimal.localcontext() as c:
+        c.prec = 60
+        e = decimal.Decimal(v).exp()
+        # past the largest float plus half its ulp the nearest float is inf
+        if e >= decimal.Decimal(float(np.finfo(np.float32).max)) + decimal.Decimal(2.0 ** 103):
+            return np.float32(np.inf)
+        # nearest float: round the exact value via the two float neighbours of
+        # its double approximation (60 digits decide every tie)
+        f = np.float32(float(e))
+        lo, hi = sorted((f, np.nextafter(f, np.float32(np.inf) if decimal.Decimal(float(f)) < e
+                                          else np.float32(-np.inf))))
+        dlo, dhi = e - decimal.Decimal(float(lo)), decimal.Decimal(float(hi)) - e
+        if dlo < dhi:
+            return lo
+        if dhi < dlo:
+            return hi
+        return lo if (lo.view(np.uint32) & 1) == 0 else hi
+
+
+def _sweep():
+    xs = np.concatenate([np.linspace(-30, 30, 6001), np.linspace(-2, 2, 4001),
+                         [0.0, 1e-30, -1e-30, 1e-7, -1e-7, 88.0, -88.0, 103.0, -103.0]])
+    return np.unique(xs.astype(np.float32))
+
+
+def test_sigmoid_is_the_double_exp_sequence(oracle_mod):
+    """d_sigmoid (layer.cu:435): e = (float)exp(-(double)x) (exp correctly
+    rounded to double, then to float), then 1.0f + e and 1.0f / that, each
+    rounded to float.  Bit-equal over a dense sweep.  The sweep separates this
+    three-rounding sequence from a sigmoid evaluated in double and rounded
+    once (which differs at thousands of points).  A correctly rounded expf in
+    place of the double exp gives the same e except where the double result
+    sits within half a double ulp of a float rounding boundary, which no point
+    of the sweep hits: that choice is bounded (at most one float ulp in e on
+    such a point) rather than pinned."""
+    one = np.float32(1.0)
+    d_one = 0
+    for x in _sweep():
+        e = np.float32(_dec_exp_to_double(-float(x)))
+        ref = one / (one + e)
+        got = np.float32(oracle_mod.sigmoid(float(x)))
+        assert got.view(np.uint32) == ref.view(np.uint32), (x, got, ref)
+        alt1 = np.float32(1.0 / (1.0 + _dec_exp_to_double(-float(x))))  # one rounding
+        d_one += alt1.view(np.uint32) != ref.view(np.uint32)
+    assert d_one > 100, d_one
+
+
+def test_silu_dexp_is_the_double_exp_sequence(oracle_mod):
+    """d_silu (layer.cu:436): x / (1.0f + (float)exp(-(double)x)), bit-equal."""
+    one = np.float32(1.0)
+    for x in _sweep():
+        e = np.float32(_dec_exp_to_double(-float(x)))
+        ref = x / (one + e)
+        got = np.float32(oracle_mod.silu_dexp(float(x)))
+        assert got.view(np.uint32) == ref.view(np.uint32), (x, got, ref)
+
+
+def test_silu_is_the_expf_sequence(oracle_mod):
+    """d_silu_opt (layer.cu:728): x / (1.0f + expf(-x)) with expf rounded
+    once to float.  The host's expf is a library routine: it must agree with
+    the correctly rounded exp on all but a few last-bit ties of the sweep, and
+    wherever it does the rest of the sequence is bit-equal.  The sweep
+    separates it from x * sigmoid(x) and from silu evaluated in double and
+    rounded once (each differs at many points)."""
+    one = np.float32(1.0)
+    n = miss = d_mul = d_one = 0
+    for x in _sweep():
+        e = _dec_exp_to_float(-float(x))
+        ref = x / (one + e)
+        got = np.float32(oracle_mod.silu(float(x)))
+        n += 1
+        if got.view(np.uint32) != ref.view(np.uint32):
+            miss += 1
+            assert abs(float(got) - float(ref)) <= 2 * float(np.spacing(np.abs(ref))), (x, got, ref)
+        d_mul += (x * (one / (one + e))).view(np.uint32) != ref.view(np.uint32)
+        alt1 = np.float32(float(x) / (1.0 + _dec_exp_to_double(-float(x))))
+        d_one += alt1.view(np.uint32) != ref.view(np.uint32)
+    assert miss <= n // 1000, (miss, n)
+    assert d_mul > 100 and d_one > 100, (d_mul, d_one)

@@ -1,0 +1,197 @@
+"""A CPU model of the expert kernels' task-claim and dependency-wait protocol,
+explored exhaustively on small instances under every interleaving of the
+blocks and with only some blocks resident (another kernel holding CUs).
+
+What is modelled (final_amd/csrc/moe_kernels.hip):
+
+* Tasks are numbered in the order the queue counter hands them out.  A task
+  may wait only for tasks of smaller number: gate/up tiles for the dispatch
+  tasks, down tiles / down row tasks for their unit's or expert's gate/up
+  tasks, the ring kernel's combine tasks for their token's down tasks.
+* expert_mfma_kernel: a block claims its first task as it starts, then per
+  task waits for the task's inputs (block_wait), computes, claims its next
+  task after the MFMAs and finishes the epilogue (which never waits).
+* expert_ring_kernel: a block claims its first task as it starts; streaming
+  wave 0 claims the next one at an early step of the current task, which may
+  come before or after the current task's wait for its inputs (the model
+  allows both orders); after the row tasks a block runs the combine tasks
+  dealt to it round-robin (block b: tokens b, b+G, ...).
+* Residency: of G blocks only R run at once; block b starts when a running
+  block exits, in index order.
+
+The model explores every interleaving (memoised depth-first search) and
+reports a reachable state in which tasks remain and no block can move.  Both
+kernels' protocols are shown free of such states; two variants are shown to
+reach one, which is what proves the model can see a deadlock: a first task
+given statically by block index (the ring kernel before its first claim came
+from the queue: a non-resident block then owns a gate/up task that running
+down tasks wait for), and a block that waits for its next task's inputs
+before finishing its current one (the shape of a removed ring-kernel variant
+that parked down tasks until their expert's values had landed and ended in a
+device-side wait timeout: its block could hold the gate/up task that its own
+next down task needed).
+"""
+from __future__ import annotations
+
+import sys
+from dataclasses import dataclass
+
+import pytest
+
+sys.setrecursionlimit(100000)
+
+
+@dataclass(frozen=True)
+class Plan:
+    deps: tuple            # deps[t]: frozenset of tasks t waits for (all < t)
+    n_row: int             # tasks handed out by the queue
+    combine_deps: tuple    # ring kernel: per token, the tasks its combine waits for
+
+
+def mfma_plan(n_dispatch=2, units=2, p1=2, p2=2):
+    deps = [frozenset()] * n_dispatch
+    g0 = n_dispatch
+    for u in range(units):
+        deps += [frozenset(range(n_dispatch))] * p1
+    for u in range(units):
+        deps += [frozenset(range(g0 + u * p1, g0 + (u + 1) * p1))] * p2
+    return Plan(tuple(deps), len(deps), ())
+
+
+def ring_plan(experts=2, p1=2, p2=2, tokens=((0, 1), (1,))):
+    deps = []
+    for e in range(experts):
+        deps += [frozenset()] * p1
+    d0 = experts * p1
+    for e in range(experts):
+        deps += [frozenset(range(e * p1, (e + 1) * p1))] * p2
+    comb = tuple(frozenset(t for e in tok for t in range(d0 + e * p2, d0 + (e + 1) * p2))
+                 for tok in tokens)
+    return Plan(tuple(deps), len(deps), comb)
+
+
+# block state: (status, cur, nxt, flags, comb_i)
+#   status 0 waiting to start, 1 running, 2 exited
+#   flags: bit 0 = current task's inputs awaited, bit 1 = next task claimed
+PENDING, RUNNING, EXITED = 0, 1, 2
+
+
+def explore(plan: Plan, kind: str, G: int, R: int, first="queue", park=False):
+    """Returns None if every interleaving finishes, else a description of a
+    reachable stuck state."""
+    n = plan.n_row
+    ncomb = len(plan.combine_deps)
+    seen = set()
+
+    def done_set(done_mask, t):
+        return (done_mask >> t) & 1
+
+    def deps_done(done_mask, deps):
+        return all(done_set(done_mask, d) for d in deps)
+
+    def moves(state):
+        head, done, blocks = state
+        running = sum(1 for b in blocks if b[0] == RUNNING)
+        out = []
+        for i, (st, cur, nxt, fl, ci) in enumerate(blocks):
+            if st == PENDING:
+                # start in index order when a slot is free
+                if running < R and all(b[0] != PENDING for b in blocks[:i]):
+                    if first == "static":
+                        t = i if i < n else n
+                        h = head
+                    else:
+                        t, h = (head, head + 1) if head < n else (n, head)
+                    nb = list(blocks)
+                    nb[i] = (RUNNING, t, -1, 0, 0)
+                    out.append((h, done, tuple(nb)))
+                continue
+            if st != RUNNING:
+                continue
+            if cur < n:
+                awaited, claimed = fl & 1, fl & 2
+                # wait for the current task's inputs
+                if not awaited and deps_done(done, plan.deps[cur]):
+                    nb = list(blocks)
+                    nb[i] = (st, cur, nxt, fl | 1, ci)
+                    out.append((head, done, tuple(nb)))
+                # claim the next task: the ring kernel at an early step (before
+                # or after the wait), the MFMA kernel after the MFMAs
+                if not claimed and (kind == "ring" or awaited):
+                    if first == "static" and head < G:
+                        h = max(head, G)  # static first tasks 0..G-1; the queue starts at G
+                    else:
+                        h = head
+                    t, h = (h, h + 1) if h < n else (n, h)
+                    nb = list(blocks)
+                    nb[i] = (st, cur, t, fl | 2, ci)
+                    out.append((h, done, tuple(nb)))
+                # finish the current task (park: only once the next task's
+                # inputs are there too)
+                if awaited and claimed and (not park or nxt >= n or deps_done(done, plan.deps[nxt])):
+                    nb = list(blocks)
+                    nb[i] = (st, nxt, -1, 0, ci)
+                    out.append((head, done | (1 << cur), tuple(nb)))
+                continue
+            # row tasks exhausted: the ring kernel's combine tasks for this block
+            tok = i + ci * G
+            if kind == "ring" and tok < ncomb:
+                if deps_done(done, plan.combine_deps[tok]):
+                    nb = list(blocks)
+                    nb[i] = (st, cur, nxt, fl, ci + 1)
+                    out.append((head, done, tuple(nb)))
+                continue
+            nb = list(blocks)
+            nb[i] = (EXITED, cur, nxt, fl, ci)
+            out.append((head, done, tuple(nb)))
+        return out
+
+    start = (0, 0, tuple((PENDING, -1, -1, 0, 0) for _ in range(G)))
+    if first == "static":
+        start = (0, 0, start[2])
+    stack = [start]
+    while stack:
+        s = stack.pop()
+        if s in seen:
+            continue
+        seen.add(s)
+        nxt_states = moves(s)
+        if not nxt_states:
+            head, done, blocks = s
+            if not all(b[0] == EXITED for b in blocks):
+                return f"stuck: done={bin(done)} blocks={blocks}"
+        stack.extend(nxt_states)
+    return None
+
+
+CASES = [(G, R) for G in (1, 2, 3) for R in range(1, G + 1)]
+
+
+@pytest.mark.parametrize("G,R", CASES)
+def test_mfma_kernel_protocol_never_sticks(G, R):
+    assert explore(mfma_plan(), "mfma", G, R) is None
+    assert explore(mfma_plan(n_dispatch=1, units=3, p1=1, p2=2), "mfma", G, R) is None
+
+
+@pytest.mark.parametrize("G,R", CASES)
+def test_ring_kernel_protocol_never_sticks(G, R):
+    assert explore(ring_plan(), "ring", G, R) is None
+    assert explore(ring_plan(experts=3, p1=1, p2=1, tokens=((0, 2), (1,), (2, 1))), "ring",
+                   G, R) is None
+
+
+def test_static_first_task_sticks_with_partial_residency():
+    # with every block resident it finishes ...
+    assert explore(ring_plan(experts=1, p1=2, p2=1, tokens=()), "ring", 2, 2, first="static") is None
+    # ... but a non-resident block 1 owns gate/up task 1, which the running
+    # block's down task waits for
+    r = explore(ring_plan(experts=1, p1=2, p2=1, tokens=()), "ring", 2, 1, first="static")
+    assert r is not None and "stuck" in r
+
+
+def test_parking_on_the_next_task_sticks():
+    # one block, one expert: it holds gate/up task 0 while its next task, the
+    # expert's down task, needs task 0 finished
+    r = explore(ring_plan(experts=1, p1=1, p2=1, tokens=()), "ring", 1, 1, park=True)
+    assert r is not None and "stuck" in r
+    assert explore(ring_plan(experts=1, p1=1, p2=1, tokens=()), "ring", 1, 1) is None
