@@ -132,6 +132,65 @@ __device__ __forceinline__ float norm_rms(float total, int H) {
   return 1.0f / sqrtf(total / (float)H + kNormEps);
 }
 
+// dst_m = rmsnorm(src_m) * w for NR rows of dim floats (row m valid when
+// m < nrows), 256 threads.  Thread t holds row elements t, t+256, ... in
+// registers (up to kNormRegs per row, so every load is in flight before the
+// first FMA) and sums their squares in that order; rows longer than
+// 256 * kNormRegs are read in a loop instead.  s_grp [NR][kNormGroups],
+// s_tot [NR]: LDS scratch.  dst may alias src.
+constexpr int kNormRegs = 8;
+
+template <int NR>
+__device__ __forceinline__ void norm_rows(const float *const (&src)[NR], float *const (&dst)[NR],
+                                          int nrows, const float *w, int dim, float *s_grp,
+                                          float *s_tot) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  float part[NR];
+  if (dim <= kNormThreads * kNormRegs) {
+    float v[NR][kNormRegs];
+#pragma unroll
+    for (int m = 0; m < NR; ++m)
+#pragma unroll
+      for (int j = 0; j < kNormRegs; ++j) {
+        const int i = tid + j * kNormThreads;
+        v[m][j] = (m < nrows && i < dim) ? src[m][i] : 0.0f;
+      }
+#pragma unroll
+    for (int m = 0; m < NR; ++m) {
+      part[m] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < kNormRegs; ++j)
+        if (tid + j * kNormThreads < dim) part[m] = __builtin_fmaf(v[m][j], v[m][j], part[m]);
+    }
+    norm_totals<NR>(part, s_grp, s_tot);
+#pragma unroll
+    for (int m = 0; m < NR; ++m) {
+      if (m >= nrows) break;
+      const float rms = norm_rms(s_tot[m], dim);
+#pragma unroll
+      for (int j = 0; j < kNormRegs; ++j) {
+        const int i = tid + j * kNormThreads;
+        if (i < dim) dst[m][i] = (v[m][j] * rms) * w[i];
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int m = 0; m < NR; ++m) {
+    part[m] = 0.0f;
+    if (m < nrows)
+      for (int i = tid; i < dim; i += kNormThreads) part[m] = __builtin_fmaf(src[m][i], src[m][i], part[m]);
+  }
+  norm_totals<NR>(part, s_grp, s_tot);
+#pragma unroll
+  for (int m = 0; m < NR; ++m) {
+    if (m >= nrows) break;
+    const float rms = norm_rms(s_tot[m], dim);
+    for (int i = tid; i < dim; i += kNormThreads) dst[m][i] = (src[m][i] * rms) * w[i];
+  }
+}
+
 // layer.cu:728 d_silu_opt.
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + expf(-v)); }
 

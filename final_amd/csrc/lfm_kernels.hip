@@ -125,18 +125,21 @@ __global__ __launch_bounds__(256) void embed_kernel(const int *ids, const float 
 // the reduction order is moe::norm_totals')
 // ---------------------------------------------------------------------------
 
+constexpr int kNormRows = 4;  // rows per block (their loads in flight together)
+
 __global__ __launch_bounds__(moe::kNormThreads) void rmsnorm_rows_kernel(
-    const float *x, long long xs, const float *w, float *y, long long ys, int dim) {
-#pragma clang fp contract(off)
-  __shared__ float s_grp[moe::kNormGroups], s_tot[1];
-  const float *src = x + (long long)blockIdx.x * xs;
-  float *dst = y + (long long)blockIdx.x * ys;
-  float part[1] = {0.0f};
-  for (int i = threadIdx.x; i < dim; i += moe::kNormThreads)
-    part[0] = __builtin_fmaf(src[i], src[i], part[0]);
-  moe::norm_totals<1>(part, s_grp, s_tot);
-  const float rms = moe::norm_rms(s_tot[0], dim);
-  for (int i = threadIdx.x; i < dim; i += moe::kNormThreads) dst[i] = (src[i] * rms) * w[i];
+    const float *x, long long xs, const float *w, float *y, long long ys, int rows, int dim) {
+  __shared__ float s_grp[kNormRows * moe::kNormGroups], s_tot[kNormRows];
+  const int r0 = blockIdx.x * kNormRows;
+  const float *src[kNormRows];
+  float *dst[kNormRows];
+#pragma unroll
+  for (int m = 0; m < kNormRows; ++m) {
+    const long long r = min(r0 + m, rows - 1);
+    src[m] = x + r * xs;
+    dst[m] = y + r * ys;
+  }
+  moe::norm_rows<kNormRows>(src, dst, min(kNormRows, rows - r0), w, dim, s_grp, s_tot);
 }
 
 // ---------------------------------------------------------------------------
@@ -153,6 +156,8 @@ constexpr int kHeadDim = 64;
 // 217-228) for position s = t % seq: out[d] = q1*c1 - q2*s1,
 // out[d+32] = q2*c2 + q1*s2 with q1 = x[d], q2 = x[d+32]; nvcc's contraction of
 // each line is restated as fmaf(first product, -/+ second product).
+constexpr int kRopeRows = 4;  // rows per wave (their loads in flight together)
+
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(float *qkv, int ld, const float *qw,
                                                            const float *kw, const float *cos_t,
                                                            const float *sin_t, long long nrows,
@@ -160,84 +165,102 @@ __global__ __launch_bounds__(256) void qk_norm_rope_kernel(float *qkv, int ld, c
                                                            int k_col) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
-  const long long row = (long long)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (row >= nrows) return;  // whole waves
-  const long long t = row / per_tok;
-  const int hd = (int)(row - t * per_tok);
-  const bool is_q = hd < heads;
-  float *p = qkv + t * ld + (is_q ? hd * kHeadDim : k_col + (hd - heads) * kHeadDim);
-  const float x = p[lane];
-  float v = x * x;
+  const long long row0 = ((long long)blockIdx.x * 4 + (threadIdx.x >> 6)) * kRopeRows;
+  float *p[kRopeRows];
+  float x[kRopeRows], wv[kRopeRows];
+  int pos[kRopeRows];
 #pragma unroll
-  for (int off = 16; off > 0; off >>= 1) v += __shfl_down(v, off, 32);
-  const float total = __shfl(v, 0) + __shfl(v, 32);
-  const float rms = 1.0f / sqrtf(total / (float)kHeadDim + moe::kNormEps);
-  const float y = (x * rms) * (is_q ? qw : kw)[lane];
-  const int s = (int)(t % seq);
-  const float c = cos_t[s * kHeadDim + lane], sn = sin_t[s * kHeadDim + lane];
-  const float other = __shfl_xor(y, 32);
-  p[lane] = lane < 32 ? __builtin_fmaf(y, c, -(other * sn)) : __builtin_fmaf(y, c, other * sn);
+  for (int m = 0; m < kRopeRows; ++m) {
+    const long long row = min(row0 + m, nrows - 1);  // a wave past the end redoes the last row
+    const long long t = row / per_tok;
+    const int hd = (int)(row - t * per_tok);
+    const bool is_q = hd < heads;
+    p[m] = qkv + t * ld + (is_q ? hd * kHeadDim : k_col + (hd - heads) * kHeadDim);
+    pos[m] = (int)(t % seq);
+    x[m] = p[m][lane];
+    wv[m] = (is_q ? qw : kw)[lane];
+  }
+  if (row0 >= nrows) return;  // whole waves
+#pragma unroll
+  for (int m = 0; m < kRopeRows; ++m) {
+    float v = x[m] * x[m];
+#pragma unroll
+    for (int off = 16; off > 0; off >>= 1) v += __shfl_down(v, off, 32);
+    const float total = __shfl(v, 0) + __shfl(v, 32);
+    const float rms = 1.0f / sqrtf(total / (float)kHeadDim + moe::kNormEps);
+    const float y = (x[m] * rms) * wv[m];
+    const float c = cos_t[pos[m] * kHeadDim + lane], sn = sin_t[pos[m] * kHeadDim + lane];
+    const float other = __shfl_xor(y, 32);
+    const float o = lane < 32 ? __builtin_fmaf(y, c, -(other * sn)) : __builtin_fmaf(y, c, other * sn);
+    if (row0 + m < nrows) p[m][lane] = o;
+  }
 }
 
 // ---------------------------------------------------------------------------
 // Causal GQA attention, head_dim 64
 // ---------------------------------------------------------------------------
 //
-// Block = (sequence b, kv head g, 16 consecutive queries); wave w serves q
-// head g*4 + w for those queries, so the four heads of a group share every
-// K/V tile staged in LDS.  Keys are taken 64 at a time.  Both products run on
-// v_mfma_f32_16x16x4_f32 in transposed form, S^T = K Q^T and O^T = V^T P^T, so
-// that a lane's query is always l % 16: the softmax statistics of a query
+// Block = (sequence b, kv head g, 32 consecutive queries), 8 waves: wave w
+// serves q head g*4 + (w & 3) for the 16 queries q0 + 16*(w >> 2), so the
+// eight waves share every 64-key K/V tile staged in LDS (the four heads of a
+// group and both query halves).  Both products run on
+// v_mfma_f32_16x16x4_f32 in transposed form, S^T = K Q^T and O^T = V^T P^T,
+// so that a lane's query is always l % 16: the softmax statistics of a query
 // live in its four lanes (l % 16 equal), P goes from the S^T result registers
 // straight into the B operand of O^T (the reduction index k of both MFMAs is
-// permuted the same way in A and B), and nothing is transposed through LDS
-// except V once per tile.  Online softmax in fp32 (running max per query,
-// partial sums per lane folded at the end); scores are scaled by 1/8 through
-// q (exact: a power of two).  Masked scores are -1e30 as in the reference
-// (layer.cu:316-318), so exp gives exactly 0.
-constexpr int kAttnQ = 16;
-constexpr int kAttnKT = 64;
-constexpr int kAttnPitch = 68;  // floats per LDS row (K tile [key][d], V tile [d][key])
+// permuted the same way in A and B), and nothing is transposed.  Online
+// softmax in fp32 with base-2 exponentials: q is scaled by log2(e)/8, so a
+// score is log2 of the unnormalised weight and v_exp_f32 gives it directly
+// (the 1/8 is exact, log2(e) adds one rounding per q element).  Masked
+// scores are -1e30 as in the reference (layer.cu:316-318), so exp2 gives 0.
+constexpr int kAttnQW = 16;             // queries per wave
+constexpr int kAttnQB = 2 * kAttnQW;    // queries per block
+constexpr int kAttnThreads = 512;
+constexpr int kAttnKT = 64;             // keys per tile
+constexpr int kAttnPitch = 68;          // floats per LDS row of the K and V tiles [key][d]
+constexpr float kLog2e = 1.44269504088896340736f;
 
-typedef float f32x4v __attribute__((ext_vector_type(4)));
-
-__global__ __launch_bounds__(256) void attention_kernel(const float *qkv, int ld, float *out,
-                                                        int ldo, int seq, int kv_heads,
-                                                        int group, int qgroups, int k_col,
-                                                        int v_col) {
+__global__ __launch_bounds__(kAttnThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void attention_kernel(const float *qkv, int ld, float *out, int ldo, int seq, int kv_heads,
+                      int group, int qblocks, int k_col, int v_col) {
   __shared__ float Ks[kAttnKT * kAttnPitch];
-  __shared__ float Vt[kHeadDim * kAttnPitch];
+  __shared__ float Vs[kAttnKT * kAttnPitch];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int bid = blockIdx.x;
-  const int qg = qgroups - 1 - bid % qgroups;  // the longer rows of a sequence first
-  const int rest = bid / qgroups;
+  const int qb = qblocks - 1 - bid % qblocks;  // the longer rows of a sequence first
+  const int rest = bid / qblocks;
   const int g = rest % kv_heads, b = rest / kv_heads;
-  const int h = g * group + wave;
-  const int q0 = qg * kAttnQ;
+  const int h = g * group + (wave & 3);
+  const int q0b = qb * kAttnQB;
+  const int q0 = q0b + kAttnQW * (wave >> 2);
   const size_t tok0 = (size_t)b * seq;
   const int ql = lane & 15, kq = lane >> 4;
   const int q = q0 + ql;
   const bool qvalid = q < seq;
   const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 
-  // B operand of S^T: lane (ql, kq) holds q[16a + 4kq + j] / 8, a, j = 0..3
+  // B operand of S^T: lane (ql, kq) holds q[16a + 4kq + j] * log2(e) / 8
   f32x4 qv[4];
+  const float qscale = 0.125f * kLog2e;
 #pragma unroll
   for (int a = 0; a < 4; ++a)
-    qv[a] = qvalid ? moe::ld4(qkv + (tok0 + q) * ld + h * kHeadDim + 16 * a + 4 * kq) * 0.125f : zero;
+    qv[a] = qvalid ? moe::ld4(qkv + (tok0 + q) * ld + h * kHeadDim + 16 * a + 4 * kq) * qscale : zero;
 
-  const int kend = min(seq, q0 + kAttnQ);
+  // keys [0, kend) serve the block; the last tile starts at or before q0b,
+  // so no valid query sees a tile with every key masked
+  const int kend = min(seq, q0b + kAttnQB);
   const int ntiles = (kend + kAttnKT - 1) / kAttnKT;
   float m = -1e30f, l = 0.0f;
   f32x4 o[4] = {zero, zero, zero, zero};
 
-  // staging: thread tid moves key rows tid/16 + 16i, float4 column (tid%16)*4
+  // staging: thread tid moves rows tid/16 and tid/16 + 32 of K and V, float4
+  // column (tid%16)*4
   const int srow = tid >> 4, scol = (tid & 15) * 4;
-  f32x4 kreg[4], vreg[4];
+  f32x4 kreg[2], vreg[2];
   auto gload = [&](int kt) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int kr = kt * kAttnKT + srow + 16 * i;
+    for (int i = 0; i < 2; ++i) {
+      const int kr = kt * kAttnKT + srow + 32 * i;
       const bool ok = kr < kend;
       const float *rowp = qkv + (tok0 + (ok ? kr : 0)) * ld;
       kreg[i] = ok ? moe::ld4(rowp + k_col + g * kHeadDim + scol) : zero;
@@ -248,17 +271,16 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *qkv, int ld
   for (int kt = 0; kt < ntiles; ++kt) {
     __syncthreads();  // the previous tile's readers are done
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = srow + 16 * i;
+    for (int i = 0; i < 2; ++i) {
+      const int r = srow + 32 * i;
       moe::st4(Ks + r * kAttnPitch + scol, kreg[i]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) Vt[(scol + j) * kAttnPitch + r] = vreg[i][j];
+      moe::st4(Vs + r * kAttnPitch + scol, vreg[i]);
     }
     __syncthreads();
     if (kt + 1 < ntiles) gload(kt + 1);
 
     // S^T blocks: s[kb] holds S^T[key = 64kt + 16kb + 4kq + i][q]
-    f32x4v s[4];
+    f32x4 s[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       s[kb] = zero;
@@ -287,29 +309,30 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *qkv, int ld
     mt = fmaxf(mt, __shfl_xor(mt, 16));
     mt = fmaxf(mt, __shfl_xor(mt, 32));
     const float mn = fmaxf(m, mt);
-    const float alpha = expf(m - mn);
+    const float alpha = __builtin_amdgcn_exp2f(m - mn);
     m = mn;
     float ps = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[kb][i] = expf(s[kb][i] - mn);
+        s[kb][i] = __builtin_amdgcn_exp2f(s[kb][i] - mn);
         ps += s[kb][i];
       }
     l = l * alpha + ps;
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] *= alpha;
-    // O^T[d = 16db + 4kq + j][q] += sum over keys of V^T[d][key] P[q][key]
+    // O^T[d = 16db + 4kq + j][q] += sum over keys of V^T[d][key] P[q][key]:
+    // the A operand of step (kb, i) is V[16kb + 4kq + i][16db + ql]
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
-      f32x4v acc = o[db];
+      f32x4 acc = o[db];
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        const f32x4 vf = moe::ld4(Vt + (db * 16 + ql) * kAttnPitch + kb * 16 + 4 * kq);
+        const float *vp = Vs + (kb * 16 + 4 * kq) * kAttnPitch + db * 16 + ql;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[i], s[kb][i], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(vp[i * kAttnPitch], s[kb][i], acc, 0, 0, 0);
       }
       o[db] = acc;
     }
@@ -328,28 +351,60 @@ __global__ __launch_bounds__(256) void attention_kernel(const float *qkv, int ld
 // Short-conv mix
 // ---------------------------------------------------------------------------
 
-// One thread per (token, 4 channels): Bx = B * gate (conv_transpose_split_
-// kernel, layer.cu:377-378), the causal conv as the FMA chain of
+// One thread per (4 consecutive tokens, 4 channels): Bx = B * gate
+// (conv_transpose_split_kernel, layer.cu:377-378) of the window's rows, each
+// computed once, then per token the causal conv as the FMA chain of
 // causal_conv1d_kernel (layer.cu:397-403: sum from 0, taps k ascending, only
-// positions >= 0), times C (conv_gating_transpose_kernel, layer.cu:420).
-// Rows of the other taps are re-read (they stay in cache).
+// positions of the token's own sequence), times C
+// (conv_gating_transpose_kernel, layer.cu:420).  Threads next to each other
+// take neighbouring channels of the same tokens (coalesced rows); the window's
+// first L-1 rows are re-read by the thread of the previous tokens.
+constexpr int kConvTok = 4;   // tokens per thread
+constexpr int kConvMaxL = 4;  // taps the window holds
+
 __global__ __launch_bounds__(256) void shortconv_kernel(const float *bcg, const float *w, float *y,
-                                                        long long n4, int seq, int H, int L) {
+                                                        long long T, int seq, int H, int L) {
 #pragma clang fp contract(off)
   const int H4 = H / 4;
-  for (long long f = blockIdx.x * 256LL + threadIdx.x; f < n4; f += (long long)gridDim.x * 256) {
-    const long long t = f / H4;
-    const int c = (int)(f - t * H4) * 4;
-    const int s = (int)(t % seq);
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int k = 0; k < L; ++k) {
-      if (s - (L - 1) + k < 0) continue;
-      const float *row = bcg + (t - (L - 1) + k) * 3 * H;
-      const f32x4 bx = moe::ld4(row + c) * moe::ld4(row + 2 * H + c);
+  const long long groups = (T + kConvTok - 1) / kConvTok;
+  for (long long f = blockIdx.x * 256LL + threadIdx.x; f < groups * H4;
+       f += (long long)gridDim.x * 256) {
+    const long long tg = f / H4;
+    const int c = (int)(f - tg * H4) * 4;
+    const long long t0 = tg * kConvTok;
+    // taps of the 4 channels: w[c + j][k] = w[c*L + j*L + k], 4L floats from c*L
+    float wk[4][kConvMaxL];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(bx[j], w[(c + j) * L + k], acc[j]);
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int k = 0; k < kConvMaxL; ++k) wk[j][k] = k < L ? w[(c + j) * L + k] : 0.0f;
+    // Bx of tokens t0 - (L-1) .. t0 + kConvTok - 1 (zero where outside the tensor)
+    f32x4 bx[kConvTok + kConvMaxL - 1];
+#pragma unroll
+    for (int r = 0; r < kConvTok + kConvMaxL - 1; ++r) {
+      const long long t = t0 - (kConvMaxL - 1) + r;
+      if (t >= 0 && t < T && r >= kConvMaxL - L) {
+        const float *row = bcg + t * 3 * H;
+        bx[r] = moe::ld4(row + c) * moe::ld4(row + 2 * H + c);
+      } else {
+        bx[r] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+      }
     }
-    moe::st4(y + t * H + c, moe::ld4(bcg + t * 3 * H + H + c) * acc);
+#pragma unroll
+    for (int u = 0; u < kConvTok; ++u) {
+      const long long t = t0 + u;
+      if (t >= T) break;
+      const int s = (int)(t % seq);
+      f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int k = 0; k < kConvMaxL; ++k) {
+        if (k >= L || s - (L - 1) + k < 0) continue;
+        const f32x4 v = bx[u + (kConvMaxL - L) + k];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j] = __builtin_fmaf(v[j], wk[j][k], acc[j]);
+      }
+      moe::st4(y + t * H + c, moe::ld4(bcg + t * 3 * H + H + c) * acc);
+    }
   }
 }
 
@@ -427,8 +482,8 @@ hipError_t launch_embed(const int *ids, const float *table, float *h, int T, int
 hipError_t launch_rmsnorm_rows(const float *x, long long x_stride, const float *w, float *y,
                                long long y_stride, int rows, int dim, hipStream_t st) {
   if (rows <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(moe::kNormThreads), 0, st, x, x_stride,
-                     w, y, y_stride, dim);
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3((rows + kNormRows - 1) / kNormRows),
+                     dim3(moe::kNormThreads), 0, st, x, x_stride, w, y, y_stride, rows, dim);
   return hipGetLastError();
 }
 
@@ -437,7 +492,7 @@ hipError_t launch_qk_norm_rope(float *qkv, int ld, const float *qw, const float 
                                int heads, int kv_heads, int k_col, hipStream_t st) {
   const long long nrows = (long long)batch * seq * (heads + kv_heads);
   if (nrows <= 0) return hipSuccess;
-  const long long grid = (nrows + 3) / 4;
+  const long long grid = (nrows + 4 * kRopeRows - 1) / (4 * kRopeRows);
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)grid), dim3(256), 0, st, qkv, ld, qw, kw,
                      cos_t, sin_t, nrows, seq, heads, heads + kv_heads, k_col);
   return hipGetLastError();
@@ -447,20 +502,21 @@ hipError_t launch_attention(const float *qkv, int ld, float *out, int batch, int
                             int kv_heads, int k_col, int v_col, hipStream_t st) {
   if (batch <= 0 || seq <= 0) return hipSuccess;
   if (kv_heads <= 0 || heads != 4 * kv_heads) return hipErrorInvalidValue;
-  const int qgroups = (seq + kAttnQ - 1) / kAttnQ;
-  const long long grid = (long long)batch * kv_heads * qgroups;
-  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)grid), dim3(256), 0, st, qkv, ld, out,
-                     heads * kHeadDim, seq, kv_heads, heads / kv_heads, qgroups, k_col, v_col);
+  const int qblocks = (seq + kAttnQB - 1) / kAttnQB;
+  const long long grid = (long long)batch * kv_heads * qblocks;
+  hipLaunchKernelGGL(attention_kernel, dim3((unsigned)grid), dim3(kAttnThreads), 0, st, qkv, ld,
+                     out, heads * kHeadDim, seq, kv_heads, heads / kv_heads, qblocks, k_col, v_col);
   return hipGetLastError();
 }
 
 hipError_t launch_shortconv(const float *bcg, const float *w, float *y, int batch, int seq, int H,
                             int L, hipStream_t st) {
-  const long long n4 = (long long)batch * seq * (H / 4);
-  if (n4 <= 0) return hipSuccess;
-  if (H % 4 != 0 || L <= 0) return hipErrorInvalidValue;
-  const long long grid = std::min<long long>((n4 + 255) / 256, 65536);
-  hipLaunchKernelGGL(shortconv_kernel, dim3((unsigned)grid), dim3(256), 0, st, bcg, w, y, n4, seq,
+  const long long T = (long long)batch * seq;
+  if (T <= 0) return hipSuccess;
+  if (H % 4 != 0 || L <= 0 || L > kConvMaxL) return hipErrorInvalidValue;
+  const long long n = (T + kConvTok - 1) / kConvTok * (H / 4);
+  const long long grid = std::min<long long>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(shortconv_kernel, dim3((unsigned)grid), dim3(256), 0, st, bcg, w, y, T, seq,
                      H, L);
   return hipGetLastError();
 }

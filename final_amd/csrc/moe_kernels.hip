@@ -65,20 +65,25 @@ __device__ __forceinline__ float ref_sigmoid(float x) {
 }
 
 
-// One row per block: out = rmsnorm(h) (large batches; small ones normalise
-// inside router_decode_kernel).
+// Four rows per block (their loads in flight together): out = rmsnorm(h)
+// (large batches; small ones normalise inside router_decode_kernel).
+constexpr int kNormRowsPerBlock = 4;
+
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float *h, const float *w,
-                                                               float *out, int H) {
-#pragma clang fp contract(off)
-  __shared__ float s_grp[kNormGroups], s_tot[1];
-  const float *src = h + (size_t)blockIdx.x * H;
-  float *dst = out + (size_t)blockIdx.x * H;
-  float part[1] = {0.0f};
-  for (int i = threadIdx.x; i < H; i += kNormThreads) part[0] = __builtin_fmaf(src[i], src[i], part[0]);
-  norm_totals<1>(part, s_grp, s_tot);
-  const float rms = norm_rms(s_tot[0], H);
-  for (int i = threadIdx.x; i < H; i += kNormThreads) dst[i] = (src[i] * rms) * w[i];
+                                                               float *out, int T, int H) {
+  constexpr int NR = kNormRowsPerBlock;
+  __shared__ float s_grp[NR * kNormGroups], s_tot[NR];
+  const int r0 = blockIdx.x * NR;
+  const float *src[NR];
+  float *dst[NR];
+#pragma unroll
+  for (int m = 0; m < NR; ++m) {
+    src[m] = h + (size_t)min(r0 + m, T - 1) * H;
+    dst[m] = out + (size_t)min(r0 + m, T - 1) * H;
+  }
+  norm_rows<NR>(src, dst, min(NR, T - r0), w, H, s_grp, s_tot);
 }
+
 
 // acc = FMA chain over k = 0 .. K-1 of x[k] * g[k] (LDS rows xp, gp), k
 // ascending (layer.cu:109-127).  The chain is latency-bound, so the operands
@@ -1774,7 +1779,8 @@ hipError_t launch_router_dense(const RouterArgs &a, hipStream_t st) {
 
 hipError_t launch_rmsnorm(const float *h, const float *w, float *out, int T, int H, hipStream_t st) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, st, h, w, out, H);
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3((T + kNormRowsPerBlock - 1) / kNormRowsPerBlock),
+                     dim3(kNormThreads), 0, st, h, w, out, T, H);
   return hipGetLastError();
 }
 

@@ -81,7 +81,8 @@ int lfm_attention(const float *qkv, int ld, float *out, int batch, int seq, int 
  * with B, C, g the column blocks [0,H), [H,2H), [2H,3H) of bcg
  * [batch*seq][3*hidden], y[t][h] = C[t][h] * sum_{k: s-L+1+k >= 0}
  * (B*g)[t-L+1+k][h] * conv_weight[h][k], s = t % seq, L = kernel.
- * y [batch*seq][hidden], hidden % 4 == 0. */
+ * y [batch*seq][hidden], hidden % 4 == 0, kernel <= 4 (the reference's is 3,
+ * config.h:29). */
 int lfm_shortconv(const float *bcg, const float *conv_weight, float *y, int batch, int seq,
                   int hidden, int kernel, moe_stream_t stream);
 
