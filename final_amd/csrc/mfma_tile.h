@@ -16,35 +16,36 @@ template <int BM> struct TileCfg;
 // blocks.  B rows come in groups of 64 (gate/up phase: 32 rows of W1, then
 // the same 32 columns' rows of W3), and the epilogue pairs them through LDS.
 template <> struct TileCfg<128> {
-  static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, WN = 2, BK = 32;
+  static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, WN = 2, BK = 32, NS = 3;
 };
 // 64x128 tiles (128-1535 tokens): 64x256 tiles left 1.4 tiles per block at
 // T=256 (637 us per step, 527 with 64x128); 64x64 tiles balance the blocks
 // better but lose more per tile (537 us at T=256, 1208 vs 1115 at T=1024)
 template <> struct TileCfg<64> {
-  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, WN = 2, BK = 32;
+  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, WN = 2, BK = 32, NS = 3;
 };
 template <> struct TileCfg<32> {
-  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 2, BK = 16;
+  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 2, BK = 16, NS = 3;
 };
 
 // Half-width down tiles for the last units of a launch (same rows, half the
 // columns), so the last round of tiles is half as long.
 template <int BM> struct TileHalfCfg;
 template <> struct TileHalfCfg<128> {
-  static constexpr int WAVES_M = 4, WM = 1, WAVES_N = 1, WN = 2, BK = 32;
+  static constexpr int WAVES_M = 4, WM = 1, WAVES_N = 1, WN = 2, BK = 32, NS = 3;
 };
 template <> struct TileHalfCfg<64> {
-  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, WN = 1, BK = 32;
+  static constexpr int WAVES_M = 2, WM = 1, WAVES_N = 2, WN = 1, BK = 32, NS = 3;
 };
 template <> struct TileHalfCfg<32> {
-  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 1, BK = 16;
+  static constexpr int WAVES_M = 1, WM = 1, WAVES_N = 4, WN = 1, BK = 16, NS = 3;
 };
 
 template <int BM_, typename C> struct TileT {
   static constexpr int BM = BM_;
   static constexpr int WAVES_M = C::WAVES_M, WM = C::WM, WAVES_N = C::WAVES_N, WN = C::WN;
   static constexpr int BK = C::BK;
+  static constexpr int NS = C::NS;             // slabs of global loads in flight
   static constexpr int BN = WAVES_N * WN * 32;
   static constexpr int PITCH = BK + 4;           // floats per LDS row
   static constexpr int KV = BK / 4;              // float4 per row per slab
@@ -98,8 +99,6 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
   for (int i = 0; i < B_PER; ++i) st4(Bs + lds_st + i * RPP * PITCH, rb[i]);
 }
 
-// Slabs of global loads in flight ahead of the MFMAs (register sets).
-constexpr int kTilePrefetch = 3;
 
 // One output tile of C[rows][cols] = A[rows][K] . B[cols][K]^T.
 // A rows are gathered: row r starts at abase + aoff[r] (aoff in LDS; rows at
@@ -128,7 +127,17 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   float *Bs = lds + 2 * BM * PITCH;     // [2][BN][PITCH]
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave % TL::WAVES_M, wn = wave / TL::WAVES_M;
+  // Narrow layout of the 64-row tile: when every valid row fits the first
+  // 32-row block, the two waves of the empty second block would idle on their
+  // SIMDs; instead each of the 4 waves takes all rows and one 32-column block
+  // (same tile, same LDS layout, same products).  Not for 128-row tiles: the
+  // runtime column count in the inner loop costs their full tiles more
+  // (1.5% on a skewed T=16384 step) than their partial tiles gain.
+  constexpr bool kNarrowable = TL::WAVES_M == 2 && TL::WAVES_N == 2 && WM == 1 && WN == 2;
+  const bool narrow = kNarrowable && rows_valid <= WM * 32;
+  const int wm = narrow ? 0 : wave % TL::WAVES_M;
+  const int cb0 = narrow ? wave : (wave / TL::WAVES_M) * WN;  // this wave's first 32-column block
+  const int ncb = narrow ? 1 : WN;                            // its column blocks
   const int lrow = tid / KV, lc4 = (tid % KV) * 4;
 
   uint32_t a_src[A_PER];  // byte offset of this thread's A float4 (kTileOOB: zero row)
@@ -166,7 +175,7 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   // Global loads run kPrefetch slabs ahead in kPrefetch register sets: slab
   // t + kPrefetch is loaded while slab t's MFMAs run, and slab t + 1 (loaded
   // kPrefetch - 1 slabs earlier) is written to LDS after them.
-  constexpr int NS = kTilePrefetch;
+  constexpr int NS = TL::NS;
   constexpr int L = NS % 2 == 0 ? NS : 2 * NS;  // steps per unrolled round
   f32x4 sa[NS][A_PER], sb[NS][B_PER];
 #pragma unroll
@@ -179,7 +188,7 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   __syncthreads();
   const int lr = lane & 31, lh = (lane >> 5) * 4;
   const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
-  const float *b_rd = Bs + (wn * WN * 32 + lr) * PITCH + lh;
+  const float *b_rd = Bs + (cb0 * 32 + lr) * PITCH + lh;
   for (int s = 0; s < nslab; s += L) {
 #pragma unroll
     for (int u = 0; u < L; ++u) {
@@ -200,12 +209,14 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
 #pragma unroll
           for (int i = 0; i < WM; ++i) af[i] = ld4(Ac + i * 32 * PITCH + g8 * 8);
 #pragma unroll
-          for (int c = 0; c < WN; ++c) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
+          for (int c = 0; c < WN; ++c)
+            if (c < ncb) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
 #pragma unroll
           for (int i = 0; i < WM; ++i) {
             if (i > 0 && wrows <= 32) break;
 #pragma unroll
             for (int c = 0; c < WN; ++c) {
+              if (c >= ncb) break;
 #pragma unroll
               for (int q = 0; q < 4; ++q)
                 acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[c][q], acc[i][c], 0, 0, 0);
@@ -238,7 +249,8 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
       for (int r = 0; r < 16; ++r) {
         const int row = wrow0 + i * 32 + 8 * (r >> 2) + (lane >> 5) * 4 + (r & 3);
 #pragma unroll
-        for (int c = 0; c < WN; ++c) Cs[row * CP + (wn * WN + c) * 32 + lr] = acc[i][c][r];
+        for (int c = 0; c < WN; ++c)
+          if (c < ncb) Cs[row * CP + (cb0 + c) * 32 + lr] = acc[i][c][r];
       }
     }
   }
