@@ -100,81 +100,82 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 }
 
 
-// One output tile of C[rows][cols] = A[rows][K] . B[cols][K]^T.
-// A rows are gathered: row r starts at abase + aoff[r] (aoff in LDS; rows at
-// or past rows_valid are zero; abytes = bytes readable from abase).  B rows
-// are contiguous with stride K from brow0.  GATED: per wave the B tile holds 32 rows of W1 then the same 32 of
-// W3 and the epilogue writes silu(W1 x) * (W3 x); otherwise the product.
-//
-// Slab pipeline: global loads of slab s+1 are in flight while the MFMAs of
-// slab s run from LDS; one barrier per slab (double-buffered LDS).
-// Thread 0 claims the block's next task from `head` once the MFMAs are done
-// (returned; other threads return 0): the epilogue hides the claim's round
-// trip, and a block commits to its next task only near the end of this one.
-// head == nullptr: no claim (grids of one tile per block).  `out` stores the
-// epilogue's float4s: out.store(byte offset into [rows][ldo], value).
-template <typename TL, bool GATED, typename Out = AgentOut>
-__device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_t abytes,
-                                         const int *aoff, int rows_valid,
-                                         const float *brow0, int K, const Out &out,
-                                         int row0, int ldo, int col0, int *head) {
-  constexpr int BM = TL::BM;
-  constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH, KV = TL::KV;
+// Wave layouts of the slab loop.  Wide: the config's WAVES_M x WAVES_N grid
+// of 32x32 blocks.  Narrow (64-row tiles whose valid rows fit the first
+// 32-row block): instead of the second block's two waves idling on their
+// SIMDs, each of the 4 waves takes all rows and one 32-column block.  Not
+// for 128-row tiles: the runtime column count in the inner loop costs their
+// full tiles more (1.5% on a skewed T=16384 step) than their partial tiles
+// gain.  Skinny (64-row tiles with 1-16 or 33-48 valid rows, which 32-row
+// blocks pad to twice or 4/3 the rows): v_mfma_f32_16x16x4_f32 over 1 or 3
+// 16-row blocks (a template parameter, so the inner loop has no runtime
+// branches), each wave taking its 32 columns as two 16-column blocks.  Same
+// tile, LDS layout and products in every layout.
+template <typename TL>
+constexpr bool tile_narrowable() {
+  return TL::WAVES_M == 2 && TL::WAVES_N == 2 && TL::WM == 1 && TL::WN == 2;
+}
+
+// Slab loop of one tile: global loads NS slabs ahead in registers, LDS
+// double-buffered, one barrier per slab; then the block's next task is
+// claimed (thread 0; returned) and the products are written to the LDS
+// epilogue tile Cs [BM][CPITCH] in B-row order.
+template <typename TL, int SKINNY_RB>
+__device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL::A_PER],
+                                          __amdgpu_buffer_rsrc_t abase_r,
+                                          __amdgpu_buffer_rsrc_t bsrc_r,
+                                          __amdgpu_buffer_rsrc_t none_r, uint32_t bsrc, int lds_st,
+                                          int lrow, int K, int rows_valid, int *head) {
+  constexpr int BM = TL::BM, BN = TL::BN;
+  constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
-  constexpr int ROWS_PER_PASS = kThreads / KV;  // rows one pass of loads covers
-  static_assert(TL::B_F4 % kThreads == 0, "B slab splits evenly");
+  constexpr int ROWS_PER_PASS = kThreads / TL::KV;
+  constexpr bool SKINNY = SKINNY_RB > 0;  // 0: the 32x32 layouts
+  static_assert(!SKINNY || tile_narrowable<TL>(), "skinny layout of 64x128 tiles");
   float *As = lds;                      // [2][BM][PITCH]
   float *Bs = lds + 2 * BM * PITCH;     // [2][BN][PITCH]
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  // Narrow layout of the 64-row tile: when every valid row fits the first
-  // 32-row block, the two waves of the empty second block would idle on their
-  // SIMDs; instead each of the 4 waves takes all rows and one 32-column block
-  // (same tile, same LDS layout, same products).  Not for 128-row tiles: the
-  // runtime column count in the inner loop costs their full tiles more
-  // (1.5% on a skewed T=16384 step) than their partial tiles gain.
-  constexpr bool kNarrowable = TL::WAVES_M == 2 && TL::WAVES_N == 2 && WM == 1 && WN == 2;
-  const bool narrow = kNarrowable && rows_valid <= WM * 32;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
+  // 32x32 layouts: this wave's row block, first 32-column block, column
+  // blocks, and rows that hold data (0 = skip the MFMAs, <= 32 with WM == 2 =
+  // only the first row block; wave-uniform branches)
+  const bool narrow = tile_narrowable<TL>() && rows_valid <= 32;
   const int wm = narrow ? 0 : wave % TL::WAVES_M;
-  const int cb0 = narrow ? wave : (wave / TL::WAVES_M) * WN;  // this wave's first 32-column block
-  const int ncb = narrow ? 1 : WN;                            // its column blocks
-  const int lrow = tid / KV, lc4 = (tid % KV) * 4;
-
-  uint32_t a_src[A_PER];  // byte offset of this thread's A float4 (kTileOOB: zero row)
-#pragma unroll
-  for (int i = 0; i < A_PER; ++i) {
-    const int r = lrow + i * ROWS_PER_PASS;
-    a_src[i] = (r < BM && r < rows_valid) ? (uint32_t)(aoff[r] + lc4) * 4u : kTileOOB;
-  }
-  const __amdgpu_buffer_rsrc_t abase_r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(abase), 0, (int)abytes, kBufferRsrcWord3);
-  const __amdgpu_buffer_rsrc_t bsrc_r = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float *>(brow0), 0, (int)((uint32_t)TL::BN * K * 4u), kBufferRsrcWord3);
-  // loads past the last slab use descriptors of size 0 (zeros, no traffic):
-  // every load and LDS store of the loop is unconditional, which keeps the
-  // compiler's count of loads in flight exact across the loop
-  const __amdgpu_buffer_rsrc_t none_r =
-      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(brow0), 0, 0, kBufferRsrcWord3);
-  const uint32_t bsrc = (uint32_t)(lrow * K + lc4) * 4u;
-  const int lds_st = lrow * PITCH + lc4;
-
-  floatx16 acc[WM][WN];
-#pragma unroll
-  for (int i = 0; i < WM; ++i)
-#pragma unroll
-    for (int c = 0; c < WN; ++c)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.0f;
-
-  // Rows of this wave that hold data: 0 = skip the MFMAs, <= 32 with WM == 2
-  // = only the first row block (wave-uniform branches).
+  const int cb0 = narrow ? wave : (wave / TL::WAVES_M) * WN;
+  const int ncb = narrow ? 1 : WN;
   const int wrow0 = wm * WM * 32;
   const int wrows = min(max(rows_valid - wrow0, 0), WM * 32);
+  const int lr = lane & 31, lh = (lane >> 5) * 4;
+  const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
+  const float *b_rd = Bs + (cb0 * 32 + lr) * PITCH + lh;
+  // skinny layout: lane l supplies row l % 16 at k offset 4 * (l / 16) of each
+  // 16-wide k group, as a float4 whose component q feeds the q-th MFMA (the
+  // same k permutation in A and B)
+  constexpr int SRB = SKINNY ? SKINNY_RB : 1;
+  const int l16 = lane & 15, k16 = (lane >> 4) * 4;
+  const float *a16 = As + l16 * PITCH + k16;
+  const float *b16 = Bs + (wave * 32 + l16) * PITCH + k16;
+
+  floatx16 acc[SKINNY ? 1 : WM][SKINNY ? 1 : WN];
+  f32x4 acc16[SRB][SKINNY ? 2 : 1];
+  if constexpr (SKINNY) {
+#pragma unroll
+    for (int i = 0; i < SRB; ++i)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) acc16[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  } else {
+#pragma unroll
+    for (int i = 0; i < WM; ++i)
+#pragma unroll
+      for (int c = 0; c < WN; ++c)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.0f;
+  }
 
   const int nslab = K / BK;
-  // Global loads run kPrefetch slabs ahead in kPrefetch register sets: slab
-  // t + kPrefetch is loaded while slab t's MFMAs run, and slab t + 1 (loaded
-  // kPrefetch - 1 slabs earlier) is written to LDS after them.
+  // Global loads run NS slabs ahead in NS register sets: slab t + NS is
+  // loaded while slab t's MFMAs run, and slab t + 1 (loaded NS - 1 slabs
+  // earlier) is written to LDS after them.
   constexpr int NS = TL::NS;
   constexpr int L = NS % 2 == 0 ? NS : 2 * NS;  // steps per unrolled round
   f32x4 sa[NS][A_PER], sb[NS][B_PER];
@@ -186,9 +187,6 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   }
   slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(sa[0], sb[0], As, Bs, lds_st, lrow);
   __syncthreads();
-  const int lr = lane & 31, lh = (lane >> 5) * 4;
-  const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
-  const float *b_rd = Bs + (cb0 * 32 + lr) * PITCH + lh;
   for (int s = 0; s < nslab; s += L) {
 #pragma unroll
     for (int u = 0; u < L; ++u) {
@@ -200,9 +198,27 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
         slab_load<A_PER, B_PER, ROWS_PER_PASS>(sa[u % NS], sb[u % NS], a_src, in ? abase_r : none_r,
                                                bsrc, in ? bsrc_r : none_r, K, in ? (t + NS) * BK : 0);
       }
-      const float *Ac = a_rd + (u & 1) * BM * PITCH;
-      const float *Bc = b_rd + (u & 1) * TL::BN * PITCH;
-      if (wrows > 0) {
+      if constexpr (SKINNY) {
+        const float *A16 = a16 + (u & 1) * BM * PITCH;
+        const float *B16 = b16 + (u & 1) * BN * PITCH;
+#pragma unroll
+        for (int g16 = 0; g16 < BK / 16; ++g16) {
+          f32x4 af[SRB], bf[2];
+#pragma unroll
+          for (int i = 0; i < SRB; ++i) af[i] = ld4(A16 + i * 16 * PITCH + g16 * 16);
+#pragma unroll
+          for (int c = 0; c < 2; ++c) bf[c] = ld4(B16 + c * 16 * PITCH + g16 * 16);
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int i = 0; i < SRB; ++i)
+#pragma unroll
+              for (int c = 0; c < 2; ++c)
+                acc16[i][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][q], bf[c][q], acc16[i][c], 0, 0, 0);
+        }
+      } else if (wrows > 0) {
+        const float *Ac = a_rd + (u & 1) * BM * PITCH;
+        const float *Bc = b_rd + (u & 1) * BN * PITCH;
 #pragma unroll
         for (int g8 = 0; g8 < BK / 8; ++g8) {
           f32x4 af[WM], bf[WN];
@@ -227,22 +243,30 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
       // slab t + 1 (past the end: zeros into a buffer nobody reads again)
       slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(
           sa[(u + 1) % NS], sb[(u + 1) % NS], As + ((u + 1) & 1) * BM * PITCH,
-          Bs + ((u + 1) & 1) * TL::BN * PITCH, lds_st, lrow);
+          Bs + ((u + 1) & 1) * BN * PITCH, lds_st, lrow);
       __syncthreads();
     }
   }
 
   const int next = threadIdx.x == 0 && head ? claim(head) : 0;
 
-  // Epilogue through LDS (the slab buffers are free after the last barrier):
-  // the products are written as a [BM][BN] tile in B-row order, then stored
-  // as whole-row float4s; gate/up tiles store silu(W1 x) * (W3 x) of each
-  // 64-row group's two halves.  32x32 f32 MFMA result layout: lane l holds
-  // column l % 32 and rows 8*(r/4) + 4*(l/32) + r%4 for r = 0..15.
-  constexpr int NC = GATED ? TL::BN / 2 : TL::BN;  // output columns of the tile
+  // Products into the epilogue tile (the slab buffers are free after the
+  // last barrier).
   constexpr int CP = TL::CPITCH;
   float *Cs = lds;
-  if (wrows > 0) {
+  if constexpr (SKINNY) {
+    // 16x16 f32 MFMA result layout: lane l holds column l % 16 and rows
+    // 4 * (l / 16) + r for r = 0..3
+#pragma unroll
+    for (int i = 0; i < SRB; ++i)
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          Cs[(i * 16 + k16 + r) * CP + wave * 32 + c * 16 + l16] = acc16[i][c][r];
+  } else if (wrows > 0) {
+    // 32x32 f32 MFMA result layout: lane l holds column l % 32 and rows
+    // 8*(r/4) + 4*(l/32) + r%4 for r = 0..15
 #pragma unroll
     for (int i = 0; i < WM; ++i) {
 #pragma unroll
@@ -254,6 +278,70 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
       }
     }
   }
+  return next;
+}
+
+// One output tile of C[rows][cols] = A[rows][K] . B[cols][K]^T.
+// A rows are gathered: row r starts at abase + aoff[r] (aoff in LDS; rows at
+// or past rows_valid are zero; abytes = bytes readable from abase).  B rows
+// are contiguous with stride K from brow0.  GATED: per wave the B tile holds
+// 32 rows of W1 then the same 32 of W3 and the epilogue writes
+// silu(W1 x) * (W3 x); otherwise the product.
+//
+// Slab pipeline: global loads of slab s+1 are in flight while the MFMAs of
+// slab s run from LDS; one barrier per slab (double-buffered LDS).
+// Thread 0 claims the block's next task from `head` once the MFMAs are done
+// (returned; other threads return 0): the epilogue hides the claim's round
+// trip, and a block commits to its next task only near the end of this one.
+// head == nullptr: no claim (grids of one tile per block).  `out` stores the
+// epilogue's float4s: out.store(byte offset into [rows][ldo], value).
+template <typename TL, bool GATED, typename Out = AgentOut>
+__device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_t abytes,
+                                         const int *aoff, int rows_valid,
+                                         const float *brow0, int K, const Out &out,
+                                         int row0, int ldo, int col0, int *head) {
+  constexpr int BM = TL::BM;
+  constexpr int KV = TL::KV, A_PER = TL::A_PER;
+  constexpr int ROWS_PER_PASS = kThreads / KV;  // rows one pass of loads covers
+  static_assert(TL::B_F4 % kThreads == 0, "B slab splits evenly");
+  const int tid = threadIdx.x;
+  const int lrow = tid / KV, lc4 = (tid % KV) * 4;
+
+  uint32_t a_src[A_PER];  // byte offset of this thread's A float4 (kTileOOB: zero row)
+#pragma unroll
+  for (int i = 0; i < A_PER; ++i) {
+    const int r = lrow + i * ROWS_PER_PASS;
+    a_src[i] = (r < BM && r < rows_valid) ? (uint32_t)(aoff[r] + lc4) * 4u : kTileOOB;
+  }
+  const __amdgpu_buffer_rsrc_t abase_r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(abase), 0, (int)abytes, kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t bsrc_r = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float *>(brow0), 0, (int)((uint32_t)TL::BN * K * 4u), kBufferRsrcWord3);
+  // loads past the last slab use descriptors of size 0 (zeros, no traffic):
+  // every load and LDS store of the loop is unconditional, which keeps the
+  // compiler's count of loads in flight exact across the loop
+  const __amdgpu_buffer_rsrc_t none_r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float *>(brow0), 0, 0, kBufferRsrcWord3);
+  const uint32_t bsrc = (uint32_t)(lrow * K + lc4) * 4u;
+  const int lds_st = lrow * TL::PITCH + lc4;
+
+  constexpr bool kSk = tile_narrowable<TL>();
+  int next;
+  if (kSk && rows_valid <= 16)
+    next = tile_slabs<TL, kSk ? 1 : 0>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                                       rows_valid, head);
+  else if (kSk && rows_valid > 32 && rows_valid <= 48)
+    next = tile_slabs<TL, kSk ? 3 : 0>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                                       rows_valid, head);
+  else
+    next = tile_slabs<TL, 0>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                             rows_valid, head);
+
+  // Epilogue: the [BM][BN] tile in LDS is stored as whole-row float4s;
+  // gate/up tiles store silu(W1 x) * (W3 x) of each 64-row group's two halves.
+  constexpr int NC = GATED ? TL::BN / 2 : TL::BN;  // output columns of the tile
+  constexpr int CP = TL::CPITCH;
+  const float *Cs = lds;
   __syncthreads();
   constexpr int NC4 = NC / 4;
   for (int f = tid; f < BM * NC4; f += kThreads) {
