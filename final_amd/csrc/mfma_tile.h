@@ -100,17 +100,21 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 }
 
 
-// Wave layouts of the slab loop.  Wide: the config's WAVES_M x WAVES_N grid
-// of 32x32 blocks.  Narrow (64-row tiles whose valid rows fit the first
-// 32-row block): instead of the second block's two waves idling on their
-// SIMDs, each of the 4 waves takes all rows and one 32-column block.  Not
-// for 128-row tiles: the runtime column count in the inner loop costs their
-// full tiles more (1.5% on a skewed T=16384 step) than their partial tiles
-// gain.  Skinny (64-row tiles with 1-16 or 33-48 valid rows, which 32-row
-// blocks pad to twice or 4/3 the rows): v_mfma_f32_16x16x4_f32 over 1 or 3
-// 16-row blocks (a template parameter, so the inner loop has no runtime
-// branches), each wave taking its 32 columns as two 16-column blocks.  Same
-// tile, LDS layout and products in every layout.
+// Wave layouts of the slab loop, chosen once per tile (each is its own
+// instantiation, so the inner loops have no runtime branches on the layout).
+//   kWide: the config's WAVES_M x WAVES_N grid of 32x32 blocks.
+//   kNarrow (64-row tiles whose valid rows fit the first 32-row block):
+//     instead of the second block's two waves idling on their SIMDs, each of
+//     the 4 waves takes all rows and one 32-column block.
+//   kSkinny1 / kSkinny3 (64-row tiles with 1-16 or 33-48 valid rows, which
+//     32-row blocks pad to twice or 4/3 the rows): v_mfma_f32_16x16x4_f32
+//     over 1 or 3 16-row blocks, each wave taking its 32 columns as two
+//     16-column blocks.
+// Same tile, LDS layout and products in every layout.
+enum TileLayout { kWide = 0, kNarrow = 1, kSkinny1 = 2, kSkinny3 = 3 };
+
+// 64x128 tiles: the 2 x 2 grid of 32x64 wave tiles.  (A 128-row tile with
+// at most 64 valid rows runs as a 64-row tile; its caller decides.)
 template <typename TL>
 constexpr bool tile_narrowable() {
   return TL::WAVES_M == 2 && TL::WAVES_N == 2 && TL::WM == 1 && TL::WN == 2;
@@ -120,7 +124,7 @@ constexpr bool tile_narrowable() {
 // double-buffered, one barrier per slab; then the block's next task is
 // claimed (thread 0; returned) and the products are written to the LDS
 // epilogue tile Cs [BM][CPITCH] in B-row order.
-template <typename TL, int SKINNY_RB>
+template <typename TL, TileLayout LAYOUT>
 __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL::A_PER],
                                           __amdgpu_buffer_rsrc_t abase_r,
                                           __amdgpu_buffer_rsrc_t bsrc_r,
@@ -130,8 +134,9 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
   constexpr int ROWS_PER_PASS = kThreads / TL::KV;
-  constexpr bool SKINNY = SKINNY_RB > 0;  // 0: the 32x32 layouts
-  static_assert(!SKINNY || tile_narrowable<TL>(), "skinny layout of 64x128 tiles");
+  constexpr bool SKINNY = LAYOUT == kSkinny1 || LAYOUT == kSkinny3;
+  constexpr bool NARROW = LAYOUT == kNarrow;
+  static_assert(!(SKINNY || NARROW) || tile_narrowable<TL>(), "layouts of 64x128 tiles");
   float *As = lds;                      // [2][BM][PITCH]
   float *Bs = lds + 2 * BM * PITCH;     // [2][BN][PITCH]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -139,10 +144,9 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   // 32x32 layouts: this wave's row block, first 32-column block, column
   // blocks, and rows that hold data (0 = skip the MFMAs, <= 32 with WM == 2 =
   // only the first row block; wave-uniform branches)
-  const bool narrow = tile_narrowable<TL>() && rows_valid <= 32;
-  const int wm = narrow ? 0 : wave % TL::WAVES_M;
-  const int cb0 = narrow ? wave : (wave / TL::WAVES_M) * WN;
-  const int ncb = narrow ? 1 : WN;
+  const int wm = NARROW ? 0 : wave % TL::WAVES_M;
+  const int cb0 = NARROW ? wave : (wave / TL::WAVES_M) * WN;
+  constexpr int ncb = NARROW ? 1 : WN;
   const int wrow0 = wm * WM * 32;
   const int wrows = min(max(rows_valid - wrow0, 0), WM * 32);
   const int lr = lane & 31, lh = (lane >> 5) * 4;
@@ -151,7 +155,7 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   // skinny layout: lane l supplies row l % 16 at k offset 4 * (l / 16) of each
   // 16-wide k group, as a float4 whose component q feeds the q-th MFMA (the
   // same k permutation in A and B)
-  constexpr int SRB = SKINNY ? SKINNY_RB : 1;
+  constexpr int SRB = LAYOUT == kSkinny3 ? 3 : 1;
   const int l16 = lane & 15, k16 = (lane >> 4) * 4;
   const float *a16 = As + l16 * PITCH + k16;
   const float *b16 = Bs + (wave * 32 + l16) * PITCH + k16;
@@ -325,17 +329,22 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   const uint32_t bsrc = (uint32_t)(lrow * K + lc4) * 4u;
   const int lds_st = lrow * TL::PITCH + lc4;
 
-  constexpr bool kSk = tile_narrowable<TL>();
+  constexpr bool kNa = tile_narrowable<TL>();
+  constexpr TileLayout kS1 = kNa ? kSkinny1 : kWide, kS3 = kNa ? kSkinny3 : kWide;
+  constexpr TileLayout kNw = kNa ? kNarrow : kWide;
   int next;
-  if (kSk && rows_valid <= 16)
-    next = tile_slabs<TL, kSk ? 1 : 0>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                                       rows_valid, head);
-  else if (kSk && rows_valid > 32 && rows_valid <= 48)
-    next = tile_slabs<TL, kSk ? 3 : 0>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                                       rows_valid, head);
+  if (kNa && rows_valid <= 16)
+    next = tile_slabs<TL, kS1>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head);
+  else if (kNa && rows_valid > 32 && rows_valid <= 48)
+    next = tile_slabs<TL, kS3>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head);
+  else if (kNa && rows_valid <= 32)
+    next = tile_slabs<TL, kNw>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head);
   else
-    next = tile_slabs<TL, 0>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                             rows_valid, head);
+    next = tile_slabs<TL, kWide>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                                 rows_valid, head);
 
   // Epilogue: the [BM][BN] tile in LDS is stored as whole-row float4s;
   // gate/up tiles store silu(W1 x) * (W3 x) of each 64-row group's two halves.

@@ -170,14 +170,14 @@ static int plan_index(int rows) {
 }
 
 // Crossovers measured on MI355X with the seed-0 workload (whole-step times):
-// weight streaming is fastest up to 128 tokens (323 vs 349 us at 96, even at
-// 128), 64-row MFMA tiles from 160 to 1024 tokens (448 vs 483 us at 256),
-// 128-row tiles from 1536 (1381 vs 1453 us).
+// weight streaming is fastest up to 96 tokens (324 vs 329 us at 80, even at
+// 96), 64-row MFMA tiles from 112 to 1024 tokens (334 vs 342 us at 112, 331
+// vs 350 at 128), 128-row tiles from 1536 (1381 vs 1453 us).
 // The dense FFN's 4 chunk experts each hold every token, so its MFMA plans
 // have few tiles at small T: streaming stays fastest up to ~192 tokens (220
 // vs 284 us at 128), 64-row tiles from 256 (338 vs 365 us).
 static int auto_plan(int T, bool stream_ok, bool dense) {
-  if (T <= (dense ? 192 : 128) && stream_ok) return 0;
+  if (T <= (dense ? 192 : 96) && stream_ok) return 0;
   if (T < 1536) return 64;
   return 128;
 }

@@ -15,7 +15,7 @@
 //      a dispatch phase that assigns slots (replaces moe_scatter_kernel,
 //      layer.cu:501-542, without copying x), one dynamic task queue, the
 //      combine inside the down tiles; 64-row tiles up to 1535 tokens,
-//      128-row tiles above.  T <= 128:
+//      128-row tiles above.  T <= 96:
 //      expert_ring_kernel, weight streaming through MFMA 16x16x4 f32 with
 //      round-robin tasks and slots assigned by the router.
 //
@@ -931,9 +931,16 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
       __syncthreads();
       const float *brow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TL::BN) * H;
-      next = mfma_tile<Tile<BM>, true>(lds, a.x, (uint32_t)((size_t)a.T * H * sizeof(float)), s_aoff,
-                                       rows, brow0, H, inter_out, slot0, I, nt * (TL::BN / 2),
-                                       &c->head);
+      const uint32_t xbytes = (uint32_t)((size_t)a.T * H * sizeof(float));
+      // a 128-row unit holding at most 64 rows runs as a 64x128 tile (same
+      // columns and outputs, half the padding MFMAs)
+      static_assert(Tile<64>::BN == Tile<128>::BN, "a 64-row tile covers a 128-row unit's columns");
+      if (BM == 128 && rows <= 64)
+        next = mfma_tile<Tile<64>, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
+                                         I, nt * (TL::BN / 2), &c->head);
+      else
+        next = mfma_tile<Tile<BM>, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
+                                         I, nt * (TL::BN / 2), &c->head);
       block_signal(&a.s.dep[u]);
     } else if (task < nb + n1 + n2) {
       // down tiles: full width for the first units, two half-width tiles per
@@ -960,8 +967,12 @@ void expert_mfma_kernel(ExpertArgs a) {
         tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb);
       } else {
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
-        next = mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
-                                    H, ht * TL::BN, &c->head);
+        if (BM == 128 && rows <= 64)
+          next = mfma_tile<Tile<64>, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out,
+                                            slot0, H, ht * TL::BN, &c->head);
+        else
+          next = mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
+                                      H, ht * TL::BN, &c->head);
         tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb);
       }
     }
