@@ -16,7 +16,7 @@ template <int BM> struct TileCfg;
 // blocks.  B rows come in groups of 64 (gate/up phase: 32 rows of W1, then
 // the same 32 columns' rows of W3), and the epilogue pairs them through LDS.
 template <> struct TileCfg<128> {
-  static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, WN = 2, BK = 32, NS = 3;
+  static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, WN = 2, BK = 32, NS = 2;
 };
 // 64x128 tiles (73-831 tokens): 64x256 tiles left 1.4 tiles per block at
 // T=256 (637 us per step, 527 with 64x128); 64x64 tiles balance the blocks
@@ -79,13 +79,17 @@ __device__ __forceinline__ void slab_load(f32x4 (&ra)[A_PER], f32x4 (&rb)[B_PER]
                                           const uint32_t (&a_off)[A_PER],
                                           __amdgpu_buffer_rsrc_t ar, uint32_t b_off,
                                           __amdgpu_buffer_rsrc_t br, int K, int k0) {
+  // per-thread offsets are the same for every slab; the slab's k offset is
+  // the instruction's scalar offset, so no VGPR is rewritten per slab (a
+  // rewritten address register made the compiler wait for loads in flight)
+  const int ks = k0 * 4;
 #pragma unroll
   for (int i = 0; i < A_PER; ++i)
-    ra[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, a_off[i] + k0 * 4u, 0, 0));
+    ra[i] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(ar, a_off[i], ks, 0));
 #pragma unroll
   for (int i = 0; i < B_PER; ++i)
     rb[i] = __builtin_bit_cast(
-        f32x4, __builtin_amdgcn_raw_buffer_load_b128(br, b_off + (uint32_t)(i * RPP * K + k0) * 4u, 0, 0));
+        f32x4, __builtin_amdgcn_raw_buffer_load_b128(br, b_off + (uint32_t)(i * RPP * K) * 4u, ks, 0));
 }
 
 template <int BM, int A_PER, int B_PER, int RPP, int PITCH>
@@ -103,6 +107,8 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 // Wave layouts of the slab loop, chosen once per tile (each is its own
 // instantiation, so the inner loops have no runtime branches on the layout).
 //   kWide: the config's WAVES_M x WAVES_N grid of 32x32 blocks.
+//   kFull: kWide for a tile whose rows are all valid, with no row checks in
+//     its inner loop (straight-line MFMA code).
 //   kNarrow (64-row tiles whose valid rows fit the first 32-row block):
 //     instead of the second block's two waves idling on their SIMDs, each of
 //     the 4 waves takes all rows and one 32-column block.
@@ -111,7 +117,7 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 //     over 1 or 3 16-row blocks, each wave taking its 32 columns as two
 //     16-column blocks.
 // Same tile, LDS layout and products in every layout.
-enum TileLayout { kWide = 0, kNarrow = 1, kSkinny1 = 2, kSkinny3 = 3 };
+enum TileLayout { kWide = 0, kNarrow = 1, kSkinny1 = 2, kSkinny3 = 3, kFull = 4 };
 
 // 64x128 tiles: the 2 x 2 grid of 32x64 wave tiles.  (A 128-row tile with
 // at most 64 valid rows runs as a 64-row tile; its caller decides.)
@@ -139,7 +145,8 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   static_assert(!(SKINNY || NARROW) || tile_narrowable<TL>(), "layouts of 64x128 tiles");
   float *As = lds;                      // [2][BM][PITCH]
   float *Bs = lds + 2 * BM * PITCH;     // [2][BN][PITCH]
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform branches
 
   // 32x32 layouts: this wave's row block, first 32-column block, column
   // blocks, and rows that hold data (0 = skip the MFMAs, <= 32 with WM == 2 =
@@ -148,7 +155,7 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   const int cb0 = NARROW ? wave : (wave / TL::WAVES_M) * WN;
   constexpr int ncb = NARROW ? 1 : WN;
   const int wrow0 = wm * WM * 32;
-  const int wrows = min(max(rows_valid - wrow0, 0), WM * 32);
+  const int wrows = LAYOUT == kFull ? WM * 32 : min(max(rows_valid - wrow0, 0), WM * 32);
   const int lr = lane & 31, lh = (lane >> 5) * 4;
   const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
   const float *b_rd = Bs + (cb0 * 32 + lr) * PITCH + lh;
@@ -196,12 +203,16 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
     for (int u = 0; u < L; ++u) {
       const int t = s + u;
       if (t >= nslab) break;
-      // the set of slab t is free (written to LDS a step ago): slab t + NS
+      // the set of slab t is free (written to LDS a step ago): slab t + NS.
+      // The scheduling barrier keeps these loads ahead of the step's MFMAs:
+      // sunk below them, their destinations took the MFMA operands'
+      // registers, and the next step's first LDS reads then waited for them.
       {
         const bool in = t + NS < nslab;
         slab_load<A_PER, B_PER, ROWS_PER_PASS>(sa[u % NS], sb[u % NS], a_src, in ? abase_r : none_r,
                                                bsrc, in ? bsrc_r : none_r, K, in ? (t + NS) * BK : 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
       if constexpr (SKINNY) {
         const float *A16 = a16 + (u & 1) * BM * PITCH;
         const float *B16 = b16 + (u & 1) * BN * PITCH;
@@ -342,6 +353,9 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   else if (kNa && rows_valid <= 32)
     next = tile_slabs<TL, kNw>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
+  else if (rows_valid >= BM)
+    next = tile_slabs<TL, kFull>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                                 rows_valid, head);
   else
     next = tile_slabs<TL, kWide>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                  rows_valid, head);
