@@ -154,6 +154,24 @@ def roofline(plan, flops, nbytes, ms, name):
     return roof
 
 
+SETTLE_S = 0.1
+
+
+def settle_clock(step, stream):
+    """Runs untimed steps for SETTLE_S seconds before the warm-up steps: the
+    GPU clock ramps up over the first tens of milliseconds of work (T=4096
+    forwards run 3.4 ms at first, 2.78 ms from about the eighth), so short
+    runs and profiles would otherwise time the ramp."""
+    t0 = time.perf_counter()
+    i = 0
+    while time.perf_counter() - t0 < SETTLE_S:
+        step(i)
+        i += 1
+        if i % 4 == 0:
+            stream.synchronize()
+    stream.synchronize()
+
+
 def measure_moe(name, w, x, steps, warmup, nsets):
     """Times `steps` back-to-back forwards of workload `name` (weights w,
     tokens x) cycling nsets device copies of the weights, then the same steps
@@ -172,6 +190,7 @@ def measure_moe(name, w, x, steps, warmup, nsets):
     plan = blocks[0].plan(T)
     log(f"[bench] {name}: T={T} plan={plan} (0 = weight streaming, else MFMA tile rows), "
         f"weight sets={nsets}")
+    settle_clock(lambda i: blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream), stream)
     for i in range(warmup):
         blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream)
     stream.synchronize()
@@ -327,6 +346,7 @@ def bench_dense(args, wl):
     dx = hip.DeviceArray.from_numpy(x)
     dy = hip.DeviceArray((T, W.H))
     plan = mlps[0].plan(T)
+    settle_clock(lambda i: mlps[i % nsets].forward_gpu(dx, dy, T, stream=stream), stream)
     for i in range(args.warmup):
         mlps[i % nsets].forward_gpu(dx, dy, T, stream=stream)
     stream.synchronize()
