@@ -77,26 +77,22 @@ def test_every_kernel_plan(plan, block, real_weights, oracle_mod):
 def test_router_block_splits(T, block, real_weights, oracle_mod):
     """Large batches split each 64-token router block's experts over 4, 2 or 1
     blocks (6000 tokens: 94 token blocks, split in 2; 8200: 129, unsplit;
-    4096 in test_forward_matches_oracle: split in 4).  Routing checked on
-    every token, y on every 8th."""
+    4096 in test_forward_matches_oracle: split in 4).  Routing and y checked
+    on every token."""
     from final_amd import workloads as W
     say(f"[router split] T={T} plan={block.plan(T)}")
     x = W.gen_x(T, seed=5)
     y = block.forward(x)
     rt = block.last_routing()
-    mask = np.zeros(T, np.uint8)
-    mask[::8] = 1
-    ref = oracle_forward(oracle_mod, real_weights, x, token_mask=mask)
+    ref = oracle_forward(oracle_mod, real_weights, x)
     check_routing(rt, ref)
-    sel = mask.astype(bool)
-    np.testing.assert_allclose(y[sel], ref["y"][sel], rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(y, ref["y"], rtol=RTOL, atol=ATOL)
 
 
 @pytest.mark.gpu
 def test_zipf_skew_t16384(block, real_weights, oracle_mod):
     """Skewed routing: Zipf(1.2) expert frequencies, 3 empty experts, one expert
-    taking nearly every token.  Routing checked on all 16384 tokens; y on
-    every 16th token (the oracle's y rows are independent per token)."""
+    taking nearly every token.  Routing and y checked on all 16384 tokens."""
     from final_amd import workloads as W
     T = 16384
     w = dict(real_weights)
@@ -110,13 +106,10 @@ def test_zipf_skew_t16384(block, real_weights, oracle_mod):
     finally:
         rw = real_weights
         block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
-    mask = np.zeros(T, np.uint8)
-    mask[::16] = 1
-    ref = oracle_forward(oracle_mod, w, x, token_mask=mask)
+    ref = oracle_forward(oracle_mod, w, x)
     check_routing(rt, ref)
     assert (rt["counts"] == 0).sum() >= 3
-    sel = mask.astype(bool)
-    np.testing.assert_allclose(y[sel], ref["y"][sel], rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(y, ref["y"], rtol=RTOL, atol=ATOL)
 
 
 @pytest.mark.gpu
@@ -227,16 +220,10 @@ def test_forward_norm_matches_oracle(T, block, real_weights, oracle_mod):
     out = block.forward_norm(h)
     xn = block.last_normed()
     rt = block.last_routing()
-    mask = None
-    if T > 1000:
-        mask = np.zeros(T, np.uint8)
-        mask[::8] = 1
-    ref = oracle_mod.moe_forward_norm(h, nw, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"],
-                                      token_mask=mask)
+    ref = oracle_mod.moe_forward_norm(h, nw, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
     assert np.array_equal(bits(xn), bits(ref["xn"])), "normalised rows differ"
     check_routing(rt, ref)
-    sel = slice(None) if mask is None else mask.astype(bool)
-    np.testing.assert_allclose(out[sel], ref["y"][sel], rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(out, ref["y"], rtol=RTOL, atol=ATOL)
 
 
 @pytest.mark.gpu
