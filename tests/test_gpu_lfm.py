@@ -36,8 +36,10 @@ def dev(a):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("M,N,K,res", [(1, 128, 32, False), (64, 65536 // 16, 2048, False),
+@pytest.mark.parametrize("M,N,K,res", [(1, 128, 32, False), (20, 256, 512, False),
+                                       (64, 65536 // 16, 2048, False),
                                        (100, 3072, 2048, True), (300, 256, 64, False),
+                                       (1050, 128, 2048, False), (1100, 384, 256, True),
                                        (2048, 6144, 2048, False), (4096, 2048, 2048, True)])
 def test_gemm_nt(M, N, K, res, oracle_mod):
     from final_amd import hip, lfm
