@@ -62,7 +62,11 @@ int lfm_qk_norm_rope(float *qkv, int ld, const float *q_weight, const float *k_w
   if (batch < 0 || seq < 0 || heads <= 0 || kv_heads <= 0) return MOE_ERR_INVALID_ARG;
   if (batch == 0 || seq == 0) return MOE_OK;
   if (!qkv || !q_weight || !k_weight || !cos_table || !sin_table) return MOE_ERR_INVALID_ARG;
+  if (!al16(qkv) || !al16(q_weight) || !al16(k_weight) || !al16(cos_table) || !al16(sin_table) ||
+      ld % 4 != 0 || k_col % 4 != 0)
+    return MOE_ERR_INVALID_ARG;
   if (k_col < heads * 64 || ld < k_col + kv_heads * 64) return MOE_ERR_INVALID_ARG;
+  if (heads + kv_heads > 64) return MOE_ERR_UNSUPPORTED;
   return launch_status(lfm::launch_qk_norm_rope(qkv, ld, q_weight, k_weight, cos_table, sin_table,
                                                 batch, seq, heads, kv_heads, k_col, S(stream)));
 }

@@ -148,51 +148,79 @@ __global__ __launch_bounds__(moe::kNormThreads) void rmsnorm_rows_kernel(
 
 constexpr int kHeadDim = 64;
 
-// One wave per (token, head) row of 64.  The norm is rms_norm_kernel on a
-// 64-wide row launched with 256 threads (layer.cu:1146): threads 0..63 hold
-// one square each (fmaf(x, x, 0) = x*x), warps 0 and 1 fold theirs with
-// shuffle-down at 16..1, and the 8-warp fold adds warps 2..7's zeros, which
-// leaves warp0 + warp1.  Then rope_transpose_kernel's rotation (layer.cu:
-// 217-228) for position s = t % seq: out[d] = q1*c1 - q2*s1,
-// out[d+32] = q2*c2 + q1*s2 with q1 = x[d], q2 = x[d+32]; nvcc's contraction of
-// each line is restated as fmaf(first product, -/+ second product).
-constexpr int kRopeRows = 4;  // rows per wave (their loads in flight together)
+// One wave per token: its heads + kv_heads rows of 64 (q heads at columns
+// h*64, k heads at k_col + h*64), four rows per float4 load (16 lanes per
+// row, lane l holding elements 4(l%16)..4(l%16)+3), with the cos/sin row of
+// the token's position and both norm weights held in registers.  The norm is
+// rms_norm_kernel on a 64-wide row launched with 256 threads (layer.cu:1146):
+// threads 0..63 hold one square each (fmaf(x, x, 0) = x*x), warps 0 and 1
+// fold elements 0..31 and 32..63 with shuffle-down at 16..1, and the 8-warp
+// fold adds warps 2..7's zeros, which leaves warp0 + warp1.  The same binary
+// tree runs here over the float4 layout (16 -> 4 lanes down, 8 -> 2 lanes,
+// 4 -> 1 lane, then 2 and 1 across a lane's components), so every addition is
+// the reference's.  Then rope_transpose_kernel's rotation (layer.cu:217-228)
+// for position s = t % seq: out[d] = q1*c1 - q2*s1, out[d+32] = q2*c2 + q1*s2
+// with q1 = x[d], q2 = x[d+32] (element d + 32 is 8 lanes up); nvcc's
+// contraction of each line is restated as fmaf(first product, -/+ second
+// product).
+constexpr int kRopeTokens = 4;   // tokens per block, one per wave
+constexpr int kRopeGroups = 16;  // groups of 4 rows a wave holds: heads + kv_heads <= 64
 
 __global__ __launch_bounds__(256) void qk_norm_rope_kernel(float *qkv, int ld, const float *qw,
                                                            const float *kw, const float *cos_t,
-                                                           const float *sin_t, long long nrows,
-                                                           int seq, int heads, int per_tok,
-                                                           int k_col) {
+                                                           const float *sin_t, int ntok, int seq,
+                                                           int heads, int per_tok, int k_col) {
 #pragma clang fp contract(off)
-  const int lane = threadIdx.x & 63;
-  const long long row0 = ((long long)blockIdx.x * 4 + (threadIdx.x >> 6)) * kRopeRows;
-  float *p[kRopeRows];
-  float x[kRopeRows], wv[kRopeRows];
-  int pos[kRopeRows];
+  const int lane = threadIdx.x & 63, r = lane >> 4, c4 = (lane & 15) * 4;
+  const int t = blockIdx.x * kRopeTokens + (threadIdx.x >> 6);
+  if (t >= ntok) return;  // whole waves; the kernel has no block barrier
+  const int ng = (per_tok + 3) >> 2;
+  const int pos = t % seq;
+  const f32x4 cs = moe::ld4(cos_t + (size_t)pos * kHeadDim + c4);
+  const f32x4 sn = moe::ld4(sin_t + (size_t)pos * kHeadDim + c4);
+  const f32x4 wq = moe::ld4(qw + c4), wk = moe::ld4(kw + c4);
+  float *row0 = qkv + (size_t)t * ld;
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc(row0, 0, ld * (int)sizeof(float), moe::kBufferRsrcWord3);
+  // every load is unconditional (rows past per_tok read past the token's row:
+  // zeros), so all of a token's loads are in flight together
+  f32x4 x[kRopeGroups];
+  uint32_t off[kRopeGroups];
 #pragma unroll
-  for (int m = 0; m < kRopeRows; ++m) {
-    const long long row = min(row0 + m, nrows - 1);  // a wave past the end redoes the last row
-    const long long t = row / per_tok;
-    const int hd = (int)(row - t * per_tok);
-    const bool is_q = hd < heads;
-    p[m] = qkv + t * ld + (is_q ? hd * kHeadDim : k_col + (hd - heads) * kHeadDim);
-    pos[m] = (int)(t % seq);
-    x[m] = p[m][lane];
-    wv[m] = (is_q ? qw : kw)[lane];
+  for (int j = 0; j < kRopeGroups; ++j) {
+    const int row = 4 * j + r;
+    off[j] = row < per_tok ? (uint32_t)((row < heads ? row * kHeadDim : k_col + (row - heads) * kHeadDim) + c4) * 4u
+                           : 0x7FFFFFF0u;
+    x[j] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, off[j], 0, 0));
   }
-  if (row0 >= nrows) return;  // whole waves
 #pragma unroll
-  for (int m = 0; m < kRopeRows; ++m) {
-    float v = x[m] * x[m];
+  for (int j = 0; j < kRopeGroups; ++j) {
+    if (j >= ng) continue;  // wave-uniform
+    const int row = 4 * j + r;
+    f32x4 sq;
 #pragma unroll
-    for (int off = 16; off > 0; off >>= 1) v += __shfl_down(v, off, 32);
-    const float total = __shfl(v, 0) + __shfl(v, 32);
+    for (int i = 0; i < 4; ++i) sq[i] = x[j][i] * x[j][i];
+    f32x4 a, b, cc;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) a[i] = sq[i] + __shfl_down(sq[i], 4, 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = a[i] + __shfl_down(a[i], 2, 16);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cc[i] = b[i] + __shfl_down(b[i], 1, 16);
+    const float f = (cc[0] + cc[2]) + (cc[1] + cc[3]);
+    const float total = __shfl(f, 16 * r) + __shfl(f, 16 * r + 8);
     const float rms = 1.0f / sqrtf(total / (float)kHeadDim + moe::kNormEps);
-    const float y = (x[m] * rms) * wv[m];
-    const float c = cos_t[pos[m] * kHeadDim + lane], sn = sin_t[pos[m] * kHeadDim + lane];
-    const float other = __shfl_xor(y, 32);
-    const float o = lane < 32 ? __builtin_fmaf(y, c, -(other * sn)) : __builtin_fmaf(y, c, other * sn);
-    if (row0 + m < nrows) p[m][lane] = o;
+    const f32x4 w = row < heads ? wq : wk;
+    f32x4 y, other, o;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) y[i] = (x[j][i] * rms) * w[i];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) other[i] = __shfl_xor(y[i], 8);
+    const bool lo = (lane & 15) < 8;  // elements d < 32
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      o[i] = lo ? __builtin_fmaf(y[i], cs[i], -(other[i] * sn[i])) : __builtin_fmaf(y[i], cs[i], other[i] * sn[i]);
+    if (row < per_tok) __builtin_amdgcn_raw_buffer_store_b128(o, rs, off[j], 0, 0);
   }
 }
 
@@ -490,11 +518,11 @@ hipError_t launch_rmsnorm_rows(const float *x, long long x_stride, const float *
 hipError_t launch_qk_norm_rope(float *qkv, int ld, const float *qw, const float *kw,
                                const float *cos_t, const float *sin_t, int batch, int seq,
                                int heads, int kv_heads, int k_col, hipStream_t st) {
-  const long long nrows = (long long)batch * seq * (heads + kv_heads);
-  if (nrows <= 0) return hipSuccess;
-  const long long grid = (nrows + 4 * kRopeRows - 1) / (4 * kRopeRows);
+  const long long ntok = (long long)batch * seq;
+  if (ntok <= 0) return hipSuccess;
+  const long long grid = (ntok + kRopeTokens - 1) / kRopeTokens;
   hipLaunchKernelGGL(qk_norm_rope_kernel, dim3((unsigned)grid), dim3(256), 0, st, qkv, ld, qw, kw,
-                     cos_t, sin_t, nrows, seq, heads, heads + kv_heads, k_col);
+                     cos_t, sin_t, (int)ntok, seq, heads, heads + kv_heads, k_col);
   return hipGetLastError();
 }
 

@@ -63,7 +63,8 @@ int lfm_rmsnorm(const float *x, long long x_stride, const float *weight, float *
  * q_layernorm / k_layernorm of Attention::forward_gpu, layer.cu:1638-1642)
  * and rotated for position s = t % seq with cos/sin [>= seq][64]
  * (rope_transpose_kernel, layer.cu:195-231, without its transpose).
- * head_dim 64. */
+ * head_dim 64, heads + kv_heads <= 64; qkv, the weights and tables 16-byte
+ * aligned, ld and k_col multiples of 4. */
 int lfm_qk_norm_rope(float *qkv, int ld, const float *q_weight, const float *k_weight,
                      const float *cos_table, const float *sin_table, int batch, int seq,
                      int heads, int kv_heads, int k_col, moe_stream_t stream);
