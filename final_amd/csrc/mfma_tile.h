@@ -112,18 +112,25 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 //   kNarrow (64-row tiles whose valid rows fit the first 32-row block):
 //     instead of the second block's two waves idling on their SIMDs, each of
 //     the 4 waves takes all rows and one 32-column block.
-//   kSkinny1 / kSkinny3 (64-row tiles with 1-16 or 33-48 valid rows, which
-//     32-row blocks pad to twice or 4/3 the rows): v_mfma_f32_16x16x4_f32
-//     over 1 or 3 16-row blocks, each wave taking its 32 columns as two
-//     16-column blocks.
+//   kSkinny1 / kSkinny2 / kSkinny3 (64-row tiles with 1-16, 17-32 or 33-48
+//     valid rows, which 32-row blocks pad to twice or 4/3 the rows):
+//     v_mfma_f32_16x16x4_f32 over 1, 2 or 3 16-row blocks, each wave taking
+//     a quarter of the columns as 16-column blocks (the 2-block form serves
+//     the half-width tiles, which the narrow layout cannot split in four).
 // Same tile, LDS layout and products in every layout.
-enum TileLayout { kWide = 0, kNarrow = 1, kSkinny1 = 2, kSkinny3 = 3, kFull = 4 };
+enum TileLayout { kWide = 0, kNarrow = 1, kSkinny1 = 2, kSkinny3 = 3, kFull = 4, kSkinny2 = 5 };
 
 // 64x128 tiles: the 2 x 2 grid of 32x64 wave tiles.  (A 128-row tile with
 // at most 64 valid rows runs as a 64-row tile; its caller decides.)
 template <typename TL>
 constexpr bool tile_narrowable() {
   return TL::WAVES_M == 2 && TL::WAVES_N == 2 && TL::WM == 1 && TL::WN == 2;
+}
+// 64-row tiles of 4 waves whose columns split into 16-column blocks per wave
+// (64x128 and the half-width 64x64): the 16-row layouts.
+template <typename TL>
+constexpr bool tile_skinnyable() {
+  return TL::BM == 64 && TL::WAVES_M * TL::WAVES_N == 4 && TL::BN % 64 == 0;
 }
 
 // Slab loop of one tile: global loads NS slabs ahead in registers, LDS
@@ -140,9 +147,10 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
   constexpr int ROWS_PER_PASS = kThreads / TL::KV;
-  constexpr bool SKINNY = LAYOUT == kSkinny1 || LAYOUT == kSkinny3;
+  constexpr bool SKINNY = LAYOUT == kSkinny1 || LAYOUT == kSkinny2 || LAYOUT == kSkinny3;
   constexpr bool NARROW = LAYOUT == kNarrow;
-  static_assert(!(SKINNY || NARROW) || tile_narrowable<TL>(), "layouts of 64x128 tiles");
+  static_assert(!NARROW || tile_narrowable<TL>(), "narrow layout of 64x128 tiles");
+  static_assert(!SKINNY || tile_skinnyable<TL>(), "16-row layouts of 64-row tiles");
   float *As = lds;                      // [2][BM][PITCH]
   float *Bs = lds + 2 * BM * PITCH;     // [2][BN][PITCH]
   const int lane = threadIdx.x & 63;
@@ -162,18 +170,19 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   // skinny layout: lane l supplies row l % 16 at k offset 4 * (l / 16) of each
   // 16-wide k group, as a float4 whose component q feeds the q-th MFMA (the
   // same k permutation in A and B)
-  constexpr int SRB = LAYOUT == kSkinny3 ? 3 : 1;
+  constexpr int SRB = LAYOUT == kSkinny3 ? 3 : LAYOUT == kSkinny2 ? 2 : 1;
+  constexpr int SKC = BN / 64;  // 16-column blocks per wave
   const int l16 = lane & 15, k16 = (lane >> 4) * 4;
   const float *a16 = As + l16 * PITCH + k16;
-  const float *b16 = Bs + (wave * 32 + l16) * PITCH + k16;
+  const float *b16 = Bs + (wave * 16 * SKC + l16) * PITCH + k16;
 
   floatx16 acc[SKINNY ? 1 : WM][SKINNY ? 1 : WN];
-  f32x4 acc16[SRB][SKINNY ? 2 : 1];
+  f32x4 acc16[SRB][SKINNY ? SKC : 1];
   if constexpr (SKINNY) {
 #pragma unroll
     for (int i = 0; i < SRB; ++i)
 #pragma unroll
-      for (int c = 0; c < 2; ++c) acc16[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < SKC; ++c) acc16[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   } else {
 #pragma unroll
     for (int i = 0; i < WM; ++i)
@@ -218,17 +227,17 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
         const float *B16 = b16 + (u & 1) * BN * PITCH;
 #pragma unroll
         for (int g16 = 0; g16 < BK / 16; ++g16) {
-          f32x4 af[SRB], bf[2];
+          f32x4 af[SRB], bf[SKC];
 #pragma unroll
           for (int i = 0; i < SRB; ++i) af[i] = ld4(A16 + i * 16 * PITCH + g16 * 16);
 #pragma unroll
-          for (int c = 0; c < 2; ++c) bf[c] = ld4(B16 + c * 16 * PITCH + g16 * 16);
+          for (int c = 0; c < SKC; ++c) bf[c] = ld4(B16 + c * 16 * PITCH + g16 * 16);
 #pragma unroll
           for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int i = 0; i < SRB; ++i)
 #pragma unroll
-              for (int c = 0; c < 2; ++c)
+              for (int c = 0; c < SKC; ++c)
                 acc16[i][c] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i][q], bf[c][q], acc16[i][c], 0, 0, 0);
         }
       } else if (wrows > 0) {
@@ -275,10 +284,10 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
 #pragma unroll
     for (int i = 0; i < SRB; ++i)
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
+      for (int c = 0; c < SKC; ++c)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          Cs[(i * 16 + k16 + r) * CP + wave * 32 + c * 16 + l16] = acc16[i][c][r];
+          Cs[(i * 16 + k16 + r) * CP + wave * 16 * SKC + c * 16 + l16] = acc16[i][c][r];
   } else if (wrows > 0) {
     // 32x32 f32 MFMA result layout: lane l holds column l % 32 and rows
     // 8*(r/4) + 4*(l/32) + r%4 for r = 0..15
@@ -340,18 +349,21 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   const uint32_t bsrc = (uint32_t)(lrow * K + lc4) * 4u;
   const int lds_st = lrow * TL::PITCH + lc4;
 
-  constexpr bool kNa = tile_narrowable<TL>();
-  constexpr TileLayout kS1 = kNa ? kSkinny1 : kWide, kS3 = kNa ? kSkinny3 : kWide;
-  constexpr TileLayout kNw = kNa ? kNarrow : kWide;
+  constexpr bool kNa = tile_narrowable<TL>(), kSk = tile_skinnyable<TL>();
+  constexpr TileLayout kS1 = kSk ? kSkinny1 : kWide, kS2 = kSk ? kSkinny2 : kWide;
+  constexpr TileLayout kS3 = kSk ? kSkinny3 : kWide, kNw = kNa ? kNarrow : kWide;
   int next;
-  if (kNa && rows_valid <= 16)
+  if (kSk && rows_valid <= 16)
     next = tile_slabs<TL, kS1>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
-  else if (kNa && rows_valid > 32 && rows_valid <= 48)
+  else if (kSk && rows_valid > 32 && rows_valid <= 48)
     next = tile_slabs<TL, kS3>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
   else if (kNa && rows_valid <= 32)
     next = tile_slabs<TL, kNw>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head);
+  else if (kSk && rows_valid <= 32)
+    next = tile_slabs<TL, kS2>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
   else if (rows_valid >= BM)
     next = tile_slabs<TL, kFull>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,

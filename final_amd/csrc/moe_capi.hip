@@ -190,15 +190,18 @@ static int ctx_plan(const moe_ctx *ctx, int T) {
   return p == 0 && T > stream_max_tokens() ? 64 : p;
 }
 
-// 128-row MFMA plan: the last units' down tiles run as two half-width tiles,
-// about one block's worth each, so the last round of tiles is half as long
-// (T=4096: 3.01 -> 2.95 ms).  The 64-row plan has too few units for this:
-// most of its down tiles would be halves (T=256: 445 -> 456 us).
+// MFMA plans: the last units' down tiles run as two half-width tiles, so the
+// last round of tiles is about half as long.  128-row plan: about one
+// block's worth of half tiles (T=4096: 3.01 -> 2.95 ms).  64-row plan: half
+// that many units (its units are few; with every expert in one unit, the
+// longest-first order puts the smallest experts last): T=256 expert launch
+// 329 -> 311 us; one block's worth, 16 units at T=256, took as much there
+// and lost 2 % at T=128.
 static int tail_units(const moe_ctx *ctx, int tile_rows, int bn) {
   const int pi = plan_index(tile_rows);
-  if (tile_rows != 128 || pi < 0) return 0;
+  if ((tile_rows != 128 && tile_rows != 64) || pi < 0) return 0;
   const int half_tiles_per_unit = 2 * (ctx->d.hidden / bn);
-  const int k = ctx->grid[pi] / half_tiles_per_unit;
+  const int k = ctx->grid[pi] / half_tiles_per_unit / (tile_rows == 64 ? 2 : 1);
   return k > 0 ? k : 1;
 }
 
