@@ -170,8 +170,8 @@ static int plan_index(int rows) {
 }
 
 // Crossovers measured on MI355X with the seed-0 workload (whole-step times):
-// weight streaming is fastest up to 64 tokens (296 vs 302 us at 64), 64-row
-// MFMA tiles from 80 to 768 tokens (305 vs 321 us at 80, 315 vs 350 at 128,
+// weight streaming is fastest up to 64 tokens (295 vs 299 us at 64), 64-row
+// MFMA tiles from 72 to 768 tokens (300 vs 303 us at 72, 299 vs 322 at 80,
 // 800 vs 819 at 768), 128-row tiles from 896 (842 vs 876 us; 907 vs 958 at
 // 1024).
 // The dense FFN's 4 chunk experts each hold every token, so its MFMA plans
@@ -179,7 +179,7 @@ static int plan_index(int rows) {
 // vs 284 us at 128), 64-row tiles at 256 (303 vs 404 us), 128-row tiles from
 // 512 (433 vs 495 us).
 static int auto_plan(int T, bool stream_ok, bool dense) {
-  if (T <= (dense ? 192 : 72) && stream_ok) return 0;
+  if (T <= (dense ? 192 : 64) && stream_ok) return 0;
   if (T < (dense ? 384 : 832)) return 64;
   return 128;
 }

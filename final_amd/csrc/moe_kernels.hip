@@ -15,7 +15,7 @@
 //      a dispatch phase that assigns slots (replaces moe_scatter_kernel,
 //      layer.cu:501-542, without copying x), one dynamic task queue, the
 //      combine inside the down tiles; 64-row tiles up to 831 tokens,
-//      128-row tiles above.  T <= 72:
+//      128-row tiles above.  T <= 64:
 //      expert_ring_kernel, weight streaming through MFMA 16x16x4 f32 with
 //      round-robin tasks and slots assigned by the router.
 //
