@@ -115,9 +115,13 @@ def cpu_baseline(w, x, threads: int, single_tokens: int = 128, min_s: float = 0.
 
 
 def roofline(plan, flops, nbytes, ms, name):
-    """Primary bound of the expert kernel for its plan; the other bound too
-    when the arithmetic intensity is within 2x of the ridge (157.3/8 FLOP/B)."""
-    mfma_bound = plan != 0
+    """Primary bound of the expert kernel: MFMA when its arithmetic intensity
+    (algorithmic FLOP per algorithmic byte) is at or above the ridge
+    (157.3/8 FLOP/B), HBM below it; the other bound too when the intensity is
+    within 2x of the ridge."""
+    ridge = PEAK_MFMA_F32_TFLOPS * 1e3 / PEAK_HBM_GBS
+    ai = flops / max(nbytes, 1)
+    mfma_bound = ai >= ridge
     if mfma_bound:
         a = flops / (ms / 1e3) / 1e12
         roof = {"bound": "mfma", "achieved": round(a, 3), "peak": PEAK_MFMA_F32_TFLOPS,
@@ -126,8 +130,6 @@ def roofline(plan, flops, nbytes, ms, name):
         a = nbytes / (ms / 1e3) / 1e9
         roof = {"bound": "hbm", "achieved": round(a, 1), "peak": PEAK_HBM_GBS,
                 "unit": "GB/s", "frac": round(a / PEAK_HBM_GBS, 4)}
-    ai = flops / max(nbytes, 1)
-    ridge = PEAK_MFMA_F32_TFLOPS * 1e3 / PEAK_HBM_GBS
     if 0.5 <= ai / ridge <= 2.0:
         if mfma_bound:
             o = nbytes / (ms / 1e3) / 1e9
@@ -148,7 +150,7 @@ def roofline(plan, flops, nbytes, ms, name):
         if tr:
             roof["traffic"] = tr.get("bytes_per_launch")
             roof["traffic_source"] = TRAFFIC_SOURCE
-    roof["kernel"] = "expert_mfma_kernel<%d>" % plan if mfma_bound else "expert_ring_kernel"
+    roof["kernel"] = "expert_mfma_kernel<%d>" % plan if plan else "expert_ring_kernel"
     roof["kernel_ms"] = round(ms, 4)
     roof["per_launch"] = {"flop": flops} if mfma_bound else {"bytes": nbytes}
     return roof

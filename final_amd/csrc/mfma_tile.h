@@ -18,7 +18,7 @@ template <int BM> struct TileCfg;
 template <> struct TileCfg<128> {
   static constexpr int WAVES_M = 2, WM = 2, WAVES_N = 2, WN = 2, BK = 32, NS = 2;
 };
-// 64x128 tiles (65-831 tokens): 64x256 tiles left 1.4 tiles per block at
+// 64x128 tiles (49-831 tokens): 64x256 tiles left 1.4 tiles per block at
 // T=256 (637 us per step, 527 with 64x128); 64x64 tiles balance the blocks
 // better but lose more per tile (537 us at T=256, 1208 vs 1115 at T=1024)
 template <> struct TileCfg<64> {

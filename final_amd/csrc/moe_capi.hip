@@ -169,17 +169,18 @@ static int plan_index(int rows) {
   }
 }
 
-// Crossovers measured on MI355X with the seed-0 workload (whole-step times):
-// weight streaming is fastest up to 64 tokens (295 vs 299 us at 64), 64-row
-// MFMA tiles from 72 to 768 tokens (300 vs 303 us at 72, 299 vs 322 at 80,
-// 800 vs 819 at 768), 128-row tiles from 896 (842 vs 876 us; 907 vs 958 at
-// 1024).
+// Crossovers measured on MI355X with the seed-0 workload (whole-step times,
+// four weight copies cycled, clocks settled): weight streaming is fastest up
+// to 48 tokens (266 vs 276 us at 32, 279 vs 284 at 40, 284 vs 284 at 48),
+// 64-row MFMA tiles from 49 to 831 tokens (285 vs 288 us at 56, 286 vs 294
+// at 64, 782 vs 790 at 768), 128-row tiles from 832 (806 vs 822 us; 902 vs
+// 935 at 1024).
 // The dense FFN's 4 chunk experts each hold every token, so its MFMA plans
-// have few tiles at small T: streaming stays fastest up to ~192 tokens (220
-// vs 284 us at 128), 64-row tiles at 256 (303 vs 404 us), 128-row tiles from
-// 512 (433 vs 495 us).
+// have few tiles at small T: streaming stays fastest up to 192 tokens (214
+// vs 217 us at 128, 280 vs 283 at 192), 64-row tiles at 256 (290 vs 349 us),
+// 128-row tiles from 384 (433 vs 495 us at 512).
 static int auto_plan(int T, bool stream_ok, bool dense) {
-  if (T <= (dense ? 192 : 64) && stream_ok) return 0;
+  if (T <= (dense ? 192 : 48) && stream_ok) return 0;
   if (T < (dense ? 384 : 832)) return 64;
   return 128;
 }

@@ -14,6 +14,7 @@ constexpr int kTopK = 4;         // NUM_EXPERTS_PER_TOK, config.h:15
 constexpr int kMinRouterTokens = 8;  // smallest token block of the router
 constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
 constexpr int kCombineCols = 64;  // columns per combine counter (MFMA plans)
+constexpr int kRouterSlotTokens = 1024;  // MFMA plans up to this many tokens: the router assigns slots
 constexpr int kStreamRows = 16;  // weight rows per streaming-plan task (small batches)
 constexpr int kStreamWideTokens = 32;  // batches from this size use 64-row tasks
 // Streaming kernel shapes: tokens per MFMA pass; token passes of 16- and
@@ -49,6 +50,7 @@ struct Ctrl {
   int rtokens;      // tokens per router block (dispatch task size)
   int stream_rows;  // streaming plan: weight rows per task (16, 32 or 64)
   int max_count;    // tokens of the largest expert
+  int slots_assigned;  // MFMA plans: the router wrote every slot (pos = slot, slot_token)
   int tail_units;   // last units whose down tiles run as two half-width tiles
   int counts[kExperts];
   int offsets[kExperts + 1];

@@ -11,11 +11,11 @@
 //   2. expert kernel -- persistent, gate/up projection with the SwiGLU
 //      epilogue (layer.cu:773-972), down projection (layer.cu:974-1126) and
 //      the weighted top-4 combine with the residual add (layer.cu:695-721,
-//      1860-1880).  Large T: expert_mfma_kernel, MFMA 32x32x2 f32 tiles with
-//      a dispatch phase that assigns slots (replaces moe_scatter_kernel,
-//      layer.cu:501-542, without copying x), one dynamic task queue, the
-//      combine inside the down tiles; 64-row tiles up to 831 tokens,
-//      128-row tiles above.  T <= 64:
+//      1860-1880).  T > 48: expert_mfma_kernel, MFMA 32x32x2 f32 tiles with
+//      slots assigned by the router up to 1024 tokens, by a dispatch phase
+//      above (both replace moe_scatter_kernel, layer.cu:501-542, without
+//      copying x), one dynamic task queue, the combine inside the down
+//      tiles; 64-row tiles up to 831 tokens, 128-row tiles above.  T <= 48:
 //      expert_ring_kernel, weight streaming through MFMA 16x16x4 f32 with
 //      round-robin tasks and slots assigned by the router.
 //
@@ -272,7 +272,11 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
   }
   const int units = min(ps.units, a.max_units);
   for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
-  if (a.tile_rows == 0) {
+  // The streaming plan takes its slots from here, and so do the MFMA plans of
+  // small batches (a few slots per thread): their gate/up tiles then start
+  // without waiting for the expert kernel's dispatch tasks (T=256: ~7 us).
+  const bool router_slots = a.tile_rows == 0 || T <= kRouterSlotTokens;
+  if (router_slots) {
     __syncthreads();  // the block bases above are read back below
     // slot = token block base + in-block rank (stable by token), as the
     // dispatch tasks of the tiled plans compute it
@@ -282,13 +286,20 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
       int slot = -1;
       if (ee >= 0 && ee < kExperts) {
         slot = a.s.blk[(t / RT) * kExperts + ee] + a.s.pos[f];
-        if (slot >= 0 && slot < T * kTopK) a.s.slot_token[slot] = t;
-        else slot = -1;
+        if (slot >= 0 && slot < T * kTopK) {
+          a.s.slot_token[slot] = t;
+        } else {  // inconsistent plan: flag it, never write out of range
+          slot = -1;
+          __hip_atomic_store(&ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
       a.s.pos[f] = slot;
     }
   }
-  if (tid == 0) ctrl->router_done = 0;  // every token block has counted in
+  if (tid == 0) {
+    ctrl->router_done = 0;  // every token block has counted in
+    ctrl->slots_assigned = router_slots ? 1 : 0;
+  }
 }
 
 // Router.  A block computes the gate logits of RT tokens x (32/ES) experts as
@@ -745,12 +756,14 @@ __global__ __launch_bounds__(kThreads) void router_dense_kernel(RouterArgs a) {
 // Dispatch task q: slots of the 64 tokens of router block q (replaces
 // moe_scatter_kernel layer.cu:501-542: slot = block base + in-block rank, so
 // slots are stable by token; x itself is not copied, the GEMM gathers rows).
-__device__ void assign_task(const ExpertArgs &a, int q, int rt) {
+__device__ void assign_task(const ExpertArgs &a, int q, int rt, bool slots_ready) {
   const int tl = threadIdx.x >> 2, k = threadIdx.x & 3;
   const int tok = q * rt + tl;
   if (tl < rt && tok < a.T) {
     const int ee = a.s.idx[(size_t)tok * kTopK + k];
-    if (ee >= 0 && ee < kExperts) {
+    if (slots_ready) {
+      // the router assigned the slots (pos holds them already)
+    } else if (ee >= 0 && ee < kExperts) {
       const int slot = a.s.blk[q * kExperts + ee] + a.s.pos[(size_t)tok * kTopK + k];
       if (slot >= 0 && slot < a.T * kTopK) {
         st_agent(&a.s.pos[(size_t)tok * kTopK + k], slot);
@@ -968,12 +981,16 @@ void expert_mfma_kernel(ExpertArgs a) {
   __syncthreads();
   const UnitOrder uo{s_unit_off, s_full_off, s_pexp, s_counts, BM <= 64 ? s_nfull : 0,
                      BM <= 64 && s_lpt != 0};
+  // slots written by the router: gate/up tiles need not wait for the dispatch
+  // tasks, which then only clear the combine counters (down tiles wait for
+  // them) and write the rows of tokens without an expert
+  const bool slots_ready = c->slots_assigned != 0;
   int task = s_task;
   while (task < ntot) {
     int next = 0;  // the block's next task (thread 0), claimed near this one's end
     if (task < nb) {
       const int rt = c->rtokens;
-      assign_task(a, task, rt);
+      assign_task(a, task, rt, slots_ready);
       // this router block's tokens start with no expert outputs counted
       const int ncc = H / kCombineCols;
       for (int i = tid; i < rt * ncc; i += kThreads) {
@@ -988,7 +1005,7 @@ void expert_mfma_kernel(ExpertArgs a) {
       int e, m0, rows;
       unit_rows<BM>(u, uo, e, m0, rows);
       const int slot0 = s_offsets[e] + m0;
-      block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
+      if (!slots_ready) block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
       if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
       __syncthreads();
       const float *brow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TL::BN) * H;
@@ -1014,6 +1031,7 @@ void expert_mfma_kernel(ExpertArgs a) {
       int e, m0, rows;
       unit_rows<BM>(u, uo, e, m0, rows);
       const int slot0 = s_offsets[e] + m0;
+      block_wait(&c->assign_done, nb, a.wait_limit, &c->err);  // combine counters cleared
       block_wait(&a.s.dep[u], p1u, a.wait_limit, &c->err);
       if (tid < BM) s_aoff[tid] = tid < rows ? tid * I : -1;
       __syncthreads();

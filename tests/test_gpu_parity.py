@@ -146,31 +146,34 @@ def test_streaming_four_experts(block, real_weights, oracle_mod):
 @pytest.mark.gpu
 @pytest.mark.parametrize("T", [32, 40, 48, 57, 64])
 def test_streaming_wide_tasks(T, block, real_weights, oracle_mod):
-    """32-64 tokens under the weight-streaming plan: 64-row tasks, streamed as
-    four 16-row groups that reuse one load of the token rows when every expert
-    holds at most 16 tokens, else as four row groups at once over two token
-    passes (one expert made hot by a bias so it holds all T tokens)."""
+    """32-64 tokens under the weight-streaming plan (the automatic plan up to
+    48 tokens, forced above): 64-row tasks, streamed as four 16-row groups
+    that reuse one load of the token rows when every expert holds at most 16
+    tokens, else as four row groups at once over two token passes (one expert
+    made hot by a bias so it holds all T tokens)."""
     from final_amd import workloads as W
-    assert block.plan(T) == 0
-    x = W.gen_x(T, seed=40 + T)
-    say(f"[wide tasks] T={T} natural routing")
-    y = block.forward(x)
-    rt = block.last_routing()
-    ref = oracle_forward(oracle_mod, real_weights, x)
-    check_routing(rt, ref)
-    block.check_device()
-    np.testing.assert_allclose(y, ref["y"], rtol=RTOL, atol=ATOL)
-    w = dict(real_weights)
-    bias = np.array(real_weights["bias"], np.float32).copy()
-    bias[5] += 2.0
-    w["bias"] = bias
-    block.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+    assert block.plan(T) == (0 if T <= 48 else 64)
+    block.force_tile_rows(0)
     try:
-        say(f"[wide tasks] T={T} expert 5 hot")
+        x = W.gen_x(T, seed=40 + T)
+        say(f"[wide tasks] T={T} natural routing, plan=0")
+        y = block.forward(x)
+        rt = block.last_routing()
+        ref = oracle_forward(oracle_mod, real_weights, x)
+        check_routing(rt, ref)
+        block.check_device()
+        np.testing.assert_allclose(y, ref["y"], rtol=RTOL, atol=ATOL)
+        w = dict(real_weights)
+        bias = np.array(real_weights["bias"], np.float32).copy()
+        bias[5] += 2.0
+        w["bias"] = bias
+        block.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+        say(f"[wide tasks] T={T} expert 5 hot, plan=0")
         y = block.forward(x)
         rt = block.last_routing()
         block.check_device()
     finally:
+        block.force_tile_rows(-1)
         rw = real_weights
         block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
     ref = oracle_forward(oracle_mod, w, x)
