@@ -153,11 +153,27 @@ __device__ __forceinline__ float chain_dot(const float *gp, const float *xp, int
 // block's base within every expert, the units (tiles, or one per active
 // expert for the streaming plan), the expert kernel's task plan, and for the
 // streaming plan each slot's token (slot = block base + in-block rank).
+// The planning block holds up to kPlanRegBlocks token blocks per thread in
+// registers (nb <= 8 * kPlanRegBlocks), and then also keeps the block bases in
+// LDS for the slot assignment.
+constexpr int kPlanRegBlocks = 4;
+constexpr int kPlanLdsBlocks = 8 * kPlanRegBlocks;
+constexpr int kPlanSlotsPerThread = kRouterSlotTokens * kTopK / kThreads;
+
 struct PlanShared {
   int part[8][kExperts];
   int off[kExperts + 1];
   int cnt[kExperts];
   int units;
+  int base[kPlanLdsBlocks][kExperts];
+};
+
+// A planning block that routed the only token block itself passes its
+// routing from LDS instead of reading it back from memory.
+struct PlanLocal {
+  const int *cnt;              // [kExperts] tokens per expert
+  const int (*ids)[kTopK];     // [token][k] expert ids (-1: none)
+  const int (*rank)[kTopK];    // [token][k] in-block ranks
 };
 
 // Exclusive prefix sum over lanes 0..31 of a wave (lanes >= 32 idle).
@@ -173,7 +189,8 @@ __device__ __forceinline__ int lane_scan32(int v, int lane, int *total) {
 }
 
 template <int RT>
-__device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) {
+__device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
+                            const PlanLocal *loc = nullptr) {
   Ctrl *ctrl = a.s.ctrl;
   const int tid = threadIdx.x;
   const int e = tid & (kExperts - 1);
@@ -181,9 +198,21 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
   const int per = (nb + 7) / 8;
   const int lo = part * per;
   const int hi = min(nb, lo + per);
+  // small plans: each thread's token-block counts stay in registers (all
+  // loads in flight at once) and the block bases go to LDS as well
+  const bool in_regs = per <= kPlanRegBlocks;
+  int bv[kPlanRegBlocks];
   {
     int sum = 0;
-    for (int bb = lo; bb < hi; ++bb) sum += a.s.blk[bb * kExperts + e];
+    if (in_regs) {
+#pragma unroll
+      for (int i = 0; i < kPlanRegBlocks; ++i)
+        bv[i] = lo + i < hi ? (loc ? loc->cnt[e] : a.s.blk[(lo + i) * kExperts + e]) : 0;
+#pragma unroll
+      for (int i = 0; i < kPlanRegBlocks; ++i) sum += bv[i];
+    } else {
+      for (int bb = lo; bb < hi; ++bb) sum += a.s.blk[bb * kExperts + e];
+    }
     ps.part[part][e] = sum;
   }
   __syncthreads();
@@ -264,10 +293,21 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
   {
     // block bases: offsets[e] + tokens of e in earlier token blocks
     int base = ps.off[e] + ps.part[part][e];
-    for (int bb = lo; bb < hi; ++bb) {
-      const int c = a.s.blk[bb * kExperts + e];
-      a.s.blk[bb * kExperts + e] = base;
-      base += c;
+    if (in_regs) {
+#pragma unroll
+      for (int i = 0; i < kPlanRegBlocks; ++i) {
+        if (lo + i < hi) {
+          a.s.blk[(lo + i) * kExperts + e] = base;
+          ps.base[lo + i][e] = base;
+          base += bv[i];
+        }
+      }
+    } else {
+      for (int bb = lo; bb < hi; ++bb) {
+        const int c = a.s.blk[bb * kExperts + e];
+        a.s.blk[bb * kExperts + e] = base;
+        base += c;
+      }
     }
   }
   const int units = min(ps.units, a.max_units);
@@ -280,20 +320,55 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps) 
     __syncthreads();  // the block bases above are read back below
     // slot = token block base + in-block rank (stable by token), as the
     // dispatch tasks of the tiled plans compute it
-    for (int f = tid; f < T * kTopK; f += kThreads) {
-      const int t = f / kTopK;
-      const int ee = a.s.idx[f];
-      int slot = -1;
-      if (ee >= 0 && ee < kExperts) {
-        slot = a.s.blk[(t / RT) * kExperts + ee] + a.s.pos[f];
-        if (slot >= 0 && slot < T * kTopK) {
-          a.s.slot_token[slot] = t;
-        } else {  // inconsistent plan: flag it, never write out of range
-          slot = -1;
-          __hip_atomic_store(&ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int n = T * kTopK;
+    if (in_regs && n <= kThreads * kPlanSlotsPerThread) {
+      // every thread's (expert, rank) pairs loaded at once, bases from LDS
+      int id[kPlanSlotsPerThread], rk[kPlanSlotsPerThread];
+#pragma unroll
+      for (int i = 0; i < kPlanSlotsPerThread; ++i) {
+        const int f = tid + i * kThreads;
+        if (loc) {
+          id[i] = f < n ? loc->ids[f / kTopK][f % kTopK] : -1;
+          rk[i] = f < n ? loc->rank[f / kTopK][f % kTopK] : 0;
+        } else {
+          id[i] = f < n ? a.s.idx[f] : -1;
+          rk[i] = f < n ? a.s.pos[f] : 0;
         }
       }
-      a.s.pos[f] = slot;
+#pragma unroll
+      for (int i = 0; i < kPlanSlotsPerThread; ++i) {
+        const int f = tid + i * kThreads;
+        if (f < n) {
+          const int t = f / kTopK, ee = id[i];
+          int slot = -1;
+          if (ee >= 0 && ee < kExperts) {
+            slot = ps.base[t / RT][ee] + rk[i];
+            if (slot >= 0 && slot < n) {
+              a.s.slot_token[slot] = t;
+            } else {  // inconsistent plan: flag it, never write out of range
+              slot = -1;
+              __hip_atomic_store(&ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+          }
+          a.s.pos[f] = slot;
+        }
+      }
+    } else {
+      for (int f = tid; f < n; f += kThreads) {
+        const int t = f / kTopK;
+        const int ee = a.s.idx[f];
+        int slot = -1;
+        if (ee >= 0 && ee < kExperts) {
+          slot = a.s.blk[(t / RT) * kExperts + ee] + a.s.pos[f];
+          if (slot >= 0 && slot < n) {
+            a.s.slot_token[slot] = t;
+          } else {  // inconsistent plan: flag it, never write out of range
+            slot = -1;
+            __hip_atomic_store(&ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+        }
+        a.s.pos[f] = slot;
+      }
     }
   }
   if (tid == 0) {
@@ -338,6 +413,7 @@ void router_kernel(RouterArgs a) {
   __shared__ float s_score[RT][kExperts + 1];
   __shared__ float s_prob[RT][kExperts + 1];
   __shared__ int s_cnt[kExperts];
+  __shared__ float s_bias[kExperts];
   __shared__ PlanShared ps;
   __shared__ int s_flag;
 
@@ -348,6 +424,7 @@ void router_kernel(RouterArgs a) {
   const int el = tid % EPB, grp = tid / EPB;
   const bool chain_lane = grp * TPL < RT;
   Ctrl *ctrl = a.s.ctrl;
+  if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;  // the score bias
   fill_unwritten(a, blockIdx.x, gridDim.x, tid, kThreads);
 
   if (!FROM_LOGITS) {
@@ -433,6 +510,7 @@ void router_kernel(RouterArgs a) {
   } else if (!FROM_LOGITS) {
     __syncthreads();  // logits written by this block are read back below
   }
+  if (FROM_LOGITS) __syncthreads();  // s_bias written
   const float *lsrc = FROM_LOGITS ? a.logits_in : a.s.logits;
   for (int f = tid; f < RT * kExperts; f += kThreads) {
     const int tl = f / kExperts, e = f % kExperts;
@@ -448,7 +526,7 @@ void router_kernel(RouterArgs a) {
     }
     const float p = ref_sigmoid(l);
     s_prob[tl][e] = p;
-    s_score[tl][e] = p + (a.w.bias ? a.w.bias[e] : 0.0f);  // layer.cu:462
+    s_score[tl][e] = p + s_bias[e];  // layer.cu:462
   }
   __syncthreads();
 
@@ -466,28 +544,33 @@ void router_kernel(RouterArgs a) {
     }
     if (valid) {
       // Insertion with strict '>' (layer.cu:465-476): rank order is score
-      // descending, lower expert index first among equal scores.
+      // descending, lower expert index first among equal scores.  The list
+      // stays sorted (ms[0] >= ... >= ms[3], never NaN), so score > ms[i]
+      // implies score > ms[i+1], and the nested insertion is the selects
+      // below; all 32 scores and probabilities are read first, so no LDS
+      // read waits on a branch.
+      float sv[kExperts], pv[kExperts];
+#pragma unroll
       for (int ee = 0; ee < kExperts; ++ee) {
-        const float score = s_score[tl][ee];
-        const float prob = s_prob[tl][ee];
-        if (score > ms[3]) {
-          if (score > ms[2]) {
-            ms[3] = ms[2]; mp[3] = mp[2]; mi[3] = mi[2];
-            if (score > ms[1]) {
-              ms[2] = ms[1]; mp[2] = mp[1]; mi[2] = mi[1];
-              if (score > ms[0]) {
-                ms[1] = ms[0]; mp[1] = mp[0]; mi[1] = mi[0];
-                ms[0] = score; mp[0] = prob; mi[0] = ee;
-              } else {
-                ms[1] = score; mp[1] = prob; mi[1] = ee;
-              }
-            } else {
-              ms[2] = score; mp[2] = prob; mi[2] = ee;
-            }
-          } else {
-            ms[3] = score; mp[3] = prob; mi[3] = ee;
-          }
-        }
+        sv[ee] = s_score[tl][ee];
+        pv[ee] = s_prob[tl][ee];
+      }
+#pragma unroll
+      for (int ee = 0; ee < kExperts; ++ee) {
+        const float score = sv[ee], prob = pv[ee];
+        const bool c0 = score > ms[0], c1 = score > ms[1], c2 = score > ms[2], c3 = score > ms[3];
+        ms[3] = c2 ? ms[2] : (c3 ? score : ms[3]);
+        mp[3] = c2 ? mp[2] : (c3 ? prob : mp[3]);
+        mi[3] = c2 ? mi[2] : (c3 ? ee : mi[3]);
+        ms[2] = c1 ? ms[1] : (c2 ? score : ms[2]);
+        mp[2] = c1 ? mp[1] : (c2 ? prob : mp[2]);
+        mi[2] = c1 ? mi[1] : (c2 ? ee : mi[2]);
+        ms[1] = c0 ? ms[0] : (c1 ? score : ms[1]);
+        mp[1] = c0 ? mp[0] : (c1 ? prob : mp[1]);
+        mi[1] = c0 ? mi[0] : (c1 ? ee : mi[1]);
+        ms[0] = c0 ? score : ms[0];
+        mp[0] = c0 ? prob : mp[0];
+        mi[0] = c0 ? ee : mi[0];
       }
       float sum = 0.0f;  // layer.cu:480-482, rank order
 #pragma unroll
@@ -504,15 +587,11 @@ void router_kernel(RouterArgs a) {
     int rank[kTopK] = {-1, -1, -1, -1};
     const unsigned long long below = (1ull << tl) - 1ull;
     for (int ee = 0; ee < kExperts; ++ee) {
-      const bool sel = valid && (mi[0] == ee || mi[1] == ee || mi[2] == ee ||
-                                 mi[3] == ee);
+      const bool sel = valid & ((mi[0] == ee) | (mi[1] == ee) | (mi[2] == ee) | (mi[3] == ee));
       const unsigned long long m = __ballot(sel);
-      if (sel) {
-        const int r = __popcll(m & below);
+      const int r = __popcll(m & below);
 #pragma unroll
-        for (int i = 0; i < kTopK; ++i)
-          if (mi[i] == ee) rank[i] = r;
-      }
+      for (int i = 0; i < kTopK; ++i) rank[i] = mi[i] == ee ? r : rank[i];
       if (tl == 0) s_cnt[ee] = __popcll(m);
     }
     if (valid) {
@@ -566,6 +645,8 @@ void router_decode_kernel(RouterArgs a) {
   __shared__ PlanShared ps;
   __shared__ int s_flag;
   __shared__ float s_ngrp[kDecRT][kNormGroups], s_ntot[kDecRT];
+  __shared__ float s_bias[kExperts];
+  __shared__ int s_rank[kDecRT][kTopK], s_bcnt[kExperts];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tb = blockIdx.x / kDecES, es = blockIdx.x % kDecES;
@@ -573,6 +654,8 @@ void router_decode_kernel(RouterArgs a) {
   const int T = a.T, H = a.H, P = H + 4;
   const int nt = min(kDecRT, T - t0);
   float *gs = lds, *xs = lds + kDecEPB * P;
+  // the score bias, read now so the finishing block finds it in LDS
+  if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
 
   // 1. gate rows e0..e0+3 and token rows t0..t0+nt-1, 1 KiB per load
   {
@@ -644,7 +727,7 @@ void router_decode_kernel(RouterArgs a) {
     const float l = tvalid ? a.s.logits[(size_t)tok * kExperts + e] : 0.0f;
     const float p = ref_sigmoid(l);
     s_prob[tl][e] = p;
-    s_score[tl][e] = p + (a.w.bias ? a.w.bias[e] : 0.0f);  // layer.cu:462
+    s_score[tl][e] = p + s_bias[e];  // layer.cu:462
     if (e < kTopK) {  // rank slots no expert fills keep the reference's -1 / 0
       s_ti[tl][e] = -1;
       s_tp[tl][e] = 0.0f;
@@ -654,15 +737,19 @@ void router_decode_kernel(RouterArgs a) {
   // 5. rank of e in the token's order (score descending, lower index first).
   // The insertion only takes a score above its -1e30 sentinel (layer.cu:452,
   // 465), so NaN and scores <= -1e30 are never selected and never outrank
-  // another expert.
+  // another expert.  All 32 scores are read first and combined without
+  // branches (short-circuit tests made each read wait for the previous one).
   int sel = -1;
   {
+    float sv[kExperts];
+#pragma unroll
+    for (int j = 0; j < kExperts; ++j) sv[j] = s_score[tl][j];
     const float sc = s_score[tl][e];
     int r = 0;
 #pragma unroll
     for (int j = 0; j < kExperts; ++j) {
-      const float sj = s_score[tl][j];
-      r += sj > -1e30f && ((sj > sc) || (sj == sc && j < e));
+      const float sj = sv[j];
+      r += (int)((sj > -1e30f) & ((sj > sc) | ((sj == sc) & (j < e))));
     }
     if (tvalid && sc > -1e30f && r < kTopK) sel = r;
     s_sel[tl][e] = sel;
@@ -684,19 +771,34 @@ void router_decode_kernel(RouterArgs a) {
       a.s.wts[(size_t)(t0 + tid) * kTopK + i] = s_tp[tid][i] * scale * 1.0f;
     }
   }
-  // 7. in-block rank among the block's tokens that chose e, and counts
-  if (sel >= 0) {
-    int c = 0;
-    for (int t2 = 0; t2 < tl; ++t2) c += s_sel[t2][e] >= 0;
-    st_agent(&a.s.pos[(size_t)tok * kTopK + sel], c);
+  // 7. in-block rank among the block's tokens that chose e, and counts (rows
+  // of tokens past nt hold -1).  A single token block plans from LDS (its
+  // planning writes pos and blk itself).
+  const int nb = gridDim.x / kDecES;
+  {
+    int before = 0, all = 0;
+#pragma unroll
+    for (int t2 = 0; t2 < kDecRT; ++t2) {
+      const int chose = s_sel[t2][e] >= 0;
+      before += chose & (t2 < tl);
+      all += chose;
+    }
+    if (nb == 1) {
+      if (sel >= 0) s_rank[tl][sel] = before;
+      if (tl == 0) s_bcnt[e] = all;
+    } else {
+      if (sel >= 0) st_agent(&a.s.pos[(size_t)tok * kTopK + sel], before);
+      if (tl == 0) st_agent(&a.s.blk[tb * kExperts + e], all);
+    }
   }
-  if (tl == 0) {
-    int c = 0;
-    for (int t2 = 0; t2 < nt; ++t2) c += s_sel[t2][e] >= 0;
-    st_agent(&a.s.blk[tb * kExperts + e], c);
+  if (nb == 1) {
+    static_assert(kDecRT <= kRouterSlotTokens, "one token block: the plan assigns every slot");
+    __syncthreads();
+    const PlanLocal loc{s_bcnt, s_ti, s_rank};
+    router_plan<kDecRT>(a, 1, T, ps, &loc);
+    return;
   }
   // 8. the token block that finishes last plans
-  const int nb = gridDim.x / kDecES;
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (tid == 0) {
