@@ -485,9 +485,12 @@ static int check_tokens(const moe_ctx *ctx, int T) {
   return MOE_OK;
 }
 
+// defer: the caller launches the experts right after (moe_forward,
+// moe_forward_norm) with arguments already checked, so a single decode token
+// block under the streaming plan may leave its routing to the expert kernel.
 static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
                     moe_stream_t stream, const float *norm_w = nullptr,
-                    float *xn = nullptr) {
+                    float *xn = nullptr, bool defer = false) {
   if (!ctx || ctx->dense) return MOE_ERR_INVALID_ARG;
   int rc = check_tokens(ctx, T);
   if (rc) return rc;
@@ -514,6 +517,7 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   a.bn = expert_bn(a.tile_rows, T);
   a.tail_units = tail_units(ctx, a.tile_rows, a.bn);
   a.max_units = ctx->max_units;
+  a.defer = defer && !logits && router_can_defer(T, a.tile_rows, a.bn) ? 1 : 0;
   a.norm_w = norm_w;
   a.xn = xn;
   if (launch_router(a, logits != nullptr, static_cast<hipStream_t>(stream)) != hipSuccess)
@@ -572,9 +576,17 @@ int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
   return MOE_OK;
 }
 
+// The experts' pointer checks (moe_experts), so a forward can tell before
+// routing whether its experts launch will be accepted.
+static bool experts_args_ok(const float *x, const float *y, const float *residual) {
+  return x && y && aligned16(x) && aligned16(y) && (!residual || aligned16(residual)) && x != y;
+}
+
 int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
                 int num_tokens, moe_stream_t stream) {
-  int rc = moe_route(ctx, x, num_tokens, stream);
+  // routing is left to the expert kernel only when its launch follows
+  int rc = do_route(ctx, x, nullptr, num_tokens, stream, nullptr, nullptr,
+                    experts_args_ok(x, y, residual));
   if (rc) return rc;
   return moe_experts(ctx, x, y, residual, num_tokens, stream);
 }
@@ -754,7 +766,8 @@ int moe_forward_norm(moe_ctx *ctx, const float *h, float *out, int num_tokens,
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (router_fuses_norm(num_tokens)) {
     // the router normalises the rows it stages and stores them for the experts
-    rc = do_route(ctx, h, nullptr, num_tokens, stream, ctx->norm_w, ctx->xn);
+    rc = do_route(ctx, h, nullptr, num_tokens, stream, ctx->norm_w, ctx->xn,
+                  experts_args_ok(ctx->xn, out, h));
   } else {
     if (launch_rmsnorm(h, ctx->norm_w, ctx->xn, num_tokens, ctx->d.hidden, st) != hipSuccess)
       return MOE_ERR_HIP;

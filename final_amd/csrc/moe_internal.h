@@ -51,6 +51,7 @@ struct Ctrl {
   int stream_rows;  // streaming plan: weight rows per task (16, 32 or 64)
   int max_count;    // tokens of the largest expert
   int slots_assigned;  // MFMA plans: the router wrote every slot (pos = slot, slot_token)
+  int deferred;     // the router stopped after the logits; the streaming kernel routes and plans
   int tail_units;   // last units whose down tiles run as two half-width tiles
   int counts[kExperts];
   int offsets[kExperts + 1];
@@ -94,6 +95,7 @@ struct RouterArgs {
   int bn;                // MFMA n-tile width (columns of the B tile)
   int tail_units;        // MFMA plans: last units whose down tiles run at half width
   int max_units;
+  int defer;             // stop after the logits (router_can_defer); the expert kernel routes
   const float *norm_w;   // post-attention RMSNorm weight [H]: x is h, normalise it (decode router only)
   float *xn;             // [T][H]: the normalised rows, for the expert kernel
 };
@@ -133,6 +135,9 @@ int expert_blocks_per_cu(int tile_rows);
 // Columns of the B tile of the MFMA kernel, or weight rows per task of the
 // streaming kernel, for a plan and batch size.
 int expert_bn(int tile_rows, int T);
+// Whether a forward may leave routing and planning to the expert kernel: one
+// decode-router token block under the weight-streaming plan with 16-row tasks.
+bool router_can_defer(int T, int tile_rows, int bn);
 // Weight rows per streaming task for the dense FFN, whose chunks all hold T
 // tokens: 32-row tasks with 4 token passes above 32 tokens.
 int stream_rows_dense(int T);

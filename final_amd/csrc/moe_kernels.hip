@@ -17,7 +17,9 @@
 //      copying x), one dynamic task queue, the combine inside the down
 //      tiles; 64-row tiles up to 831 tokens, 128-row tiles above.  T <= 48:
 //      expert_ring_kernel, weight streaming through MFMA 16x16x4 f32 with
-//      round-robin tasks and slots assigned by the router.
+//      round-robin tasks and slots assigned by the router -- or, for a fused
+//      forward of at most 8 tokens, routed and planned by each of its own
+//      blocks from the router's logits (the router then stops after them).
 //
 // Phase dependencies are counters in the control block.  A task only waits
 // on tasks with a smaller index and every block runs its tasks in increasing
@@ -286,6 +288,7 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
       ctrl->tile_rows = tr;
       ctrl->head = 0;
       ctrl->assign_done = 0;
+      ctrl->deferred = 0;
       ps.units = units;
     }
   }
@@ -617,18 +620,108 @@ void router_kernel(RouterArgs a) {
   router_plan<RT>(a, nb, T, ps);
 }
 
+// Decode router shape: 8-token blocks, 4 experts per block, 8 blocks per token block.
+constexpr int kDecRT = 8, kDecEPB = 4, kDecES = kExperts / kDecEPB;
+
+// One token block's routing (up to kDecRT tokens x 32 experts) in LDS.
+struct RouteShared {
+  float score[kDecRT][kExperts + 1];
+  float prob[kDecRT][kExperts + 1];
+  int sel[kDecRT][kExperts];   // rank in the token's top-4, or -1
+  int ti[kDecRT][kTopK];       // expert ids in rank order (-1: rank left empty)
+  float tp[kDecRT][kTopK];     // their probabilities
+  float tw[kDecRT][kTopK];     // routing weights
+  int rank[kDecRT][kTopK];     // in-block rank among the block's tokens choosing ti
+  int cnt[kExperts];           // the block's tokens per expert
+};
+
+// Routing of nt <= kDecRT tokens from their logits (logit(t, e)), threads
+// 0..255 as (token tid / 32, expert tid % 32); every thread of the block
+// calls it (it holds barriers) and finds rs complete on return.
+//  - probability 1/(1+(float)exp(-(double)l)) (layer.cu:434), score = p + bias
+//    (bias in LDS, layer.cu:462);
+//  - top-4 as a rank: e is kept iff fewer than 4 selectable experts have a
+//    higher score or an equal score and a lower index, which is what the
+//    strict-'>' insertion of layer.cu:465-476 keeps; the insertion only takes
+//    a score above its -1e30 sentinel (layer.cu:452, 465), so NaN and scores
+//    <= -1e30 are never selected and never outrank another expert; all 32
+//    scores are read first and combined without branches (short-circuit
+//    tests made each LDS read wait for the previous one);
+//  - weights p * (1 / sum) * 1.0f, the sum in rank order (layer.cu:480-489);
+//  - in-block ranks (tokens of the block before this one that chose the
+//    same expert) and per-expert counts.
+template <typename Logit>
+__device__ __forceinline__ void route_token_block(RouteShared &rs, int nt, const float *bias,
+                                                  Logit logit) {
+#pragma clang fp contract(off)
+  const int tid = threadIdx.x;
+  const bool act = tid < kDecRT * kExperts;
+  const int tl = (tid >> 5) & (kDecRT - 1), e = tid & (kExperts - 1);
+  const bool tvalid = act && tl < nt;
+  if (act) {
+    const float l = tvalid ? logit(tl, e) : 0.0f;
+    const float p = ref_sigmoid(l);
+    rs.prob[tl][e] = p;
+    rs.score[tl][e] = p + bias[e];
+    if (e < kTopK) {  // rank slots no expert fills keep the reference's -1 / 0
+      rs.ti[tl][e] = -1;
+      rs.tp[tl][e] = 0.0f;
+    }
+  }
+  __syncthreads();
+  int sel = -1;
+  if (act) {
+    const float sc = rs.score[tl][e];
+    int r = 0;
+#pragma unroll
+    for (int j0 = 0; j0 < kExperts; j0 += 8) {  // 8 scores in flight at a time
+      float sv[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sv[j] = rs.score[tl][j0 + j];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float sj = sv[j];
+        r += (int)((sj > -1e30f) & ((sj > sc) | ((sj == sc) & (j0 + j < e))));
+      }
+    }
+    if (tvalid && sc > -1e30f && r < kTopK) sel = r;
+    rs.sel[tl][e] = sel;
+    if (sel >= 0) {
+      rs.ti[tl][sel] = e;
+      rs.tp[tl][sel] = rs.prob[tl][e];
+    }
+  }
+  __syncthreads();
+  if (tid < nt) {
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i) sum += rs.tp[tid][i];
+    const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;
+#pragma unroll
+    for (int i = 0; i < kTopK; ++i) rs.tw[tid][i] = rs.tp[tid][i] * scale * 1.0f;
+  }
+  if (act) {  // rows of tokens past nt hold -1
+    int before = 0, all = 0;
+#pragma unroll
+    for (int t2 = 0; t2 < kDecRT; ++t2) {
+      const int chose = rs.sel[t2][e] >= 0;
+      before += chose & (t2 < tl);
+      all += chose;
+    }
+    if (sel >= 0) rs.rank[tl][sel] = before;
+    if (tl == 0) rs.cnt[e] = all;
+  }
+  __syncthreads();
+}
+
 // Expert-split router (T <= 256).  A token block is 8 tokens; its 32 experts are
 // split over 8 blocks of 4, so 8x more CUs share the gate.  Each block copies
 // its 4 gate rows and the token rows whole into LDS with direct-to-LDS loads
 // (no chunk loop) and runs one FMA chain per (token, expert) lane (the
 // reference's order, layer.cu:109-127).  The last of a token block's blocks
-// finishes it with one thread per (token, expert): probability, score, and
-// the top-4 as a rank - the strict-'>' insertion of layer.cu:465-476 keeps an
-// expert exactly when fewer than 4 experts have a higher score or an equal
-// score and a lower index - then weights in rank order, in-block ranks and
-// counts.  The last token block plans.
-constexpr int kDecRT = 8, kDecEPB = 4, kDecES = kExperts / kDecEPB;
-
+// finishes it (route_token_block) and the last token block plans.  With
+// defer set (one token block, weight-streaming plan) the blocks stop after
+// the logits and the expert kernel routes and plans in its own blocks.
 __host__ __device__ constexpr size_t router_decode_lds(int H) {
   return (size_t)(kDecEPB + kDecRT) * (size_t)(H + 4) * sizeof(float);
 }
@@ -637,16 +730,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))
 void router_decode_kernel(RouterArgs a) {
 #pragma clang fp contract(off)
   extern __shared__ float lds[];  // gate rows [4][H + 4], then token rows [8][H + 4]
-  __shared__ float s_score[kDecRT][kExperts + 1];
-  __shared__ float s_prob[kDecRT][kExperts + 1];
-  __shared__ int s_sel[kDecRT][kExperts];  // rank in the token's top-4, or -1
-  __shared__ int s_ti[kDecRT][kTopK];
-  __shared__ float s_tp[kDecRT][kTopK];
+  __shared__ RouteShared rs;
   __shared__ PlanShared ps;
   __shared__ int s_flag;
   __shared__ float s_ngrp[kDecRT][kNormGroups], s_ntot[kDecRT];
   __shared__ float s_bias[kExperts];
-  __shared__ int s_rank[kDecRT][kTopK], s_bcnt[kExperts];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int tb = blockIdx.x / kDecES, es = blockIdx.x % kDecES;
@@ -656,6 +744,16 @@ void router_decode_kernel(RouterArgs a) {
   float *gs = lds, *xs = lds + kDecEPB * P;
   // the score bias, read now so the finishing block finds it in LDS
   if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
+  if (a.defer && blockIdx.x == 0 && tid == 0) {
+    // the streaming kernel routes and plans: its queue starts at 0
+    Ctrl *ctrl = a.s.ctrl;
+    ctrl->head = 0;
+    ctrl->deferred = 1;
+    ctrl->num_tokens = T;
+    ctrl->tile_rows = 0;
+    ctrl->n_rblocks = 0;
+    ctrl->stream_rows = a.bn;
+  }
 
   // 1. gate rows e0..e0+3 and token rows t0..t0+nt-1, 1 KiB per load
   {
@@ -707,6 +805,7 @@ void router_decode_kernel(RouterArgs a) {
     // waves 1-3, idle during the chains, prepare the expert kernel's rows
     fill_unwritten(a, blockIdx.x, gridDim.x, tid - 64, kThreads - 64);
   }
+  if (a.defer) return;  // logits only
   // 3. the last of the token block's 8 blocks finishes it
   __builtin_amdgcn_s_waitcnt(0);  // this block's logits are stored
   __syncthreads();
@@ -719,84 +818,28 @@ void router_decode_kernel(RouterArgs a) {
   }
   __syncthreads();
   if (!s_flag) return;
-  // 4. thread = (token tl, expert e): probability and score
-  const int tl = tid >> 5, e = tid & (kExperts - 1);
-  const int tok = t0 + tl;
-  const bool tvalid = tl < nt;
-  {
-    const float l = tvalid ? a.s.logits[(size_t)tok * kExperts + e] : 0.0f;
-    const float p = ref_sigmoid(l);
-    s_prob[tl][e] = p;
-    s_score[tl][e] = p + s_bias[e];  // layer.cu:462
-    if (e < kTopK) {  // rank slots no expert fills keep the reference's -1 / 0
-      s_ti[tl][e] = -1;
-      s_tp[tl][e] = 0.0f;
-    }
-  }
-  __syncthreads();
-  // 5. rank of e in the token's order (score descending, lower index first).
-  // The insertion only takes a score above its -1e30 sentinel (layer.cu:452,
-  // 465), so NaN and scores <= -1e30 are never selected and never outrank
-  // another expert.  All 32 scores are read first and combined without
-  // branches (short-circuit tests made each read wait for the previous one).
-  int sel = -1;
-  {
-    float sv[kExperts];
-#pragma unroll
-    for (int j = 0; j < kExperts; ++j) sv[j] = s_score[tl][j];
-    const float sc = s_score[tl][e];
-    int r = 0;
-#pragma unroll
-    for (int j = 0; j < kExperts; ++j) {
-      const float sj = sv[j];
-      r += (int)((sj > -1e30f) & ((sj > sc) | ((sj == sc) & (j < e))));
-    }
-    if (tvalid && sc > -1e30f && r < kTopK) sel = r;
-    s_sel[tl][e] = sel;
-    if (sel >= 0) {
-      s_ti[tl][sel] = e;
-      s_tp[tl][sel] = s_prob[tl][e];
-    }
-  }
-  __syncthreads();
-  // 6. weights: sum in rank order (layer.cu:480-489)
+  // 4-7. probabilities, top-4, weights, in-block ranks and counts
+  const float *lg = a.s.logits + (size_t)t0 * kExperts;
+  route_token_block(rs, nt, s_bias, [lg](int t, int ee) { return lg[t * kExperts + ee]; });
+  const int nb = gridDim.x / kDecES;
   if (tid < nt) {
-    float sum = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kTopK; ++i) sum += s_tp[tid][i];
-    const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;
 #pragma unroll
     for (int i = 0; i < kTopK; ++i) {
-      st_agent(&a.s.idx[(size_t)(t0 + tid) * kTopK + i], s_ti[tid][i]);
-      a.s.wts[(size_t)(t0 + tid) * kTopK + i] = s_tp[tid][i] * scale * 1.0f;
+      st_agent(&a.s.idx[(size_t)(t0 + tid) * kTopK + i], rs.ti[tid][i]);
+      a.s.wts[(size_t)(t0 + tid) * kTopK + i] = rs.tw[tid][i];
     }
   }
-  // 7. in-block rank among the block's tokens that chose e, and counts (rows
-  // of tokens past nt hold -1).  A single token block plans from LDS (its
-  // planning writes pos and blk itself).
-  const int nb = gridDim.x / kDecES;
-  {
-    int before = 0, all = 0;
-#pragma unroll
-    for (int t2 = 0; t2 < kDecRT; ++t2) {
-      const int chose = s_sel[t2][e] >= 0;
-      before += chose & (t2 < tl);
-      all += chose;
-    }
-    if (nb == 1) {
-      if (sel >= 0) s_rank[tl][sel] = before;
-      if (tl == 0) s_bcnt[e] = all;
-    } else {
-      if (sel >= 0) st_agent(&a.s.pos[(size_t)tok * kTopK + sel], before);
-      if (tl == 0) st_agent(&a.s.blk[tb * kExperts + e], all);
-    }
-  }
-  if (nb == 1) {
+  if (nb == 1) {  // a single token block plans from LDS (its plan writes pos and blk)
     static_assert(kDecRT <= kRouterSlotTokens, "one token block: the plan assigns every slot");
-    __syncthreads();
-    const PlanLocal loc{s_bcnt, s_ti, s_rank};
+    const PlanLocal loc{rs.cnt, rs.ti, rs.rank};
     router_plan<kDecRT>(a, 1, T, ps, &loc);
     return;
+  }
+  {
+    const int tl = tid >> 5, e = tid & (kExperts - 1);
+    const int sel = rs.sel[tl][e];
+    if (sel >= 0) st_agent(&a.s.pos[(size_t)(t0 + tl) * kTopK + sel], rs.rank[tl][sel]);
+    if (tl == 0) st_agent(&a.s.blk[tb * kExperts + e], rs.cnt[e]);
   }
   // 8. the token block that finishes last plans
   __builtin_amdgcn_s_waitcnt(0);
@@ -1240,6 +1283,9 @@ struct RingShared {
   int abort;
   int seq[8];              // the block's j-th row task id at seq[j & 7]
   int nseq;                // row task ids published so far
+  int local;               // routing computed by this block (deferred router)
+  int rpos[kDecRT][kTopK]; // local routing: slot of each (token, rank), -1: none
+  float rw[kDecRT][kTopK]; // local routing: weights
 };
 
 __device__ __forceinline__ int lds_load(const int *p) {
@@ -1512,12 +1558,13 @@ struct RingRoute {
   float w[kTopK];
 };
 
-__device__ __forceinline__ RingRoute ring_route(const ExpertArgs &a, int tok) {
+__device__ __forceinline__ RingRoute ring_route(const ExpertArgs &a, const RingShared &sh, int tok) {
   RingRoute r;
+  const bool local = sh.local != 0;
 #pragma unroll
   for (int k = 0; k < kTopK; ++k) {
-    int slot = a.s.pos[(size_t)tok * kTopK + k];
-    float w = a.s.wts[(size_t)tok * kTopK + k];
+    int slot = local ? sh.rpos[tok][k] : a.s.pos[(size_t)tok * kTopK + k];
+    float w = local ? sh.rw[tok][k] : a.s.wts[(size_t)tok * kTopK + k];
     if (slot < 0 || slot >= a.T * kTopK) {
       slot = -1;
       w = 0.0f;
@@ -1734,7 +1781,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
   // combine tasks (one token each), after every row task, with the ring's
   // registers free
   for (int tok = blockIdx.x; ok && tok < pl.ncomb; tok += pl.grid)
-    ok = ring_combine(a, tok, ring_route(a, tok), (int)threadIdx.x, &sh.abort, err, ticks);
+    ok = ring_combine(a, tok, ring_route(a, sh, tok), (int)threadIdx.x, &sh.abort, err, ticks);
 }
 
 // Control side: sums the 8 k-slice partials of item (t, g) and stores the
@@ -1855,19 +1902,17 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
                 "row length");
   extern __shared__ float res[];  // partials, ring_res_bytes(row groups, passes)
   __shared__ RingShared sh;
+  __shared__ RouteShared rsh;  // deferred routing only
+  __shared__ float s_bias[kExperts];
+  __shared__ int s_nact, s_maxcnt;
   const Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
-  if (tid < kExperts) {
-    sh.active[tid] = c->active[tid];
-    sh.counts[tid] = c->counts[tid];
-    sh.offsets[tid] = c->offsets[tid];
-  }
-  const int nslots = min(a.T * kTopK, kRingMaxSlots);
-  for (int i = tid; i < nslots; i += kRingThreads) sh.tok[i] = a.s.slot_token[i];
+  const bool local = c->deferred != 0;  // the router stopped after the logits
   if (tid < 2) sh.done[tid] = 0;
   if (tid == 0) {
     sh.flushed = 0;
     sh.abort = 0;
+    sh.local = local ? 1 : 0;
     // every task, the first included, is claimed from the queue, so only a
     // block that is running owns one (blocks not yet resident own nothing
     // another block waits for)
@@ -1875,32 +1920,107 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     sh.nseq = 1;
   }
   RingPlan pl;
-  pl.n1 = c->n_p1;
-  pl.n2 = c->n_p2;
   pl.ncomb = a.T;  // combine tasks: one per token
-  pl.p1u = c->p1_per_unit;
-  pl.p2u = c->p2_per_unit;
   pl.grid = gridDim.x;
-  pl.rows = __builtin_amdgcn_readfirstlane(c->stream_rows);
-  const int maxcnt = __builtin_amdgcn_readfirstlane(c->max_count);
-  // 64-row tasks of experts holding at most 16 tokens are streamed as four
-  // 16-row sub-groups; the router then plans the last units' down rows as
-  // 16-row tasks (tail_units), so the last round of tasks is short
-  const bool seq = pl.rows == kStreamRows * kRingWideGroups && maxcnt <= kRingTokens;
-  pl.sub = seq ? kRingWideGroups : 1;
-  {
-    const int units = pl.n1 / max(pl.p1u, 1);
-    const int tail = seq ? __builtin_amdgcn_readfirstlane(c->tail_units) : 0;
-    pl.tail_u0 = units - tail;
-    pl.tail_q = (units - tail) * pl.p2u;
-  }
-  // plans for this kernel take their slots from the router, and a task
-  // covers 16, 32 or 64 rows
-  if (c->n_rblocks != 0 ||
-      (pl.rows != kStreamRows && pl.rows != kStreamRows * kRingWideGroups &&
-       pl.rows != kStreamRows * kRingDenseGroups)) {
-    if (tid == 0) st_agent(&a.s.ctrl->err, 2);
-    return;
+  int maxcnt;
+  if (local) {
+    // One token block (T <= 8), 16-row tasks: every block routes the tokens
+    // from the logits and plans the launch itself, as the router's last
+    // block would (same functions, same order), and block 0 publishes the
+    // routing for the host.  Slot = offsets[e] + in-block rank.
+    if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
+    __syncthreads();
+    const float *lg = a.s.logits;
+    route_token_block(rsh, a.T, s_bias, [lg](int t, int e) { return lg[t * kExperts + e]; });
+    if (tid < kExperts) {  // lanes 0-31 of wave 0
+      const int cnt = rsh.cnt[tid];
+      int total = 0;
+      const int off = lane_scan32(cnt, tid, &total);
+      int mc = cnt;
+#pragma unroll
+      for (int o = 16; o > 0; o >>= 1) mc = max(mc, __shfl_xor(mc, o, 32));
+      const unsigned long long act = __ballot(cnt > 0);
+      const int nact = __popcll(act);
+      const int aidx = __popcll(act & ((1ull << tid) - 1ull));
+      sh.counts[tid] = cnt;
+      sh.offsets[tid] = off;
+      if (cnt > 0) sh.active[aidx] = tid;
+      if (tid >= nact) sh.active[tid] = -1;
+      if (tid == 0) {
+        s_nact = nact;
+        s_maxcnt = mc;
+      }
+      if (blockIdx.x == 0) {
+        Ctrl *cw = a.s.ctrl;
+        cw->counts[tid] = cnt;
+        cw->offsets[tid] = off;
+        if (cnt > 0) cw->active[aidx] = tid;
+        if (tid >= nact) cw->active[tid] = -1;
+        if (tid == 0) {
+          cw->offsets[kExperts] = total;
+          cw->n_active = nact;
+          cw->max_count = mc;
+        }
+      }
+    }
+    __syncthreads();
+    if (tid < a.T * kTopK) {
+      const int t = tid / kTopK, k = tid % kTopK;
+      const int e = rsh.ti[t][k];
+      const int slot = e >= 0 ? sh.offsets[e] + rsh.rank[t][k] : -1;
+      if (slot >= 0) sh.tok[slot] = t;
+      sh.rpos[t][k] = slot;
+      sh.rw[t][k] = rsh.tw[t][k];
+      if (blockIdx.x == 0) {
+        st_agent(&a.s.idx[tid], e);
+        a.s.wts[tid] = rsh.tw[t][k];
+        st_agent(&a.s.pos[tid], slot);
+        if (slot >= 0) st_agent(&a.s.slot_token[slot], t);
+      }
+    }
+    const int units = s_nact;  // read after the barrier above
+    pl.rows = kStreamRows;
+    pl.p1u = a.I / (kStreamRows / 2);
+    pl.p2u = a.H / kStreamRows;
+    pl.n1 = units * pl.p1u;
+    pl.n2 = units * pl.p2u;
+    pl.sub = 1;
+    pl.tail_u0 = units;
+    pl.tail_q = units * pl.p2u;
+    maxcnt = __builtin_amdgcn_readfirstlane(s_maxcnt);
+  } else {
+    if (tid < kExperts) {
+      sh.active[tid] = c->active[tid];
+      sh.counts[tid] = c->counts[tid];
+      sh.offsets[tid] = c->offsets[tid];
+    }
+    const int nslots = min(a.T * kTopK, kRingMaxSlots);
+    for (int i = tid; i < nslots; i += kRingThreads) sh.tok[i] = a.s.slot_token[i];
+    pl.n1 = c->n_p1;
+    pl.n2 = c->n_p2;
+    pl.p1u = c->p1_per_unit;
+    pl.p2u = c->p2_per_unit;
+    pl.rows = __builtin_amdgcn_readfirstlane(c->stream_rows);
+    maxcnt = __builtin_amdgcn_readfirstlane(c->max_count);
+    // 64-row tasks of experts holding at most 16 tokens are streamed as four
+    // 16-row sub-groups; the router then plans the last units' down rows as
+    // 16-row tasks (tail_units), so the last round of tasks is short
+    const bool seq = pl.rows == kStreamRows * kRingWideGroups && maxcnt <= kRingTokens;
+    pl.sub = seq ? kRingWideGroups : 1;
+    {
+      const int units = pl.n1 / max(pl.p1u, 1);
+      const int tail = seq ? __builtin_amdgcn_readfirstlane(c->tail_units) : 0;
+      pl.tail_u0 = units - tail;
+      pl.tail_q = (units - tail) * pl.p2u;
+    }
+    // plans for this kernel take their slots from the router, and a task
+    // covers 16, 32 or 64 rows
+    if (c->n_rblocks != 0 ||
+        (pl.rows != kStreamRows && pl.rows != kStreamRows * kRingWideGroups &&
+         pl.rows != kStreamRows * kRingDenseGroups)) {
+      if (tid == 0) st_agent(&a.s.ctrl->err, 2);
+      return;
+    }
   }
   __syncthreads();
   const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
@@ -2082,6 +2202,10 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
 
 int stream_rows_dense(int T) {
   return T > 2 * kRingTokens ? kStreamRows * kRingDenseGroups : expert_bn(0, T);
+}
+
+bool router_can_defer(int T, int tile_rows, int bn) {
+  return T >= 1 && T <= kDecRT && T <= kSplitRouterTokens && tile_rows == 0 && bn == kStreamRows;
 }
 
 int expert_bn(int tile_rows, int T) {

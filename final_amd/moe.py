@@ -111,8 +111,14 @@ class SparseMoeBlock:
         return out
 
     def forward_gpu(self, x, y, num_tokens: int, residual=None, stream=None) -> None:
-        self.route(x, num_tokens, stream)
-        self.experts(x, y, num_tokens, residual=residual, stream=stream)
+        """Route then run the experts (one moe_forward call, so a single
+        decode token block may route inside the expert kernel)."""
+        rc = _native.lib().moe_forward(self._ctx, _ptr(x), _ptr(y), _ptr(residual),
+                                       int(num_tokens), _stream(stream))
+        # the route may have succeeded before the experts call failed; a
+        # stale count can only make a read-back fail (the C side checks it)
+        self._routed_T = int(num_tokens)
+        _native.check(rc, "moe_forward")
 
     def route(self, x, num_tokens: int, stream=None) -> None:
         _native.check(_native.lib().moe_route(self._ctx, _ptr(x), int(num_tokens), _stream(stream)),

@@ -82,7 +82,10 @@ int moe_set_weights(moe_ctx *ctx, const float *gate, const float *bias,
  * residual != NULL, the residual add_kernel after it (layer.cu:1917-1918).
  * x, y, residual: device [num_tokens][hidden] fp32, 16-byte aligned; y may
  * alias residual (in-place residual add) but not x.  Asynchronous on `stream`;
- * no host synchronisation inside. num_tokens == 0 is a no-op. */
+ * no host synchronisation inside. num_tokens == 0 is a no-op.  Same results
+ * as moe_route + moe_experts; for batches of up to 8 tokens under the
+ * weight-streaming plan the routing completes inside the experts launch
+ * (moe_last_routing reads it after either). */
 int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
                 int num_tokens, moe_stream_t stream);
 

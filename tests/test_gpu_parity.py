@@ -307,3 +307,53 @@ def test_readback_checks_token_count(block, real_weights):
     assert block.last_routing()["idx"].shape == (40, 4)
     assert L.moe_last_routing(block._ctx, idx.ctypes.data, None, None, None, 8,
                               None) == _native.MOE_ERR_INVALID_ARG
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_forward_routes_in_expert_kernel(T, block, real_weights, oracle_mod):
+    """One decode token block under the streaming plan: moe_forward lets the
+    router stop after the logits and the expert kernel route and plan in its
+    own blocks.  Its routing (idx, w, counts, logits) and y must be
+    bit-identical to moe_route + moe_experts, where the router finishes and
+    plans, and match the oracle.  A hot expert (bias +10) makes several
+    tokens share an expert, so the in-block ranks and slots are exercised."""
+    from final_amd import hip
+    from final_amd import workloads as W
+    w = dict(real_weights)
+    bias = np.array(real_weights["bias"], np.float32).copy()
+    bias[11] += 10.0
+    w["bias"] = bias
+    block.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+    try:
+        assert block.plan(T) == 0
+        x = W.gen_x(T, seed=60 + T)
+        r = W.gen_x(T, seed=70 + T)
+        dx = hip.DeviceArray.from_numpy(x)
+        dr = hip.DeviceArray.from_numpy(r)
+        say(f"[deferred routing] T={T} moe_forward")
+        dy1 = hip.DeviceArray((T, W.H))
+        block.forward_gpu(dx, dy1, T, residual=dr)
+        hip.synchronize()
+        block.check_device()
+        rt1 = block.last_routing()
+        say(f"[deferred routing] T={T} moe_route + moe_experts")
+        dy2 = hip.DeviceArray((T, W.H))
+        block.route(dx, T)
+        block.experts(dx, dy2, T, residual=dr)
+        hip.synchronize()
+        block.check_device()
+        rt2 = block.last_routing()
+    finally:
+        rw = real_weights
+        block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
+    y1, y2 = dy1.download(), dy2.download()
+    assert np.array_equal(bits(y1), bits(y2))
+    for k in ("idx", "counts"):
+        assert np.array_equal(rt1[k], rt2[k])
+    for k in ("w", "logits"):
+        assert np.array_equal(bits(rt1[k]), bits(rt2[k]))
+    assert rt1["counts"][11] == T
+    ref = oracle_forward(oracle_mod, w, x, residual=r)
+    check_routing(rt1, ref)
+    np.testing.assert_allclose(y1, ref["y"], rtol=RTOL, atol=ATOL)
