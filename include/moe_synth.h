@@ -1,8 +1,8 @@
 /*
  * moe_synth.h -- seeded synthetic workloads for the MoE block (host side).
  *
- * No counterpart in the reference (it has no data files, SURVEY of the tree:
- * data/ and model.bin are absent).  The benchmarks and tests fill weights and
+ * No counterpart in the reference (its tree holds no data files: data/ and
+ * model.bin are absent).  The benchmarks and tests fill weights and
  * activations with these generators so that every process, on any host,
  * produces bit-identical inputs from (seed, stream, index):
  *
