@@ -155,11 +155,12 @@ __device__ __forceinline__ float chain_dot(const float *gp, const float *xp, int
 // block's base within every expert, the units (tiles, or one per active
 // expert for the streaming plan), the expert kernel's task plan, and for the
 // streaming plan each slot's token (slot = block base + in-block rank).
-// The planning block holds up to kPlanRegBlocks token blocks per thread in
-// registers (nb <= 8 * kPlanRegBlocks), and then also keeps the block bases in
-// LDS for the slot assignment.
-constexpr int kPlanRegBlocks = 4;
-constexpr int kPlanLdsBlocks = 8 * kPlanRegBlocks;
+// The planning block reads each thread's token-block counts in batches of
+// kPlanRegBlocks (every load of a batch in flight at once); up to one batch
+// per thread they stay in registers, and up to kPlanLdsBlocks token blocks the
+// block bases are also kept in LDS for the slot assignment.
+constexpr int kPlanRegBlocks = 8;
+constexpr int kPlanLdsBlocks = 32;
 constexpr int kPlanSlotsPerThread = kRouterSlotTokens * kTopK / kThreads;
 
 struct PlanShared {
@@ -200,20 +201,18 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
   const int per = (nb + 7) / 8;
   const int lo = part * per;
   const int hi = min(nb, lo + per);
-  // small plans: each thread's token-block counts stay in registers (all
-  // loads in flight at once) and the block bases go to LDS as well
+  // one batch per thread: the counts stay in registers for the block bases
   const bool in_regs = per <= kPlanRegBlocks;
+  const bool bases_lds = nb <= kPlanLdsBlocks;
   int bv[kPlanRegBlocks];
   {
     int sum = 0;
-    if (in_regs) {
+    for (int b0 = lo; b0 < hi; b0 += kPlanRegBlocks) {
 #pragma unroll
       for (int i = 0; i < kPlanRegBlocks; ++i)
-        bv[i] = lo + i < hi ? (loc ? loc->cnt[e] : a.s.blk[(lo + i) * kExperts + e]) : 0;
+        bv[i] = b0 + i < hi ? (loc ? loc->cnt[e] : a.s.blk[(b0 + i) * kExperts + e]) : 0;
 #pragma unroll
       for (int i = 0; i < kPlanRegBlocks; ++i) sum += bv[i];
-    } else {
-      for (int bb = lo; bb < hi; ++bb) sum += a.s.blk[bb * kExperts + e];
     }
     ps.part[part][e] = sum;
   }
@@ -296,20 +295,19 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
   {
     // block bases: offsets[e] + tokens of e in earlier token blocks
     int base = ps.off[e] + ps.part[part][e];
-    if (in_regs) {
+    for (int b0 = lo; b0 < hi; b0 += kPlanRegBlocks) {
+      if (!in_regs) {  // several batches: read this one's counts again
+#pragma unroll
+        for (int i = 0; i < kPlanRegBlocks; ++i)
+          bv[i] = b0 + i < hi ? a.s.blk[(b0 + i) * kExperts + e] : 0;
+      }
 #pragma unroll
       for (int i = 0; i < kPlanRegBlocks; ++i) {
-        if (lo + i < hi) {
-          a.s.blk[(lo + i) * kExperts + e] = base;
-          ps.base[lo + i][e] = base;
+        if (b0 + i < hi) {
+          a.s.blk[(b0 + i) * kExperts + e] = base;
+          if (bases_lds) ps.base[b0 + i][e] = base;
           base += bv[i];
         }
-      }
-    } else {
-      for (int bb = lo; bb < hi; ++bb) {
-        const int c = a.s.blk[bb * kExperts + e];
-        a.s.blk[bb * kExperts + e] = base;
-        base += c;
       }
     }
   }
@@ -324,7 +322,7 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
     // slot = token block base + in-block rank (stable by token), as the
     // dispatch tasks of the tiled plans compute it
     const int n = T * kTopK;
-    if (in_regs && n <= kThreads * kPlanSlotsPerThread) {
+    if (bases_lds && n <= kThreads * kPlanSlotsPerThread) {
       // every thread's (expert, rank) pairs loaded at once, bases from LDS
       int id[kPlanSlotsPerThread], rk[kPlanSlotsPerThread];
 #pragma unroll
@@ -515,19 +513,27 @@ void router_kernel(RouterArgs a) {
   }
   if (FROM_LOGITS) __syncthreads();  // s_bias written
   const float *lsrc = FROM_LOGITS ? a.logits_in : a.s.logits;
-  for (int f = tid; f < RT * kExperts; f += kThreads) {
+  // every logit of the thread is loaded before any is used (a loop that
+  // waited for each load made the finishing ~8 global round trips long)
+  constexpr int LPT = RT * kExperts / kThreads;  // logits per thread
+  static_assert(RT * kExperts % kThreads == 0, "whole logit passes");
+  float lv[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int f = tid + i * kThreads;
     const int tl = f / kExperts, e = f % kExperts;
     const int tok = t0 + tl;
     float l = 0.0f;
-    if (tok < T) {
-      if (!FROM_LOGITS && ES == 1) {
-        l = s_prob[tl][e];
-      } else {
-        l = lsrc[(size_t)tok * kExperts + e];
-        if (FROM_LOGITS) a.s.logits[(size_t)tok * kExperts + e] = l;
-      }
-    }
-    const float p = ref_sigmoid(l);
+    if (tok < T) l = (!FROM_LOGITS && ES == 1) ? s_prob[tl][e] : lsrc[(size_t)tok * kExperts + e];
+    lv[i] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int f = tid + i * kThreads;
+    const int tl = f / kExperts, e = f % kExperts;
+    const int tok = t0 + tl;
+    if (FROM_LOGITS && tok < T) a.s.logits[(size_t)tok * kExperts + e] = lv[i];
+    const float p = ref_sigmoid(lv[i]);
     s_prob[tl][e] = p;
     s_score[tl][e] = p + s_bias[e];  // layer.cu:462
   }
@@ -1923,6 +1929,10 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   pl.ncomb = a.T;  // combine tasks: one per token
   pl.grid = gridDim.x;
   int maxcnt;
+  if (local && (a.T < 1 || a.T > kDecRT)) {  // a deferred route covers one token block
+    if (tid == 0) st_agent(&a.s.ctrl->err, 2);
+    return;
+  }
   if (local) {
     // One token block (T <= 8), 16-row tasks: every block routes the tokens
     // from the logits and plans the launch itself, as the router's last
