@@ -400,6 +400,57 @@ template <int RT, int ES, int KC> struct RouterCfg {
   static_assert(KC % 4 == 0 && kThreads % (KC / 4) == 0, "chunk split");
 };
 
+// One LDS chunk of TPL interleaved FMA chains (tokens j of rows xp + j *
+// PITCH against the gate row gp), k ascending, as chain_dot: the operands of
+// the next 8 k are read while this 8 k's FMAs run.  KC % 16 == 0.
+template <int TPL, int KC, int PITCH>
+__device__ __forceinline__ void chain_chunk(const float *gp, const float *xp, float (&acc)[TPL]) {
+#pragma clang fp contract(off)
+  static_assert(KC % 16 == 0 && KC >= 16, "chunk of whole 16-k steps");
+  constexpr int U = 2;  // float4 per half step: 8 k
+  f32x4 ga[U], gb[U], xa[TPL][U], xb[TPL][U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    ga[u] = ld4(gp + 4 * u);
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) xa[j][u] = ld4(xp + j * PITCH + 4 * u);
+  }
+#define MOE_CHUNK_FMAS(G, X)                                   \
+  _Pragma("unroll") for (int u = 0; u < U; ++u)                \
+  _Pragma("unroll") for (int j = 0; j < TPL; ++j) {            \
+      acc[j] = __builtin_fmaf(X[j][u].x, G[u].x, acc[j]);      \
+      acc[j] = __builtin_fmaf(X[j][u].y, G[u].y, acc[j]);      \
+      acc[j] = __builtin_fmaf(X[j][u].z, G[u].z, acc[j]);      \
+      acc[j] = __builtin_fmaf(X[j][u].w, G[u].w, acc[j]);      \
+    }
+#pragma unroll
+  for (int k = 0; k < KC - 16; k += 16) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      gb[u] = ld4(gp + k + 8 + 4 * u);
+#pragma unroll
+      for (int j = 0; j < TPL; ++j) xb[j][u] = ld4(xp + j * PITCH + k + 8 + 4 * u);
+    }
+    MOE_CHUNK_FMAS(ga, xa)
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      ga[u] = ld4(gp + k + 16 + 4 * u);
+#pragma unroll
+      for (int j = 0; j < TPL; ++j) xa[j][u] = ld4(xp + j * PITCH + k + 16 + 4 * u);
+    }
+    MOE_CHUNK_FMAS(gb, xb)
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    gb[u] = ld4(gp + KC - 8 + 4 * u);
+#pragma unroll
+    for (int j = 0; j < TPL; ++j) xb[j][u] = ld4(xp + j * PITCH + KC - 8 + 4 * u);
+  }
+  MOE_CHUNK_FMAS(ga, xa)
+  MOE_CHUNK_FMAS(gb, xb)
+#undef MOE_CHUNK_FMAS
+}
+
 // At most a few blocks per CU run (T/64 blocks), so the kernel is compiled for
 // instruction-level parallelism (all of a chunk's LDS reads in flight), not
 // occupancy.
@@ -468,22 +519,7 @@ void router_kernel(RouterArgs a) {
         for (int i = 0; i < C::G_PER; ++i)
           pg[i] = ld4(grow + (size_t)i * RPP * H + k0 + KC);
       }
-      if (chain_lane) {
-        const float *gp = gs + el * PITCH;
-        const float *xp = xs + grp * TPL * PITCH;
-#pragma unroll 4
-        for (int k = 0; k < KC; k += 4) {
-          const f32x4 gv = ld4(gp + k);
-#pragma unroll
-          for (int j = 0; j < TPL; ++j) {
-            const f32x4 xv = ld4(xp + j * PITCH + k);
-            acc[j] = __builtin_fmaf(xv.x, gv.x, acc[j]);
-            acc[j] = __builtin_fmaf(xv.y, gv.y, acc[j]);
-            acc[j] = __builtin_fmaf(xv.z, gv.z, acc[j]);
-            acc[j] = __builtin_fmaf(xv.w, gv.w, acc[j]);
-          }
-        }
-      }
+      if (chain_lane) chain_chunk<TPL, KC, PITCH>(gs + el * PITCH, xs + grp * TPL * PITCH, acc);
     }
     if (chain_lane) {
 #pragma unroll
