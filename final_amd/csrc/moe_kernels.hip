@@ -677,9 +677,11 @@ struct RouteShared {
   int cnt[kExperts];           // the block's tokens per expert
 };
 
-// Routing of nt <= kDecRT tokens from their logits (logit(t, e)), threads
-// 0..255 as (token tid / 32, expert tid % 32); every thread of the block
-// calls it (it holds barriers) and finds rs complete on return.
+// Routing of nt <= kDecRT tokens from their logits, threads 0..255 as
+// (token tid / 32, expert tid % 32), each passing the logit of its pair (l,
+// read by the caller, which can issue that load early; ignored for tokens
+// past nt); every thread of the block calls it (it holds barriers) and finds
+// rs complete on return.
 //  - probability 1/(1+(float)exp(-(double)l)) (layer.cu:434), score = p + bias
 //    (bias in LDS, layer.cu:462);
 //  - top-4 as a rank: e is kept iff fewer than 4 selectable experts have a
@@ -692,16 +694,15 @@ struct RouteShared {
 //  - weights p * (1 / sum) * 1.0f, the sum in rank order (layer.cu:480-489);
 //  - in-block ranks (tokens of the block before this one that chose the
 //    same expert) and per-expert counts.
-template <typename Logit>
 __device__ __forceinline__ void route_token_block(RouteShared &rs, int nt, const float *bias,
-                                                  Logit logit) {
+                                                  float logit) {
 #pragma clang fp contract(off)
   const int tid = threadIdx.x;
   const bool act = tid < kDecRT * kExperts;
   const int tl = (tid >> 5) & (kDecRT - 1), e = tid & (kExperts - 1);
   const bool tvalid = act && tl < nt;
   if (act) {
-    const float l = tvalid ? logit(tl, e) : 0.0f;
+    const float l = tvalid ? logit : 0.0f;
     const float p = ref_sigmoid(l);
     rs.prob[tl][e] = p;
     rs.score[tl][e] = p + bias[e];
@@ -861,8 +862,11 @@ void router_decode_kernel(RouterArgs a) {
   __syncthreads();
   if (!s_flag) return;
   // 4-7. probabilities, top-4, weights, in-block ranks and counts
-  const float *lg = a.s.logits + (size_t)t0 * kExperts;
-  route_token_block(rs, nt, s_bias, [lg](int t, int ee) { return lg[t * kExperts + ee]; });
+  {
+    const int tl = tid >> 5;  // thread = (token tl, expert tid % 32)
+    const float l = tl < nt ? a.s.logits[(size_t)(t0 + tl) * kExperts + (tid & (kExperts - 1))] : 0.0f;
+    route_token_block(rs, nt, s_bias, l);
+  }
   const int nb = gridDim.x / kDecES;
   if (tid < nt) {
 #pragma unroll
@@ -1974,10 +1978,12 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     // from the logits and plans the launch itself, as the router's last
     // block would (same functions, same order), and block 0 publishes the
     // routing for the host.  Slot = offsets[e] + in-block rank.
+    // the thread's logit and the bias are loaded together, before one barrier
+    const int ltl = tid >> 5;
+    const float l = tid < kDecRT * kExperts && ltl < a.T ? a.s.logits[tid] : 0.0f;
     if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
     __syncthreads();
-    const float *lg = a.s.logits;
-    route_token_block(rsh, a.T, s_bias, [lg](int t, int e) { return lg[t * kExperts + e]; });
+    route_token_block(rsh, a.T, s_bias, l);
     if (tid < kExperts) {  // lanes 0-31 of wave 0
       const int cnt = rsh.cnt[tid];
       int total = 0;
