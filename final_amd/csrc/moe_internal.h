@@ -15,6 +15,10 @@ constexpr int kMinRouterTokens = 8;  // smallest token block of the router
 constexpr int kThreads = 256;    // every kernel runs 4 waves of 64
 constexpr int kCombineCols = 64;  // columns per combine counter (MFMA plans)
 constexpr int kRouterSlotTokens = 1024;  // MFMA plans up to this many tokens: the router assigns slots
+// 64-row plan up to this many tokens: the last kGateUpTailUnits units run
+// half-width gate/up tiles (T=56-128: 1.2-2 % faster; 160 equal; 192-256: 1 % slower)
+constexpr int kGateUpTailTokens = 128;
+constexpr int kGateUpTailUnits = 8;
 constexpr int kStreamRows = 16;  // weight rows per streaming-plan task (small batches)
 constexpr int kStreamWideTokens = 32;  // batches from this size use 64-row tasks
 // Streaming kernel shapes: tokens per MFMA pass; token passes of 16- and
@@ -53,6 +57,7 @@ struct Ctrl {
   int slots_assigned;  // MFMA plans: the router wrote every slot (pos = slot, slot_token)
   int deferred;     // the router stopped after the logits; the streaming kernel routes and plans
   int tail_units;   // last units whose down tiles run as two half-width tiles
+  int gu_tail;      // 64-row plan: of those, the units whose gate/up tiles also run at half width
   int counts[kExperts];
   int offsets[kExperts + 1];
   int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)

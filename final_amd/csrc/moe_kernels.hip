@@ -277,7 +277,12 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
                               ? min(units, kRingTailUnits) : 0);
       const int tail_mult = tr > 0 ? 2 : kRingWideGroups;
       ctrl->tail_units = tail;
-      ctrl->n_p1 = units * p1u;
+      // 64-row plan of small batches (units of few rows, memory-bound
+      // tiles): the last units' gate/up tiles run at half width too, so the
+      // last gate/up tiles end sooner and the down tiles after them wait less
+      const int gtail = tr == 64 && T <= kGateUpTailTokens ? min(units, kGateUpTailUnits) : 0;
+      ctrl->gu_tail = gtail;
+      ctrl->n_p1 = (units + gtail) * p1u;
       ctrl->n_p2 = (units - tail + tail * tail_mult) * p2u;
       // the MFMA plans combine inside their down tiles; the streaming kernel
       // runs one combine task per token
@@ -1144,7 +1149,8 @@ void expert_mfma_kernel(ExpertArgs a) {
   if (tid < kExperts) s_counts[tid] = c->counts[tid];
   const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
   const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
-  const int nunits = n1 / p1u, tail = c->tail_units;
+  const int gtail = BM == 64 ? c->gu_tail : 0;
+  const int nunits = n1 / p1u - gtail, tail = c->tail_units;
   const int H = a.H, I = a.I;
   const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
   if (tid == 0) s_task = claim(&c->head);
@@ -1191,8 +1197,13 @@ void expert_mfma_kernel(ExpertArgs a) {
       block_signal(&c->assign_done);
       if (tid == 0) next = claim(&c->head);
     } else if (task < nb + n1) {
+      // gate/up tiles: full width for the first units, two half-width tiles
+      // per column range for the last gtail units (64-row plan)
       const int q = task - nb;
-      const int u = q / p1u, nt = q % p1u;
+      const int gfull = (nunits - gtail) * p1u;
+      const bool ghalf = q >= gfull;
+      const int u = ghalf ? nunits - gtail + (q - gfull) / (2 * p1u) : q / p1u;
+      const int nt = ghalf ? (q - gfull) % (2 * p1u) : q % p1u;
       int e, m0, rows;
       unit_rows<BM>(u, uo, e, m0, rows);
       const int slot0 = s_offsets[e] + m0;
@@ -1204,12 +1215,23 @@ void expert_mfma_kernel(ExpertArgs a) {
       // a 128-row unit holding at most 64 rows runs as a 64x128 tile (same
       // columns and outputs, half the padding MFMAs)
       static_assert(Tile<64>::BN == Tile<128>::BN, "a 64-row tile covers a 128-row unit's columns");
-      if (BM == 128 && rows <= 64)
+      if constexpr (BM == 64) {
+        if (ghalf) {  // one W1/W3 row group: 32 intermediate columns
+          using TH = TileHalf<64>;
+          const float *hrow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TH::BN) * H;
+          next = mfma_tile<TH, true>(lds, a.x, xbytes, s_aoff, rows, hrow0, H, inter_out, slot0,
+                                     I, nt * (TH::BN / 2), &c->head);
+        } else {
+          next = mfma_tile<TL, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
+                                     I, nt * (TL::BN / 2), &c->head);
+        }
+      } else if (BM == 128 && rows <= 64) {
         next = mfma_tile<Tile<64>, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
                                          I, nt * (TL::BN / 2), &c->head);
-      else
+      } else {
         next = mfma_tile<Tile<BM>, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
                                          I, nt * (TL::BN / 2), &c->head);
+      }
       block_signal(&a.s.dep[u]);
     } else if (task < nb + n1 + n2) {
       // down tiles: full width for the first units, two half-width tiles per
@@ -1223,7 +1245,7 @@ void expert_mfma_kernel(ExpertArgs a) {
       unit_rows<BM>(u, uo, e, m0, rows);
       const int slot0 = s_offsets[e] + m0;
       block_wait(&c->assign_done, nb, a.wait_limit, &c->err);  // combine counters cleared
-      block_wait(&a.s.dep[u], p1u, a.wait_limit, &c->err);
+      block_wait(&a.s.dep[u], u >= nunits - gtail ? 2 * p1u : p1u, a.wait_limit, &c->err);
       if (tid < BM) s_aoff[tid] = tid < rows ? tid * I : -1;
       __syncthreads();
       const float *abase = a.s.inter + (size_t)slot0 * I;

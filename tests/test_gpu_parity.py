@@ -183,6 +183,42 @@ def test_streaming_wide_tasks(T, block, real_weights, oracle_mod):
 
 
 @pytest.mark.gpu
+def test_gate_up_half_tiles(block, real_weights, oracle_mod):
+    """The 64-row plan up to 128 tokens runs its last eight units' gate/up
+    work as two half-width tiles each, and their down tiles wait for both.
+    Forced onto that plan: 1 token (four units, all split), 5 tokens, 128
+    tokens with natural routing (eight of some 32 units split), and 128
+    tokens on four hot experts (two units each: all eight split, two per
+    expert)."""
+    from final_amd import workloads as W
+    hot = [2, 13, 21, 30]
+    bias = np.array(real_weights["bias"], np.float32).copy()
+    bias[hot] += 10.0
+    cases = [(1, None), (5, None), (128, None), (128, bias)]
+    block.force_tile_rows(64)
+    try:
+        for T, b in cases:
+            w = dict(real_weights)
+            if b is not None:
+                w["bias"] = b
+            block.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+            say(f"[half tiles] T={T} plan=64 hot={b is not None}")
+            x = W.gen_x(T, seed=60 + T)
+            y = block.forward(x)
+            rt = block.last_routing()
+            block.check_device()
+            ref = oracle_forward(oracle_mod, w, x)
+            check_routing(rt, ref)
+            if b is not None:
+                assert sorted(np.nonzero(rt["counts"])[0].tolist()) == hot
+            np.testing.assert_allclose(y, ref["y"], rtol=RTOL, atol=ATOL)
+    finally:
+        block.force_tile_rows(-1)
+        rw = real_weights
+        block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
+
+
+@pytest.mark.gpu
 def test_residual_fused_and_in_place(block, real_weights, oracle_mod):
     """y = residual + MoE(x) (the decoder layer's add, layer.cu:1917), also
     with y aliasing the residual buffer."""
