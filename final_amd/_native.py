@@ -27,6 +27,7 @@ CAPI_SYMBOLS = (
     "moe_strerror", "moe_version", "moe_set_norm_weight", "moe_forward_norm",
     "moe_last_normed", "moe_dense_create", "moe_dense_set_weights", "moe_dense_forward",
     "moe_forward_noalloc", "moe_create_shared", "moe_dense_create_shared",
+    "moe_set_lazy_chains",
 )
 LFM_SYMBOLS = (
     "lfm_gemm_nt", "lfm_embed", "lfm_rmsnorm", "lfm_qk_norm_rope", "lfm_attention",
@@ -95,6 +96,7 @@ def lib() -> ctypes.CDLL:
     L.moe_plan_tile_rows.argtypes = [_vp, _i]
     L.moe_force_tile_rows.argtypes = [_vp, _i]
     L.moe_set_wait_divisor.argtypes = [_vp, _i]
+    L.moe_set_lazy_chains.argtypes = [_vp, _i]
     L.moe_strerror.argtypes = [_i]
     L.moe_strerror.restype = ctypes.c_char_p
     L.moe_version.restype = ctypes.c_char_p

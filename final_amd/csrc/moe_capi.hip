@@ -134,6 +134,7 @@ struct moe_ctx {
   int cus = 1;
   int tile_override = -1;
   int wait_div = 1;
+  bool lazy_chains = false;  // test hook (moe_set_lazy_chains)
   bool weights_set = false;
   bool has_bias = false;
   bool dense = false;      // dense FFN context (moe_dense_create): kDenseChunks chunk experts
@@ -517,7 +518,10 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   a.bn = expert_bn(a.tile_rows, T);
   a.tail_units = tail_units(ctx, a.tile_rows, a.bn);
   a.max_units = ctx->max_units;
-  a.defer = defer && !logits && router_can_defer(T, a.tile_rows, a.bn) ? 1 : 0;
+  // deferred decode routing: the router writes score bounds, the streaming
+  // kernel computes the logits and routes
+  a.defer = defer && !logits && router_can_defer(T, a.tile_rows, a.bn) ? 2 : 0;
+  a.lazy_chains = ctx->lazy_chains ? 1 : 0;
   a.norm_w = norm_w;
   a.xn = xn;
   if (launch_router(a, logits != nullptr, static_cast<hipStream_t>(stream)) != hipSuccess)
@@ -870,6 +874,12 @@ int moe_force_tile_rows(moe_ctx *ctx, int rows) {
 int moe_set_wait_divisor(moe_ctx *ctx, int divisor) {
   if (!ctx || divisor < 1) return MOE_ERR_INVALID_ARG;
   ctx->wait_div = divisor;
+  return MOE_OK;
+}
+
+int moe_set_lazy_chains(moe_ctx *ctx, int on) {
+  if (!ctx || ctx->dense) return MOE_ERR_INVALID_ARG;
+  ctx->lazy_chains = on != 0;
   return MOE_OK;
 }
 

@@ -32,6 +32,11 @@ constexpr int kRingDenseGroups = 2, kRingDensePasses = 4;
 // at the end of the queue when its 64-row tasks are streamed in sub-groups
 // (T=64: 277 us with none, 275.7 with 2, 274.4 with 6, 277.4 with 12).
 constexpr int kRingTailUnits = 6;
+// Tokens of one decode token block: the batches whose routing the streaming
+// kernel may finish itself (Ctrl::deferred).
+constexpr int kDeferTokens = 8;
+// Gate-logit chain jobs of a certified decode routing: 4 experts each.
+constexpr int kChainJobs = kExperts / 4;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset
@@ -55,13 +60,25 @@ struct Ctrl {
   int stream_rows;  // streaming plan: weight rows per task (16, 32 or 64)
   int max_count;    // tokens of the largest expert
   int slots_assigned;  // MFMA plans: the router wrote every slot (pos = slot, slot_token)
-  int deferred;     // the router stopped after the logits; the streaming kernel routes and plans
+  // 0: the router routed and planned; 1: it stopped after the logits and the
+  // streaming kernel routes and plans; 2: it wrote score bounds (sbound), and
+  // the streaming kernel computes the logits (chain jobs) and routes from the
+  // bounds where they settle every token's top-4
+  int deferred;
+  int chain_lazy;   // test hook: blocks leave the chain jobs to the waits that need them
   int tail_units;   // last units whose down tiles run as two half-width tiles
   int gu_tail;      // 64-row plan: of those, the units whose gate/up tiles also run at half width
   int counts[kExperts];
   int offsets[kExperts + 1];
   int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)
   int active[kExperts];
+  // deferred == 2: lower and upper bound of each (token, expert) score
+  // sigmoid(logit) + bias, whatever order the logit's FMA chain ran in
+  float sbound[2][kDeferTokens][kExperts];
+  // chain jobs claimed and stored (deferred == 2), on a cache line of their
+  // own: atomics on one line serialise, and head takes one per block
+  alignas(128) int chain_head;
+  int chain_done;
   // followed in memory by int dep[max_units]: W1W3 tasks finished per unit
 };
 
@@ -100,7 +117,8 @@ struct RouterArgs {
   int bn;                // MFMA n-tile width (columns of the B tile)
   int tail_units;        // MFMA plans: last units whose down tiles run at half width
   int max_units;
-  int defer;             // stop after the logits (router_can_defer); the expert kernel routes
+  int defer;             // 1: stop after the logits; 2: score bounds only (router_can_defer)
+  int lazy_chains;       // defer == 2: Ctrl::chain_lazy
   const float *norm_w;   // post-attention RMSNorm weight [H]: x is h, normalise it (decode router only)
   float *xn;             // [T][H]: the normalised rows, for the expert kernel
 };

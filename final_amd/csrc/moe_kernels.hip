@@ -18,8 +18,11 @@
 //      tiles; 64-row tiles up to 831 tokens, 128-row tiles above.  T <= 48:
 //      expert_ring_kernel, weight streaming through MFMA 16x16x4 f32 with
 //      round-robin tasks and slots assigned by the router -- or, for a fused
-//      forward of at most 8 tokens, routed and planned by each of its own
-//      blocks from the router's logits (the router then stops after them).
+//      forward of at most 8 tokens, planned by each of its own blocks from
+//      bounds of the scores that the router writes instead of the logits
+//      (they settle every token's top-4 set unless two scores nearly tie at
+//      the 4th place), while 8 of its blocks compute the logits as chain
+//      jobs for the weights, the rank order and the published routing.
 //
 // Phase dependencies are counters in the control block.  A task only waits
 // on tasks with a smaller index and every block runs its tasks in increasing
@@ -41,6 +44,8 @@ namespace moe {
 // a signalling NaN: arithmetic never produces one (an operation on a NaN
 // returns a quiet NaN), and every value of those rows is computed.
 constexpr uint32_t kUnwritten = 0x7FBADA55u;
+// idx / pos of a token whose routing the streaming kernel has not published yet
+constexpr int kRouteUnset = -2;
 
 // Fill rows [0, 4T) of the intermediate and expert-output buffers with
 // kUnwritten, shared by nthr threads in each of nblk blocks (this thread:
@@ -669,6 +674,41 @@ void router_kernel(RouterArgs a) {
 
 // Decode router shape: 8-token blocks, 4 experts per block, 8 blocks per token block.
 constexpr int kDecRT = 8, kDecEPB = 4, kDecES = kExperts / kDecEPB;
+static_assert(kDecRT == kDeferTokens && kDecES == kChainJobs, "a chain job is one router block's chains");
+constexpr int kChainClaimBlocks = 16;  // streaming-kernel blocks that try for a chain job as they start
+
+// Bounds of the score fl(ref_sigmoid(l) + bias) of the float logit l that an
+// FMA chain over H products computes, from s and m, float sums of the
+// products and of their magnitudes with at most n roundings on any path.
+// Each of the chain's H roundings perturbs by at most u = 2^-24 relatively,
+// so |l - sum| <= gamma_H * M with gamma_k = k u / (1 - k u) and M the exact
+// sum of magnitudes (Higham, Accuracy and Stability of Numerical Algorithms,
+// 3.1; plus 2^-150 per rounding below the normal range); likewise |s - sum| <=
+// gamma_n * M, and M <= m / (1 - gamma_n).  ref_sigmoid is within 3
+// roundings (exp to float, the add, the divide) of the real sigmoid, which is
+// monotone: its value lies within a relative 2^-20 of the sigmoid's at the
+// interval's ends.  fl(p + bias) is monotone in p.  False (bounds infinite)
+// where this does not hold: non-finite sums or bias, sums large enough for a
+// partial sum to overflow, and logits below -80, whose probability may be
+// subnormal.
+__device__ __forceinline__ bool score_bounds(float s, float m, int H, int n, float bias, float *lo,
+                                             float *hi) {
+#pragma clang fp contract(off)
+  const double u = 0x1p-24, gh = H * u / (1.0 - H * u), gn = n * u / (1.0 - n * u);
+  const double r = (gh + gn) / (1.0 - gn) * 1.0001 * (double)m + 1e-37;
+  const double sd = s;
+  const bool ok = __builtin_isfinite(s) && __builtin_isfinite(m) && m < 1e37f &&
+                  __builtin_isfinite(bias) && sd - r > -80.0;
+  if (!ok) {
+    *lo = -__builtin_inff();
+    *hi = __builtin_inff();
+    return false;
+  }
+  const double pl = 1.0 / (1.0 + exp(-(sd - r))), ph = 1.0 / (1.0 + exp(-(sd + r)));
+  *lo = __double2float_rd(pl * (1.0 - 0x1p-20)) + bias;
+  *hi = __double2float_ru(ph * (1.0 + 0x1p-20)) + bias;
+  return true;
+}
 
 // One token block's routing (up to kDecRT tokens x 32 experts) in LDS.
 struct RouteShared {
@@ -793,14 +833,17 @@ void router_decode_kernel(RouterArgs a) {
   // the score bias, read now so the finishing block finds it in LDS
   if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
   if (a.defer && blockIdx.x == 0 && tid == 0) {
-    // the streaming kernel routes and plans: its queue starts at 0
+    // the streaming kernel routes and plans: its queues start at 0
     Ctrl *ctrl = a.s.ctrl;
     ctrl->head = 0;
-    ctrl->deferred = 1;
+    ctrl->deferred = a.defer;
     ctrl->num_tokens = T;
     ctrl->tile_rows = 0;
     ctrl->n_rblocks = 0;
     ctrl->stream_rows = a.bn;
+    ctrl->chain_head = 0;
+    ctrl->chain_done = 0;
+    ctrl->chain_lazy = a.lazy_chains;
   }
 
   // 1. gate rows e0..e0+3 and token rows t0..t0+nt-1, 1 KiB per load
@@ -814,6 +857,16 @@ void router_decode_kernel(RouterArgs a) {
                          c * 256 + lane * 4;
       float *dst = (r < kDecEPB ? gs + r * P : xs + (r - kDecEPB) * P) + c * 256;
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+    }
+    if (a.defer == 2) {
+      // while the rows land: the expert kernel's rows to kUnwritten, and the
+      // token routing it publishes to "not yet" (kRouteUnset)
+      fill_unwritten(a, blockIdx.x, gridDim.x, tid, kThreads);
+      if (blockIdx.x == 0 && tid < T * kTopK) {
+        a.s.idx[tid] = kRouteUnset;
+        a.s.pos[tid] = kRouteUnset;
+        a.s.wts[tid] = __builtin_bit_cast(float, kUnwritten);
+      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -841,6 +894,38 @@ void router_decode_kernel(RouterArgs a) {
       }
     }
     __syncthreads();
+  }
+  if (a.defer == 2) {
+    // 2'. score bounds in place of the chains (score_bounds): 8 threads per
+    // (token, expert) pair, k interleaved in float4s, four float sums of
+    // products and four of magnitudes each (H / 32 FMAs per sum, then 2
+    // adds and 3 shuffle levels)
+    const int pr = tid >> 3, part = tid & 7;
+    const int tl = pr / kDecEPB, el = pr % kDecEPB;
+    const float *gp = gs + el * P, *xp = xs + min(tl, nt - 1) * P;
+    float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 8
+    for (int k = part * 4; k < H; k += 32) {
+      const f32x4 g = ld4(gp + k), xv = ld4(xp + k);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        sq[q] = __builtin_fmaf(g[q], xv[q], sq[q]);
+        mq[q] = __builtin_fmaf(__builtin_fabsf(g[q]), __builtin_fabsf(xv[q]), mq[q]);
+      }
+    }
+    float sum = (sq[0] + sq[1]) + (sq[2] + sq[3]), mag = (mq[0] + mq[1]) + (mq[2] + mq[3]);
+#pragma unroll
+    for (int o = 1; o < 8; o <<= 1) {
+      sum += __shfl_xor(sum, o, 8);
+      mag += __shfl_xor(mag, o, 8);
+    }
+    if (part == 0 && tl < nt) {
+      float lo, hi;
+      score_bounds(sum, mag, H, H / 32 + 5, s_bias[e0 + el], &lo, &hi);
+      a.s.ctrl->sbound[0][tl][e0 + el] = lo;
+      a.s.ctrl->sbound[1][tl][e0 + el] = hi;
+    }
+    return;
   }
   // 2. chains: wave 0, lane = (token l / 4, expert l % 4)
   if (wave == 0) {
@@ -1351,9 +1436,11 @@ struct RingShared {
   int abort;
   int seq[8];              // the block's j-th row task id at seq[j & 7]
   int nseq;                // row task ids published so far
-  int local;               // routing computed by this block (deferred router)
+  int local;               // 1: routing computed by this block; 2: set settled by the score bounds
   int rpos[kDecRT][kTopK]; // local routing: slot of each (token, rank), -1: none
   float rw[kDecRT][kTopK]; // local routing: weights
+  int slotmap[kDecRT][kExperts];  // settled set: slot of each (token, expert), -1: not chosen
+  float bias[kExperts];    // score bias (deferred routing)
 };
 
 __device__ __forceinline__ int lds_load(const int *p) {
@@ -1643,6 +1730,209 @@ __device__ __forceinline__ RingRoute ring_route(const ExpertArgs &a, const RingS
   return r;
 }
 
+// Chain jobs of a certified decode routing (Ctrl::deferred == 2): job j
+// stores the gate logits of experts 4j..4j+3 for the batch's <= 8 tokens,
+// with chain_dot's arithmetic (the reference's FMA order), and counts itself
+// in chain_done once its stores are complete.  Blocks claim jobs as they
+// start; a job never waits, so every claimed job ends.
+//
+// Block form: every thread of the block calls it; the operands are staged in
+// the block's partial buffers (free until it streams) with direct-to-LDS
+// loads and wave 0 runs one chain per (token, expert) lane.  The block that
+// completes the last job routes every token from the logits at once
+// (route_token_block) and publishes idx, w and pos, so the combine finds
+// them; rsh and sh.offsets serve as scratch (sh.bias must be loaded).
+__device__ __forceinline__ void ring_chain_job(const ExpertArgs &a, RingShared &sh,
+                                               RouteShared &rsh, int *s_flag, int j,
+                                               float *lds) {
+  const int T = a.T, H = a.H, P = H + 4, tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  float *gs = lds, *xs = lds + kDecEPB * P;
+  const int e0 = j * kDecEPB, nch = H >> 8, items = (kDecEPB + T) * nch;
+  for (int i = wave; i < items; i += kRingThreads / 64) {
+    const int r = i / nch, ch = i % nch;
+    const float *src = (r < kDecEPB ? a.w.gate + (size_t)(e0 + r) * H
+                                    : a.x + (size_t)(r - kDecEPB) * H) + ch * 256 + lane * 4;
+    float *dst = (r < kDecEPB ? gs + r * P : xs + (r - kDecEPB) * P) + ch * 256;
+    __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (wave == 0) {
+    const int tl = lane >> 2, el = lane & 3;
+    const float acc = chain_dot(gs + el * P, xs + min(tl, T - 1) * P, H);
+    if (tl < T) st_agent(&a.s.logits[(size_t)tl * kExperts + e0 + el], acc);
+    __builtin_amdgcn_s_waitcnt(0);  // the logits are stored
+    if (lane == 0) *s_flag = fetch_add(&a.s.ctrl->chain_done, 1) == kChainJobs - 1;
+  }
+  __syncthreads();  // the staging buffers are free again
+  if (*s_flag) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    const int tl = (tid >> 5) & (kDecRT - 1), e = tid & (kExperts - 1);
+    const float l = tid < kDecRT * kExperts && tl < T
+                        ? __hip_atomic_load(&a.s.logits[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : 0.0f;
+    route_token_block(rsh, T, sh.bias, l);
+    if (tid < kExperts) {
+      int total = 0;
+      sh.offsets[tid] = lane_scan32(rsh.cnt[tid], tid, &total);
+    }
+    __syncthreads();
+    if (tid < T * kTopK) {
+      const int t = tid / kTopK, k = tid % kTopK;
+      const int ex = rsh.ti[t][k];
+      st_agent(&a.s.idx[tid], ex);
+      st_agent(&a.s.wts[tid], rsh.tw[t][k]);
+      st_agent(&a.s.pos[tid], ex >= 0 ? sh.offsets[ex] + rsh.rank[t][k] : -1);
+    }
+    __syncthreads();
+  }
+}
+
+// Wave form, for a wave that waits for the logits while a job is still
+// unclaimed: the same chains with their operands read from global memory
+// (slow, but it lets a wait finish when blocks that have not started hold
+// the job).
+__device__ __forceinline__ void ring_chain_job_wave(const ExpertArgs &a, int j) {
+  const int T = a.T, H = a.H, lane = threadIdx.x & 63;
+  const int tl = lane >> 2, el = lane & 3, e = j * kDecEPB + el;
+  const float acc = chain_dot(a.w.gate + (size_t)e * H, a.x + (size_t)min(tl, T - 1) * H, H);
+  if (tl < T) st_agent(&a.s.logits[(size_t)tl * kExperts + e], acc);
+  __builtin_amdgcn_s_waitcnt(0);
+  if (lane == 0) fetch_add(&a.s.ctrl->chain_done, 1);
+}
+
+// A token's routing once its logits are stored (certified decode routing):
+// the calling wave waits for every chain job (running unclaimed ones
+// itself), then computes the token's top-4 in rank order and weights with
+// route_token_block's arithmetic (lane e: expert e; lanes 32-63 repeat
+// lanes 0-31).  The slots come from the set the score bounds settled, which
+// the exact top-4 must equal (else the status word reads 2 and the block
+// aborts).  Wave 0 publishes the token's idx, weights and slots.  False if
+// the block aborts or the wait times out.
+__device__ __forceinline__ bool ring_route_exact(const ExpertArgs &a, RingShared &sh, int tok,
+                                                 RingRoute *out, int *abort_flag, int *err,
+                                                 long long ticks) {
+#pragma clang fp contract(off)
+  Ctrl *ctrl = a.s.ctrl;
+  const int lane = threadIdx.x & 63, e = lane & 31;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (__builtin_amdgcn_readfirstlane(load_relaxed(&ctrl->chain_done)) < kChainJobs) {
+    const long long t0 = ring_now();
+    while (__builtin_amdgcn_readfirstlane(load_relaxed(&ctrl->chain_done)) < kChainJobs) {
+      if (__builtin_amdgcn_readfirstlane(lds_load(abort_flag))) return false;
+      if (ring_now() - t0 > ticks) {
+        if (lane == 0) {
+          st_agent(err, 1);
+          lds_store(abort_flag, 1);
+        }
+        return false;
+      }
+      int j = kChainJobs;
+      if (__builtin_amdgcn_readfirstlane(load_relaxed(&ctrl->chain_head)) < kChainJobs) {
+        j = lane == 0 ? claim(&ctrl->chain_head) : 0;
+        j = __builtin_amdgcn_readfirstlane(j);
+      }
+      if (j < kChainJobs) ring_chain_job_wave(a, j);
+      else __builtin_amdgcn_s_sleep(1);
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  const float l = __hip_atomic_load(&a.s.logits[(size_t)tok * kExperts + e], __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+  const float p = ref_sigmoid(l);
+  const float sc = p + sh.bias[e];
+  int r = 0;
+#pragma unroll
+  for (int jx = 0; jx < kExperts; ++jx) {
+    const float sj = __shfl(sc, jx, 32);
+    r += (int)((sj > -1e30f) & ((sj > sc) | ((sj == sc) & (jx < e))));
+  }
+  const int sel = (sc > -1e30f && r < kTopK) ? r : -1;
+  int ek[kTopK];
+  float pk[kTopK];
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    const uint32_t m = (uint32_t)__ballot(sel == k);  // lanes 0-31
+    ek[k] = m ? __builtin_ctz(m) : -1;
+    pk[k] = m ? __shfl(p, ek[k], 64) : 0.0f;
+  }
+  float sum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) sum += pk[k];
+  const float scale = (sum > 1e-6f) ? (1.0f / sum) : 1.0f;
+  bool same = true;
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    out->w[k] = pk[k] * scale * 1.0f;
+    out->slot[k] = ek[k] >= 0 ? sh.slotmap[tok][ek[k]] : -1;
+    same = same && out->slot[k] >= 0;  // the settled set has four experts
+  }
+  if (!same) {
+    if (lane == 0) {
+      st_agent(err, 2);
+      lds_store(abort_flag, 1);
+    }
+    return false;
+  }
+  if (w == 0 && lane < kTopK) {
+    int ev = ek[0], sv = out->slot[0];
+    float wv = out->w[0];
+#pragma unroll
+    for (int k = 1; k < kTopK; ++k)
+      if (lane == k) {
+        ev = ek[k];
+        sv = out->slot[k];
+        wv = out->w[k];
+      }
+    st_agent(&a.s.idx[(size_t)tok * kTopK + lane], ev);
+    a.s.wts[(size_t)tok * kTopK + lane] = wv;
+    st_agent(&a.s.pos[(size_t)tok * kTopK + lane], sv);
+  }
+  return true;
+}
+
+// The token's routing as the block that finished the chain jobs published
+// it (coherent loads; one round trip), checked against the set the bounds
+// settled (else the status word reads 2 and the block aborts); if it is not
+// there yet, ring_route_exact.
+__device__ __forceinline__ bool ring_route_settled(const ExpertArgs &a, RingShared &sh, int tok,
+                                                   RingRoute *out, int *abort_flag, int *err,
+                                                   long long ticks) {
+  int ex[kTopK], sl[kTopK];
+  float wv[kTopK];
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    const size_t i = (size_t)tok * kTopK + k;
+    ex[k] = __hip_atomic_load(&a.s.idx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sl[k] = __hip_atomic_load(&a.s.pos[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    wv[k] = __hip_atomic_load(&a.s.wts[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  bool there = true, same = true;
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    there = there && ex[k] != kRouteUnset && sl[k] != kRouteUnset &&
+            __builtin_bit_cast(uint32_t, wv[k]) != kUnwritten;
+    same = same && ex[k] >= 0 && ex[k] < kExperts && sl[k] >= 0 &&
+           sh.slotmap[tok][ex[k] & (kExperts - 1)] == sl[k];
+  }
+  if (!__builtin_amdgcn_readfirstlane((int)there))
+    return ring_route_exact(a, sh, tok, out, abort_flag, err, ticks);
+  if (!same) {
+    if ((threadIdx.x & 63) == 0) {
+      st_agent(err, 2);
+      lds_store(abort_flag, 1);
+    }
+    return false;
+  }
+#pragma unroll
+  for (int k = 0; k < kTopK; ++k) {
+    out->slot[k] = sl[k];
+    out->w[k] = wv[k];
+  }
+  return true;
+}
+
 // Combine of token tok by the 512 threads of the streaming waves (thread ts:
 // float4 columns ts, ts + 512, ...), with the arithmetic of tile_combine:
 // FMA chain over k ascending, then the residual.  The expert outputs are
@@ -1848,8 +2138,12 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
   }
   // combine tasks (one token each), after every row task, with the ring's
   // registers free
-  for (int tok = blockIdx.x; ok && tok < pl.ncomb; tok += pl.grid)
-    ok = ring_combine(a, tok, ring_route(a, sh, tok), (int)threadIdx.x, &sh.abort, err, ticks);
+  for (int tok = blockIdx.x; ok && tok < pl.ncomb; tok += pl.grid) {
+    RingRoute r;
+    if (sh.local == 2) ok = ring_route_settled(a, sh, tok, &r, &sh.abort, err, ticks);
+    else r = ring_route(a, sh, tok);
+    if (ok) ok = ring_combine(a, tok, r, (int)threadIdx.x, &sh.abort, err, ticks);
+  }
 }
 
 // Control side: sums the 8 k-slice partials of item (t, g) and stores the
@@ -1964,29 +2258,85 @@ __device__ __forceinline__ void ring_role(const ExpertArgs &a, RingShared &sh, f
   }
 }
 
+// Counts of a decode token block (rsh.cnt) -> the block's expert table (sh),
+// its active-expert count and largest count; block 0 also publishes them
+// for moe_last_routing.  Lanes 0-31 of wave 0.
+__device__ __forceinline__ void ring_expert_table(const ExpertArgs &a, RingShared &sh,
+                                                  const RouteShared &rsh, bool pub, int *s_nact,
+                                                  int *s_maxcnt) {
+  const int tid = threadIdx.x;
+  if (tid >= kExperts) return;
+  const int cnt = rsh.cnt[tid];
+  int total = 0;
+  const int off = lane_scan32(cnt, tid, &total);
+  int mc = cnt;
+#pragma unroll
+  for (int o = 16; o > 0; o >>= 1) mc = max(mc, __shfl_xor(mc, o, 32));
+  const unsigned long long act = __ballot(cnt > 0);
+  const int nact = __popcll(act);
+  const int aidx = __popcll(act & ((1ull << tid) - 1ull));
+  sh.counts[tid] = cnt;
+  sh.offsets[tid] = off;
+  if (cnt > 0) sh.active[aidx] = tid;
+  if (tid >= nact) sh.active[tid] = -1;
+  if (tid == 0) {
+    *s_nact = nact;
+    *s_maxcnt = mc;
+  }
+  if (pub) {
+    Ctrl *cw = a.s.ctrl;
+    cw->counts[tid] = cnt;
+    cw->offsets[tid] = off;
+    if (cnt > 0) cw->active[aidx] = tid;
+    if (tid >= nact) cw->active[tid] = -1;
+    if (tid == 0) {
+      cw->offsets[kExperts] = total;
+      cw->n_active = nact;
+      cw->max_count = mc;
+    }
+  }
+}
+
 template <int KCH1, int KCH2>
 __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a) {
   static_assert(KCH1 * 256 <= kRingWaves * kRingSlice && KCH2 * 256 <= kRingWaves * kRingSlice,
                 "row length");
-  extern __shared__ float res[];  // partials, ring_res_bytes(row groups, passes)
+  static_assert((size_t)(kDecEPB + kDecRT) * (KCH1 * 256 + 4) * sizeof(float) <=
+                    ring_res_bytes(kRingWideGroups, kRingMaxPasses),
+                "a chain job's operands fit the partial buffers");
+  // partials, ring_res_bytes(row groups, passes); 16-byte aligned for the
+  // chain jobs' float4 reads
+  extern __shared__ __align__(16) float res[];
   __shared__ RingShared sh;
   __shared__ RouteShared rsh;  // deferred routing only
-  __shared__ float s_bias[kExperts];
-  __shared__ int s_nact, s_maxcnt;
+  __shared__ int s_nact, s_maxcnt, s_job, s_fin;
   const Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
-  const bool local = c->deferred != 0;  // the router stopped after the logits
+  // 1: the router stopped after the logits; 2: it wrote score bounds, and the
+  // logits are this kernel's chain jobs
+  const int mode = c->deferred;
+  const bool local = mode != 0;
   if (tid < 2) sh.done[tid] = 0;
+  // Chain jobs (mode 2) go to the first of blocks 0..kChainClaimBlocks-1 to
+  // start, which claim their first row task after the job (a row task held
+  // through a job would hold up its expert's down tasks); the other blocks
+  // claim a row task at once and leave the chain-job counter alone (claims
+  // on one cache line serialise).  Jobs that blocks 0..15 leave unclaimed are
+  // run by the waits that need them.
+  const bool chain_try = mode == 2 && !c->chain_lazy && blockIdx.x < kChainClaimBlocks;
   if (tid == 0) {
     sh.flushed = 0;
     sh.abort = 0;
     sh.local = local ? 1 : 0;
+    const int job = chain_try ? claim(&a.s.ctrl->chain_head) : kChainJobs;
+    s_job = job;
     // every task, the first included, is claimed from the queue, so only a
     // block that is running owns one (blocks not yet resident own nothing
     // another block waits for)
-    sh.seq[0] = claim(&a.s.ctrl->head);
+    if (job >= kChainJobs) sh.seq[0] = claim(&a.s.ctrl->head);
     sh.nseq = 1;
   }
+  bool claim_late = false;  // the first row task is claimed after a chain job
   RingPlan pl;
   pl.ncomb = a.T;  // combine tasks: one per token
   pl.grid = gridDim.x;
@@ -1996,62 +2346,134 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     return;
   }
   if (local) {
-    // One token block (T <= 8), 16-row tasks: every block routes the tokens
-    // from the logits and plans the launch itself, as the router's last
-    // block would (same functions, same order), and block 0 publishes the
-    // routing for the host.  Slot = offsets[e] + in-block rank.
-    // the thread's logit and the bias are loaded together, before one barrier
-    const int ltl = tid >> 5;
-    const float l = tid < kDecRT * kExperts && ltl < a.T ? a.s.logits[tid] : 0.0f;
-    if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
-    __syncthreads();
-    route_token_block(rsh, a.T, s_bias, l);
-    if (tid < kExperts) {  // lanes 0-31 of wave 0
-      const int cnt = rsh.cnt[tid];
-      int total = 0;
-      const int off = lane_scan32(cnt, tid, &total);
-      int mc = cnt;
-#pragma unroll
-      for (int o = 16; o > 0; o >>= 1) mc = max(mc, __shfl_xor(mc, o, 32));
-      const unsigned long long act = __ballot(cnt > 0);
-      const int nact = __popcll(act);
-      const int aidx = __popcll(act & ((1ull << tid) - 1ull));
-      sh.counts[tid] = cnt;
-      sh.offsets[tid] = off;
-      if (cnt > 0) sh.active[aidx] = tid;
-      if (tid >= nact) sh.active[tid] = -1;
-      if (tid == 0) {
-        s_nact = nact;
-        s_maxcnt = mc;
+    // One token block (T <= 8), 16-row tasks: every block plans the launch
+    // itself, as the router's last block would (same functions, same order).
+    // Slot = offsets[e] + in-block rank.
+    const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
+    const int tl = (tid >> 5) & (kDecRT - 1), e = tid & (kExperts - 1);
+    const bool pair = tid < kDecRT * kExperts;
+    bool settled = false, chosen = false;
+    float l = 0.0f;
+    if (mode == 2) {
+      // The bounds settle a token when four of its experts each have fewer
+      // than four others whose upper bound reaches their lower bound: those
+      // four are then its exact top-4 whatever the logits' rounding, and the
+      // slots, which depend on the sets only, follow.  The logits (chain
+      // jobs) are needed only by the combine, for the weights and rank
+      // order.
+      float lo = 0.0f, hi = 0.0f;
+      if (pair && tl < a.T) {
+        lo = c->sbound[0][tl][e];
+        hi = c->sbound[1][tl][e];
       }
-      if (blockIdx.x == 0) {
-        Ctrl *cw = a.s.ctrl;
-        cw->counts[tid] = cnt;
-        cw->offsets[tid] = off;
-        if (cnt > 0) cw->active[aidx] = tid;
-        if (tid >= nact) cw->active[tid] = -1;
+      if (tid < kExperts) sh.bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
+      __syncthreads();
+      claim_late = s_job < kChainJobs;
+      if (claim_late) ring_chain_job(a, sh, rsh, &s_fin, s_job, res);
+      if (pair) rsh.prob[tl][e] = hi;
+      __syncthreads();
+      bool fin = true;
+      if (pair && tl < a.T) {
+        fin = __builtin_isfinite(lo) && __builtin_isfinite(hi) && lo > -1e30f;
+        int above = 0;
+#pragma unroll
+        for (int j0 = 0; j0 < kExperts; j0 += 8) {
+          float hv[8];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) hv[j] = rsh.prob[tl][j0 + j];
+#pragma unroll
+          for (int j = 0; j < 8; ++j) above += (int)((j0 + j != e) & (hv[j] >= lo));
+        }
+        chosen = fin && above < kTopK;
+      }
+      const int half = (tid & 63) >> 5;
+      const uint32_t gin = (uint32_t)(__ballot(chosen) >> (32 * half));
+      const uint32_t gfin = (uint32_t)(__ballot(fin) >> (32 * half));
+      const bool tok_ok = !pair || tl >= a.T || (__popc(gin) == kTopK && gfin == 0xffffffffu);
+      settled = __syncthreads_and(tok_ok) != 0;
+      if (!settled) {
+        // some token's top-4 is open: run the chain jobs nobody has claimed,
+        // wait for the others (all claimed by running blocks, and a job
+        // never waits), then route from the logits
+        for (;;) {
+          if (tid == 0) s_job = claim(&a.s.ctrl->chain_head);
+          __syncthreads();
+          const int j = s_job;
+          __syncthreads();
+          if (j >= kChainJobs) break;
+          ring_chain_job(a, sh, rsh, &s_fin, j, res);
+        }
         if (tid == 0) {
-          cw->offsets[kExperts] = total;
-          cw->n_active = nact;
-          cw->max_count = mc;
+          const long long t0 = ring_now();
+          while (load_relaxed(&a.s.ctrl->chain_done) < kChainJobs) {
+            if (ring_now() - t0 > ticks) {
+              st_agent(&a.s.ctrl->err, 1);
+              sh.abort = 1;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+          }
+        }
+        __syncthreads();
+        if (sh.abort) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        if (pair && tl < a.T)
+          l = __hip_atomic_load(&a.s.logits[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    } else {
+      // the thread's logit and the bias are loaded together, before one barrier
+      l = pair && tl < a.T ? a.s.logits[tid] : 0.0f;
+      if (tid < kExperts) sh.bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
+      __syncthreads();
+    }
+    if (settled) {
+      // per-expert counts and each chosen pair's rank among the block's
+      // tokens, from the settled sets
+      if (pair) rsh.sel[tl][e] = chosen ? 1 : 0;
+      __syncthreads();
+      int before = 0;
+      if (pair && tl < a.T) {
+        int all = 0;
+#pragma unroll
+        for (int t2 = 0; t2 < kDecRT; ++t2) {
+          const int ch = rsh.sel[t2][e];
+          before += ch & (t2 < tl);
+          all += ch;
+        }
+        if (tl == 0) rsh.cnt[e] = all;
+      }
+      __syncthreads();
+      ring_expert_table(a, sh, rsh, blockIdx.x == 0, &s_nact, &s_maxcnt);
+      __syncthreads();
+      if (pair) {
+        const int slot = chosen ? sh.offsets[e] + before : -1;
+        sh.slotmap[tl][e] = slot;
+        if (slot >= 0) {
+          sh.tok[slot] = tl;
+          if (blockIdx.x == 0) st_agent(&a.s.slot_token[slot], tl);
+        }
+      }
+      if (tid == 0) sh.local = 2;  // the combine routes each token from its logits
+    } else {
+      route_token_block(rsh, a.T, sh.bias, l);
+      ring_expert_table(a, sh, rsh, blockIdx.x == 0, &s_nact, &s_maxcnt);
+      __syncthreads();
+      if (tid < a.T * kTopK) {
+        const int t = tid / kTopK, k = tid % kTopK;
+        const int ex = rsh.ti[t][k];
+        const int slot = ex >= 0 ? sh.offsets[ex] + rsh.rank[t][k] : -1;
+        if (slot >= 0) sh.tok[slot] = t;
+        sh.rpos[t][k] = slot;
+        sh.rw[t][k] = rsh.tw[t][k];
+        if (blockIdx.x == 0) {
+          st_agent(&a.s.idx[tid], ex);
+          a.s.wts[tid] = rsh.tw[t][k];
+          st_agent(&a.s.pos[tid], slot);
+          if (slot >= 0) st_agent(&a.s.slot_token[slot], t);
         }
       }
     }
     __syncthreads();
-    if (tid < a.T * kTopK) {
-      const int t = tid / kTopK, k = tid % kTopK;
-      const int e = rsh.ti[t][k];
-      const int slot = e >= 0 ? sh.offsets[e] + rsh.rank[t][k] : -1;
-      if (slot >= 0) sh.tok[slot] = t;
-      sh.rpos[t][k] = slot;
-      sh.rw[t][k] = rsh.tw[t][k];
-      if (blockIdx.x == 0) {
-        st_agent(&a.s.idx[tid], e);
-        a.s.wts[tid] = rsh.tw[t][k];
-        st_agent(&a.s.pos[tid], slot);
-        if (slot >= 0) st_agent(&a.s.slot_token[slot], t);
-      }
-    }
     const int units = s_nact;  // read after the barrier above
     pl.rows = kStreamRows;
     pl.p1u = a.I / (kStreamRows / 2);
@@ -2096,6 +2518,7 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
       return;
     }
   }
+  if (claim_late && tid == 0) sh.seq[0] = claim(&a.s.ctrl->head);
   __syncthreads();
   const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
   if (pl.rows == kStreamRows) {

@@ -170,6 +170,11 @@ class SparseMoeBlock:
     def set_wait_divisor(self, d: int) -> None:
         _native.check(_native.lib().moe_set_wait_divisor(self._ctx, int(d)), "moe_set_wait_divisor")
 
+    def set_lazy_chains(self, on: bool) -> None:
+        """Test hook: decode routing leaves its logit chains to the waits that
+        need them (the path of an expert kernel whose blocks start late)."""
+        _native.check(_native.lib().moe_set_lazy_chains(self._ctx, int(bool(on))), "moe_set_lazy_chains")
+
     def close(self) -> None:
         if self._ctx:
             _native.lib().moe_destroy(self._ctx)

@@ -214,6 +214,13 @@ int moe_force_tile_rows(moe_ctx *ctx, int rows);
  * every kernel still exits normally. */
 int moe_set_wait_divisor(moe_ctx *ctx, int divisor);
 
+/* Test hook: with on != 0, moe_forward's routing of a decode batch (<= 8
+ * tokens, weight-streaming plan) leaves the gate-logit chains to the expert
+ * kernel's waits that need them instead of to its first blocks: the path its
+ * combine and fallback take when blocks start late because other kernels hold
+ * the GPU.  Results are unchanged; only the timing differs. */
+int moe_set_lazy_chains(moe_ctx *ctx, int on);
+
 const char *moe_strerror(int status);
 
 /* Library version string ("final_amd-moe <semver> gfx950"). */

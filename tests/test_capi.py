@@ -110,6 +110,7 @@ def test_argument_validation_before_any_gpu_call(L):
     assert L.moe_plan_tile_rows(None, 64) == -1
     assert L.moe_force_tile_rows(None, 0) == _native.MOE_ERR_INVALID_ARG
     assert L.moe_set_wait_divisor(None, 2) == _native.MOE_ERR_INVALID_ARG
+    assert L.moe_set_lazy_chains(None, 1) == _native.MOE_ERR_INVALID_ARG
 
 
 def test_error_raises_with_status():

@@ -345,51 +345,112 @@ def test_readback_checks_token_count(block, real_weights):
                               None) == _native.MOE_ERR_INVALID_ARG
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("T", [1, 3, 8])
-def test_forward_routes_in_expert_kernel(T, block, real_weights, oracle_mod):
-    """One decode token block under the streaming plan: moe_forward lets the
-    router stop after the logits and the expert kernel route and plan in its
-    own blocks.  Its routing (idx, w, counts, logits) and y must be
-    bit-identical to moe_route + moe_experts, where the router finishes and
-    plans, and match the oracle.  A hot expert (bias +10) makes several
-    tokens share an expert, so the in-block ranks and slots are exercised."""
+def _forward_vs_route_experts(block, w, T, x, r, label, lazy=False):
+    """y and routing of moe_forward (deferred decode routing) and of moe_route +
+    moe_experts (the router finishes and plans) on the same inputs."""
     from final_amd import hip
     from final_amd import workloads as W
-    w = dict(real_weights)
-    bias = np.array(real_weights["bias"], np.float32).copy()
-    bias[11] += 10.0
-    w["bias"] = bias
     block.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+    dx = hip.DeviceArray.from_numpy(x)
+    dr = hip.DeviceArray.from_numpy(r)
+    say(f"[{label}] T={T} lazy={lazy} moe_forward")
+    block.set_lazy_chains(lazy)
     try:
-        assert block.plan(T) == 0
-        x = W.gen_x(T, seed=60 + T)
-        r = W.gen_x(T, seed=70 + T)
-        dx = hip.DeviceArray.from_numpy(x)
-        dr = hip.DeviceArray.from_numpy(r)
-        say(f"[deferred routing] T={T} moe_forward")
         dy1 = hip.DeviceArray((T, W.H))
         block.forward_gpu(dx, dy1, T, residual=dr)
         hip.synchronize()
         block.check_device()
         rt1 = block.last_routing()
-        say(f"[deferred routing] T={T} moe_route + moe_experts")
-        dy2 = hip.DeviceArray((T, W.H))
-        block.route(dx, T)
-        block.experts(dx, dy2, T, residual=dr)
-        hip.synchronize()
-        block.check_device()
-        rt2 = block.last_routing()
     finally:
-        rw = real_weights
-        block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
-    y1, y2 = dy1.download(), dy2.download()
+        block.set_lazy_chains(False)
+    say(f"[{label}] T={T} moe_route + moe_experts")
+    dy2 = hip.DeviceArray((T, W.H))
+    block.route(dx, T)
+    block.experts(dx, dy2, T, residual=dr)
+    hip.synchronize()
+    block.check_device()
+    rt2 = block.last_routing()
+    return dy1.download(), rt1, dy2.download(), rt2
+
+
+def _check_same(y1, rt1, y2, rt2):
     assert np.array_equal(bits(y1), bits(y2))
     for k in ("idx", "counts"):
         assert np.array_equal(rt1[k], rt2[k])
     for k in ("w", "logits"):
         assert np.array_equal(bits(rt1[k]), bits(rt2[k]))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lazy", [False, True])
+@pytest.mark.parametrize("T", [1, 3, 8])
+def test_forward_routes_in_expert_kernel(T, lazy, block, real_weights, oracle_mod):
+    """One decode token block under the streaming plan: moe_forward's router
+    writes only bounds of each score (double sums of the gate products and a
+    bound of the FMA chain's rounding), the expert kernel takes each token's
+    top-4 set from them, streams, computes the logits in chain jobs meanwhile
+    and ranks and weights each token from its logits in the combine.  Its
+    routing (idx, w, counts, logits) and y must be bit-identical to moe_route
+    + moe_experts, where the router computes the logits and routes, and
+    match the oracle.  A hot expert (bias +10) makes several tokens share an
+    expert, so the in-block ranks and slots are exercised.  lazy: the chain
+    jobs are left to the combine's waits, which run them one wave each (the
+    path of blocks that start late)."""
+    from final_amd import workloads as W
+    w = dict(real_weights)
+    bias = np.array(real_weights["bias"], np.float32).copy()
+    bias[11] += 10.0
+    w["bias"] = bias
+    try:
+        assert block.plan(T) == 0
+        x = W.gen_x(T, seed=60 + T)
+        r = W.gen_x(T, seed=70 + T)
+        y1, rt1, y2, rt2 = _forward_vs_route_experts(block, w, T, x, r, "deferred routing", lazy)
+    finally:
+        rw = real_weights
+        block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
+    _check_same(y1, rt1, y2, rt2)
     assert rt1["counts"][11] == T
+    ref = oracle_forward(oracle_mod, w, x, residual=r)
+    check_routing(rt1, ref)
+    np.testing.assert_allclose(y1, ref["y"], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("lazy", [False, True])
+@pytest.mark.parametrize("T", [1, 8])
+def test_forward_routing_tie_waits_for_logits(T, lazy, block, real_weights, oracle_mod):
+    """A score tie at the top-4 boundary, which no bound can settle: token 0's
+    fifth expert gets the gate row and bias of its fourth, so their logits
+    and scores are equal and each has four experts whose upper bound reaches
+    its lower bound.  The expert kernel must then wait for the chain jobs
+    (running any that are unclaimed, all of them when lazy) and route every
+    token from the logits, with the reference's tie rule (the lower index
+    wins), bit-identical to moe_route + moe_experts and to the oracle."""
+    from final_amd import workloads as W
+    x = W.gen_x(T, seed=90 + T)
+    r = W.gen_x(T, seed=95 + T)
+    w = dict(real_weights)
+    ref0 = oracle_forward(oracle_mod, w, x)
+    l0 = np.asarray(ref0["logits"][0], np.float64)
+    score = 1.0 / (1.0 + np.exp(-l0)) + np.asarray(w["bias"], np.float64)
+    order = np.argsort(-score, kind="stable")
+    e4, e5 = int(order[3]), int(order[4])
+    gate = np.array(w["gate"], np.float32).copy()
+    bias = np.array(w["bias"], np.float32).copy()
+    gate[e5] = gate[e4]
+    bias[e5] = bias[e4]
+    w["gate"], w["bias"] = gate, bias
+    try:
+        assert block.plan(T) == 0
+        y1, rt1, y2, rt2 = _forward_vs_route_experts(block, w, T, x, r, "tie", lazy)
+    finally:
+        rw = real_weights
+        block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
+    _check_same(y1, rt1, y2, rt2)
+    lg = rt1["logits"]
+    assert lg[0, e4] == lg[0, e5]
+    assert min(e4, e5) in rt1["idx"][0].tolist() and max(e4, e5) not in rt1["idx"][0].tolist()
     ref = oracle_forward(oracle_mod, w, x, residual=r)
     check_routing(rt1, ref)
     np.testing.assert_allclose(y1, ref["y"], rtol=RTOL, atol=ATOL)
