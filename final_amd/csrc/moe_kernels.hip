@@ -1767,7 +1767,8 @@ __device__ __forceinline__ void ring_chain_job(const ExpertArgs &a, RingShared &
   }
   __syncthreads();  // the staging buffers are free again
   if (*s_flag) {
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // the other jobs' logits: stored before they counted in, read with
+    // agent-scope loads
     const int tl = (tid >> 5) & (kDecRT - 1), e = tid & (kExperts - 1);
     const float l = tid < kDecRT * kExperts && tl < T
                         ? __hip_atomic_load(&a.s.logits[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
@@ -1837,7 +1838,8 @@ __device__ __forceinline__ bool ring_route_exact(const ExpertArgs &a, RingShared
       else __builtin_amdgcn_s_sleep(1);
     }
   }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  // agent-scope loads of logits whose stores completed before their jobs
+  // counted in (no acquire fence needed)
   const float l = __hip_atomic_load(&a.s.logits[(size_t)tok * kExperts + e], __ATOMIC_RELAXED,
                                     __HIP_MEMORY_SCOPE_AGENT);
   const float p = ref_sigmoid(l);
@@ -2396,7 +2398,11 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
         // wait for the others (all claimed by running blocks, and a job
         // never waits), then route from the logits
         for (;;) {
-          if (tid == 0) s_job = claim(&a.s.ctrl->chain_head);
+          // a read first: most blocks find every job claimed and take no
+          // atomic on the counter
+          if (tid == 0)
+            s_job = load_relaxed(&a.s.ctrl->chain_head) < kChainJobs ? claim(&a.s.ctrl->chain_head)
+                                                                      : kChainJobs;
           __syncthreads();
           const int j = s_job;
           __syncthreads();
@@ -2411,12 +2417,14 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
               sh.abort = 1;
               break;
             }
-            __builtin_amdgcn_s_sleep(1);
+            __builtin_amdgcn_s_sleep(8);
           }
         }
         __syncthreads();
         if (sh.abort) return;
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+        // the logits' stores completed before their jobs counted in, and
+        // agent-scope loads read them from the coherent level: no acquire
+        // fence (each one invalidates the XCD's L2, 256 of them cost ~15 us)
         if (pair && tl < a.T)
           l = __hip_atomic_load(&a.s.logits[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
