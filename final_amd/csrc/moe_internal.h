@@ -60,8 +60,7 @@ struct Ctrl {
   int stream_rows;  // streaming plan: weight rows per task (16, 32 or 64)
   int max_count;    // tokens of the largest expert
   int slots_assigned;  // MFMA plans: the router wrote every slot (pos = slot, slot_token)
-  // 0: the router routed and planned; 1: it stopped after the logits and the
-  // streaming kernel routes and plans; 2: it wrote score bounds (sbound), and
+  // 0: the router routed and planned; 2: it wrote score bounds (sbound), and
   // the streaming kernel computes the logits (chain jobs) and routes from the
   // bounds where they settle every token's top-4
   int deferred;
@@ -117,7 +116,7 @@ struct RouterArgs {
   int bn;                // MFMA n-tile width (columns of the B tile)
   int tail_units;        // MFMA plans: last units whose down tiles run at half width
   int max_units;
-  int defer;             // 1: stop after the logits; 2: score bounds only (router_can_defer)
+  int defer;             // 2: score bounds instead of the logits (router_can_defer); else 0
   int lazy_chains;       // defer == 2: Ctrl::chain_lazy
   const float *norm_w;   // post-attention RMSNorm weight [H]: x is h, normalise it (decode router only)
   float *xn;             // [T][H]: the normalised rows, for the expert kernel

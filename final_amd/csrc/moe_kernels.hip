@@ -938,7 +938,6 @@ void router_decode_kernel(RouterArgs a) {
     // waves 1-3, idle during the chains, prepare the expert kernel's rows
     fill_unwritten(a, blockIdx.x, gridDim.x, tid - 64, kThreads - 64);
   }
-  if (a.defer) return;  // logits only
   // 3. the last of the token block's 8 blocks finishes it
   __builtin_amdgcn_s_waitcnt(0);  // this block's logits are stored
   __syncthreads();
@@ -1769,7 +1768,7 @@ __device__ __forceinline__ void ring_chain_job(const ExpertArgs &a, RingShared &
   if (*s_flag) {
     // the other jobs' logits: stored before they counted in, read with
     // agent-scope loads
-    const int tl = (tid >> 5) & (kDecRT - 1), e = tid & (kExperts - 1);
+    const int tl = (tid >> 5) & (kDecRT - 1);
     const float l = tid < kDecRT * kExperts && tl < T
                         ? __hip_atomic_load(&a.s.logits[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                         : 0.0f;
@@ -2314,10 +2313,10 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   __shared__ int s_nact, s_maxcnt, s_job, s_fin;
   const Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
-  // 1: the router stopped after the logits; 2: it wrote score bounds, and the
-  // logits are this kernel's chain jobs
+  // 2: the router wrote score bounds, and the logits are this kernel's chain
+  // jobs (0: the router routed and planned)
   const int mode = c->deferred;
-  const bool local = mode != 0;
+  const bool local = mode == 2;
   if (tid < 2) sh.done[tid] = 0;
   // Chain jobs (mode 2) go to the first of blocks 0..kChainClaimBlocks-1 to
   // start, which claim their first row task after the job (a row task held
@@ -2356,7 +2355,7 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     const bool pair = tid < kDecRT * kExperts;
     bool settled = false, chosen = false;
     float l = 0.0f;
-    if (mode == 2) {
+    {
       // The bounds settle a token when four of its experts each have fewer
       // than four others whose upper bound reaches their lower bound: those
       // four are then its exact top-4 whatever the logits' rounding, and the
@@ -2428,11 +2427,6 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
         if (pair && tl < a.T)
           l = __hip_atomic_load(&a.s.logits[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
-    } else {
-      // the thread's logit and the bias are loaded together, before one barrier
-      l = pair && tl < a.T ? a.s.logits[tid] : 0.0f;
-      if (tid < kExperts) sh.bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
-      __syncthreads();
     }
     if (settled) {
       // per-expert counts and each chosen pair's rank among the block's
