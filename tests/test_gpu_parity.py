@@ -417,6 +417,26 @@ def test_forward_routes_in_expert_kernel(T, lazy, block, real_weights, oracle_mo
 
 
 @pytest.mark.gpu
+def test_forward_routing_random_batches(block, real_weights, oracle_mod):
+    """48 random decode batches of 1-8 tokens through moe_forward's routing
+    from score bounds: with these weights about 4 % of random tokens have a
+    4th/5th score gap inside the bounds, so the batches mix the settled path
+    and the fallback (10 of these 48 fall back, by the bound restated on the
+    CPU).  Each must give the routing (idx, w, counts, logits)
+    and y of moe_route + moe_experts bit for bit, and the oracle's routing."""
+    from final_amd import workloads as W
+    w = real_weights
+    rng = np.random.default_rng(2024)
+    for i in range(48):
+        T = 1 + i % 8
+        x = rng.standard_normal((T, W.H)).astype(np.float32)
+        r = rng.standard_normal((T, W.H)).astype(np.float32)
+        y1, rt1, y2, rt2 = _forward_vs_route_experts(block, w, T, x, r, f"random batch {i}")
+        _check_same(y1, rt1, y2, rt2)
+        check_routing(rt1, oracle_forward(oracle_mod, w, x, residual=r))
+
+
+@pytest.mark.gpu
 @pytest.mark.parametrize("lazy", [False, True])
 @pytest.mark.parametrize("T", [1, 8])
 def test_forward_routing_tie_waits_for_logits(T, lazy, block, real_weights, oracle_mod):
