@@ -11,14 +11,17 @@ Prints ONE JSON line on stdout (progress goes to stderr):
                 workloads) or bytes (weight-streaming workloads) per launch,
                 divided by its average launch time from HIP events recorded on
                 the launch stream around each expert-kernel launch, in a second
-                pass of the same steps after the timed ones
+                pass of the same steps after the timed ones (moe_forward's own
+                two launches: moe_route_forward, then moe_experts)
   cpu_baseline  the CPU oracle (a restatement of the reference's arithmetic)
                 on this host, median of a few runs
   sweep         the other configurations measured the same way in the same
                 run: the decode shapes T = 1, 8, 64, 256 (four weight copies
                 cycled so the 256 MB Infinity Cache cannot serve them; T=64 is
                 also the reference's CPU-runnable case and carries its CPU
-                baseline), the skewed-routing T=16384 case, and the whole
+                baseline), T = 1 and 8 again over 32 random batches each (mean
+                step; the seed-0 batches' scores are well separated), the
+                skewed-routing T=16384 case, and the whole
                 24-layer decoder forward at batch 64 x seq 512 (embedding, 6
                 attention + 18 short-conv layers, each with the MoE FFN, final
                 norm and LM head)
@@ -216,7 +219,7 @@ def measure_moe(name, w, x, steps, warmup, nsets):
         b = blocks[i % nsets]
         e0, e1, e2 = ev[i]
         e0.record(stream)
-        b.route(dx, T, stream=stream)
+        b.route_forward(dx, T, stream=stream)  # the forward's own two launches
         e1.record(stream)
         b.experts(dx, dy, T, stream=stream)
         e2.record(stream)
@@ -234,12 +237,77 @@ def measure_moe(name, w, x, steps, warmup, nsets):
     nbytes = W.algorithmic_bytes(counts, T) - (W.E * W.H * 4 + W.E * 4)
     roof = roofline(plan, flops, nbytes, exp_ms, name)
     roof["router_ms"] = round(route_ms, 4)
+    roof["kernel_path"] = "moe_forward's two launches (moe_route_forward, moe_experts)"
     return {"workload": name, "tokens": T, "ms_per_step": round(ms_step, 4),
             "tokens_per_s": round(T * steps / (total_ms / 1e3), 1), "steps": steps,
             "plan_tile_rows": plan, "weight_sets": nsets,
             "active_experts": int((counts > 0).sum()), "zero_token_experts": int((counts == 0).sum()),
             "max_expert_tokens": int(counts.max()), "counts": [int(c) for c in counts],
             "wall_s": round(wall, 4), "roofline": roof}
+
+
+RANDOM_BATCHES = 32
+RANDOM_SEED = 20260
+
+
+def measure_decode_random(T, w, steps, warmup, nsets, nbatch=RANDOM_BATCHES):
+    """Decode steps over nbatch random batches of T tokens (N(0, 1), drawn
+    from a fixed generator, not the seed-0 tokens): each batch runs `steps`
+    back-to-back forwards (nsets weight copies cycled) timed with events.
+    Reports the mean step over the batches and how many batches planned
+    slots beyond their top-4: a token whose 4th/5th score gap lies inside
+    the score bounds gets a slot for every expert the bounds leave possible,
+    which streams a 5th expert's weights if no other token chose it."""
+    import numpy as np
+
+    from final_amd import SparseMoeBlock, hip
+    from final_amd import workloads as W
+    blocks = []
+    for _ in range(nsets):
+        b = SparseMoeBlock(max_tokens=max(T, 64))
+        b.set_weights(w["gate"], w["bias"], w["w1"], w["w3"], w["w2"])
+        blocks.append(b)
+    stream = hip.Stream()
+    rng = np.random.default_rng(RANDOM_SEED + T)
+    xs = [hip.DeviceArray.from_numpy(rng.standard_normal((T, W.H)).astype(np.float32))
+          for _ in range(nbatch)]
+    dy = hip.DeviceArray((T, W.H))
+    log(f"[bench] decode_t{T}_random: {nbatch} random batches of T={T}, weight sets={nsets}")
+    settle_clock(lambda i: blocks[i % nsets].forward_gpu(xs[i % nbatch], dy, T, stream=stream),
+                 stream)
+    per, extra, nbytes = [], [], []
+    for j, dx in enumerate(xs):
+        for i in range(warmup):
+            blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream)
+        start, stop = hip.Event(), hip.Event()
+        start.record(stream)
+        for i in range(steps):
+            blocks[i % nsets].forward_gpu(dx, dy, T, stream=stream)
+        stop.record(stream)
+        stop.synchronize()
+        per.append(start.elapsed_ms(stop) / steps)
+        b = blocks[(steps - 1) % nsets]
+        counts = b.last_routing(stream)["counts"]
+        plan = b.last_plan_counts(stream)
+        extra.append(int(plan.sum() - counts.sum()))
+        nbytes.append(W.algorithmic_bytes(counts, T) - (W.E * W.H * 4 + W.E * 4))
+    for b in blocks:
+        b.check_device(stream)
+        b.close()
+    mean_ms = statistics.mean(per)
+    achieved = sum(nbytes) / (sum(per) / 1e3) / 1e9
+    return {"workload": f"decode_t{T}_random", "tokens": T, "batches": nbatch,
+            "ms_per_step": round(mean_ms, 4), "ms_per_step_p50": round(statistics.median(per), 4),
+            "ms_per_step_max": round(max(per), 4), "tokens_per_s": round(T / (mean_ms / 1e3), 1),
+            "steps_per_batch": steps, "weight_sets": nsets,
+            "batches_with_extra_slots": sum(1 for e in extra if e > 0),
+            "extra_slots": sum(extra),
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                         "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                         "scope": "whole step (router + expert kernel), algorithmic bytes of "
+                                  "each batch's exact routing"},
+            "data": f"synthetic: {nbatch} batches of N(0,1) tokens (numpy default_rng("
+                    f"{RANDOM_SEED + T})), seed-0 weights"}
 
 
 def model_flops(batch, seq, layer_types, vocab=65536):
@@ -479,6 +547,9 @@ def main():
                 log(f"[bench] CPU oracle baseline at T=64, {threads} threads")
                 e["cpu_baseline"] = cpu_baseline(ws, xs, threads, single_tokens=64, min_s=10.0)
             sweep[name] = e
+            if name in ("decode_t1", "decode_t8"):
+                sweep[name + "_random"] = measure_decode_random(
+                    s.T, ws, 10, 2, weight_sets_for(s.T, args.weight_sets))
         sweep["lfm2_b64_s512"] = measure_model(args.model_steps, 1)
         out["sweep"] = sweep
     print(json.dumps(out), flush=True)

@@ -27,7 +27,7 @@ CAPI_SYMBOLS = (
     "moe_strerror", "moe_version", "moe_set_norm_weight", "moe_forward_norm",
     "moe_last_normed", "moe_dense_create", "moe_dense_set_weights", "moe_dense_forward",
     "moe_forward_noalloc", "moe_create_shared", "moe_dense_create_shared",
-    "moe_set_lazy_chains",
+    "moe_set_lazy_chains", "moe_route_forward", "moe_last_plan_counts",
 )
 LFM_SYMBOLS = (
     "lfm_gemm_nt", "lfm_embed", "lfm_rmsnorm", "lfm_qk_norm_rope", "lfm_attention",
@@ -83,6 +83,8 @@ def lib() -> ctypes.CDLL:
     L.moe_forward.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
     L.moe_forward_noalloc.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
     L.moe_route.argtypes = [_vp, _vp, _i, _vp]
+    L.moe_route_forward.argtypes = [_vp, _vp, _i, _vp]
+    L.moe_last_plan_counts.argtypes = [_vp, _vp, _vp]
     L.moe_experts.argtypes = [_vp, _vp, _vp, _vp, _i, _vp]
     L.moe_route_logits.argtypes = [_vp, _vp, _i, _vp]
     L.moe_last_routing.argtypes = [_vp, _vp, _vp, _vp, _vp, _i, _vp]

@@ -124,6 +124,7 @@ static bool noalloc_layout(char *base, int T, int H, int I, Scratch *s, int *max
   s->sout = reinterpret_cast<float *>(take(S * H * sizeof(float)));
   s->inter_bytes = (uint32_t)(S * I * sizeof(float));
   s->sout_bytes = (uint32_t)(S * H * sizeof(float));
+  s->slot_cap = (int)S;
   *max_units = (int)(S / 32 + E + 1);
   return off <= kNoAllocBytes;
 }
@@ -265,7 +266,12 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
   ctx->stream_ok = stream_supported(d.hidden, d.inter);
   ctx->dense = dense;
   const size_t H = d.hidden, I = d.inter, E = kExperts;
-  const size_t Tm = d.max_tokens, S = Tm * kTopK;
+  const size_t Tm = d.max_tokens;
+  // slot rows: the top-4 of every token, or the slots of every possible
+  // expert of a deferred decode routing (moe_forward up to kDeferTokens
+  // tokens), whichever is more
+  const size_t Ts = Tm < (size_t)kDeferTokens ? Tm : (size_t)kDeferTokens;
+  const size_t S = Tm * kTopK > Ts * kSpecSlots ? Tm * kTopK : Ts * kSpecSlots;
   const size_t nb = (Tm + kMinRouterTokens - 1) / kMinRouterTokens;
   ctx->max_units = (int)(S / 32 + E + 1);
   // inter and sout are addressed with 32-bit byte offsets, and the MFMA
@@ -317,6 +323,7 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
   }
   ctx->s.inter_bytes = (uint32_t)(S * I * sizeof(float));
   ctx->s.sout_bytes = (uint32_t)(S * H * sizeof(float));
+  ctx->s.slot_cap = (int)S;
   char *ctrl_mem = nullptr;
   // Ctrl, then dep[max_units]
   const size_t ctrl_bytes = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
@@ -534,6 +541,10 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
 
 int moe_route(moe_ctx *ctx, const float *x, int num_tokens, moe_stream_t stream) {
   return do_route(ctx, x, nullptr, num_tokens, stream);
+}
+
+int moe_route_forward(moe_ctx *ctx, const float *x, int num_tokens, moe_stream_t stream) {
+  return do_route(ctx, x, nullptr, num_tokens, stream, nullptr, nullptr, true);
 }
 
 int moe_route_logits(moe_ctx *ctx, const float *logits, int num_tokens,
@@ -818,13 +829,45 @@ int moe_last_routing(moe_ctx *ctx, int *idx, float *w, int *counts, float *logit
   if (w && hipMemcpyAsync(w, ctx->s.wts, T * kTopK * sizeof(float),
                           hipMemcpyDeviceToHost, st) != hipSuccess)
     return MOE_ERR_HIP;
-  if (counts && hipMemcpyAsync(counts, ctx->s.ctrl->counts, kExperts * sizeof(int),
-                               hipMemcpyDeviceToHost, st) != hipSuccess)
-    return MOE_ERR_HIP;
+  // counts: tokens per expert of the routing, the histogram of idx
+  // (layer.cu:494-497 counts every (token, rank) selection); the plan's own
+  // counts are per slot, and a deferred decode routing plans a slot for
+  // every expert a token's score bounds leave possible
+  std::vector<int> idx_own;
+  int *idx_h = idx;
+  if (counts && !idx_h) {
+    idx_own.resize(T * kTopK);
+    idx_h = idx_own.data();
+    if (hipMemcpyAsync(idx_h, ctx->s.idx, T * kTopK * sizeof(int), hipMemcpyDeviceToHost, st) !=
+        hipSuccess)
+      return MOE_ERR_HIP;
+  }
   if (logits && hipMemcpyAsync(logits, ctx->s.logits, T * kExperts * sizeof(float),
                                hipMemcpyDeviceToHost, st) != hipSuccess)
     return MOE_ERR_HIP;
   if (hipStreamSynchronize(st) != hipSuccess) return MOE_ERR_HIP;
+  if (counts) {
+    for (int e = 0; e < kExperts; ++e) counts[e] = 0;
+    for (size_t i = 0; i < T * kTopK; ++i)
+      if (idx_h[i] >= 0 && idx_h[i] < kExperts) ++counts[idx_h[i]];
+  }
+  return MOE_OK;
+}
+
+int moe_last_plan_counts(moe_ctx *ctx, int *counts, moe_stream_t stream) {
+  if (!ctx || !counts) return MOE_ERR_INVALID_ARG;
+  if (ctx->routed_T < 0) return MOE_ERR_NOT_READY;
+  DeviceGuard g(ctx->device);
+  if (!g.ok) return MOE_ERR_HIP;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (ctx->routed_T == 0) {
+    memset(counts, 0, sizeof(int) * kExperts);
+    return MOE_OK;
+  }
+  if (hipMemcpyAsync(counts, ctx->s.ctrl->counts, kExperts * sizeof(int), hipMemcpyDeviceToHost,
+                     st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return MOE_ERR_HIP;
   return MOE_OK;
 }
 

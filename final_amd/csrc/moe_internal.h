@@ -37,6 +37,10 @@ constexpr int kRingTailUnits = 6;
 constexpr int kDeferTokens = 8;
 // Gate-logit chain jobs of a certified decode routing: 4 experts each.
 constexpr int kChainJobs = kExperts / 4;
+// A deferred decode routing gives each token a slot for every expert its
+// score bounds leave possible (usually exactly its top-4, sometimes 5 or 6),
+// at most kSpecSlots; a batch with a token past that waits for its logits.
+constexpr int kSpecSlots = 8;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset
@@ -60,9 +64,9 @@ struct Ctrl {
   int stream_rows;  // streaming plan: weight rows per task (16, 32 or 64)
   int max_count;    // tokens of the largest expert
   int slots_assigned;  // MFMA plans: the router wrote every slot (pos = slot, slot_token)
-  // 0: the router routed and planned; 2: it wrote score bounds (sbound), and
-  // the streaming kernel computes the logits (chain jobs) and routes from the
-  // bounds where they settle every token's top-4
+  // 0: the router routed and planned; 2: it wrote score bounds (sbound), the
+  // streaming kernel plans a slot for every expert they leave possible, and
+  // computes the logits (chain jobs) and each token's exact top-4
   int deferred;
   int chain_lazy;   // test hook: blocks leave the chain jobs to the waits that need them
   int tail_units;   // last units whose down tiles run as two half-width tiles
@@ -95,11 +99,12 @@ struct Scratch {
   int *pos;              // [Tmax][4]: local rank, then slot
   int *blk;              // [Tmax/8][E]: block counts, then block bases
   int *tb_done;          // [Tmax/8]: expert-split blocks finished per token block
-  int *slot_token;       // [4 Tmax]
-  float *inter;          // [4 Tmax][I]
-  float *sout;           // [4 Tmax][H]
+  int *slot_token;       // [slot_cap]: token of each slot
+  float *inter;          // [slot_cap][I]
+  float *sout;           // [slot_cap][H]
   uint32_t inter_bytes;  // allocation sizes (< 4 GiB: 32-bit buffer offsets)
   uint32_t sout_bytes;
+  int slot_cap;          // slot rows of slot_token, inter and sout
   Ctrl *ctrl;
   int *dep;              // [max_units]
   int *ccount;           // [Tmax][H/64]: expert outputs landed per (token, column tile)

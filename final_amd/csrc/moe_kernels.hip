@@ -19,10 +19,11 @@
 //      expert_ring_kernel, weight streaming through MFMA 16x16x4 f32 with
 //      round-robin tasks and slots assigned by the router -- or, for a fused
 //      forward of at most 8 tokens, planned by each of its own blocks from
-//      bounds of the scores that the router writes instead of the logits
-//      (they settle every token's top-4 set unless two scores nearly tie at
-//      the 4th place), while 8 of its blocks compute the logits as chain
-//      jobs for the weights, the rank order and the published routing.
+//      bounds of the scores that the router writes instead of the logits (a
+//      slot for every expert the bounds leave possible: a token's exact
+//      top-4, and one or two more when two scores nearly tie at the 4th
+//      place), while 8 of its blocks compute the logits as chain jobs for
+//      the weights, the rank order and the published routing.
 //
 // Phase dependencies are counters in the control block.  A task only waits
 // on tasks with a smaller index and every block runs its tasks in increasing
@@ -47,15 +48,17 @@ constexpr uint32_t kUnwritten = 0x7FBADA55u;
 // idx / pos of a token whose routing the streaming kernel has not published yet
 constexpr int kRouteUnset = -2;
 
-// Fill rows [0, 4T) of the intermediate and expert-output buffers with
-// kUnwritten, shared by nthr threads in each of nblk blocks (this thread:
-// thread thr of block blk).  The kernel boundary orders these stores before
-// every store and load of the expert kernel.
+// Fill the slot rows of the intermediate and expert-output buffers (4T, or
+// kSpecSlots * T for a deferred routing) with kUnwritten, shared by nthr
+// threads in each of nblk blocks (this thread: thread thr of block blk).  The
+// kernel boundary orders these stores before every store and load of the
+// expert kernel.
 __device__ void fill_unwritten(const RouterArgs &a, int blk, int nblk, int thr, int nthr) {
   if (a.tile_rows != 0) return;
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   const f32x4 v = __builtin_bit_cast(f32x4, u32x4{kUnwritten, kUnwritten, kUnwritten, kUnwritten});
-  const size_t rows = (size_t)a.T * kTopK;
+  // a deferred routing plans up to kSpecSlots slots per token
+  const size_t rows = (size_t)a.T * (a.defer == 2 ? kSpecSlots : kTopK);
   const size_t ni = rows * (size_t)a.inter / 4, ns = rows * (size_t)a.H / 4;
   const size_t stride = (size_t)nblk * nthr;
   for (size_t i = (size_t)blk * nthr + thr; i < ni + ns; i += stride) {
@@ -1135,7 +1138,7 @@ __device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int col0,
 #pragma unroll
     for (int k = 0; k < kTopK; ++k) {
       const int slot = a.s.pos[(size_t)t * kTopK + k];
-      ok[k] = slot >= 0 && slot < a.T * kTopK;
+      ok[k] = slot >= 0 && slot < a.s.slot_cap;
       w[k] = a.s.wts[(size_t)t * kTopK + k];
       v[k] = so[(size_t)(ok[k] ? slot : 0) * H4 + c4];
     }
@@ -1435,10 +1438,10 @@ struct RingShared {
   int abort;
   int seq[8];              // the block's j-th row task id at seq[j & 7]
   int nseq;                // row task ids published so far
-  int local;               // 1: routing computed by this block; 2: set settled by the score bounds
+  int local;               // 1: routing computed by this block; 2: planned from the score bounds
   int rpos[kDecRT][kTopK]; // local routing: slot of each (token, rank), -1: none
   float rw[kDecRT][kTopK]; // local routing: weights
-  int slotmap[kDecRT][kExperts];  // settled set: slot of each (token, expert), -1: not chosen
+  int slotmap[kDecRT][kExperts];  // plan from the bounds: slot of each (token, expert), -1: none
   float bias[kExperts];    // score bias (deferred routing)
 };
 
@@ -1739,8 +1742,9 @@ __device__ __forceinline__ RingRoute ring_route(const ExpertArgs &a, const RingS
 // the block's partial buffers (free until it streams) with direct-to-LDS
 // loads and wave 0 runs one chain per (token, expert) lane.  The block that
 // completes the last job routes every token from the logits at once
-// (route_token_block) and publishes idx, w and pos, so the combine finds
-// them; rsh and sh.offsets serve as scratch (sh.bias must be loaded).
+// (route_token_block) and publishes idx and w, so the combine finds them
+// (each block maps an expert to its slot with its own plan); rsh serves as
+// scratch (sh.bias must be loaded).
 __device__ __forceinline__ void ring_chain_job(const ExpertArgs &a, RingShared &sh,
                                                RouteShared &rsh, int *s_flag, int j,
                                                float *lds) {
@@ -1773,17 +1777,10 @@ __device__ __forceinline__ void ring_chain_job(const ExpertArgs &a, RingShared &
                         ? __hip_atomic_load(&a.s.logits[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                         : 0.0f;
     route_token_block(rsh, T, sh.bias, l);
-    if (tid < kExperts) {
-      int total = 0;
-      sh.offsets[tid] = lane_scan32(rsh.cnt[tid], tid, &total);
-    }
-    __syncthreads();
     if (tid < T * kTopK) {
       const int t = tid / kTopK, k = tid % kTopK;
-      const int ex = rsh.ti[t][k];
-      st_agent(&a.s.idx[tid], ex);
+      st_agent(&a.s.idx[tid], rsh.ti[t][k]);
       st_agent(&a.s.wts[tid], rsh.tw[t][k]);
-      st_agent(&a.s.pos[tid], ex >= 0 ? sh.offsets[ex] + rsh.rank[t][k] : -1);
     }
     __syncthreads();
   }
@@ -1806,10 +1803,11 @@ __device__ __forceinline__ void ring_chain_job_wave(const ExpertArgs &a, int j) 
 // the calling wave waits for every chain job (running unclaimed ones
 // itself), then computes the token's top-4 in rank order and weights with
 // route_token_block's arithmetic (lane e: expert e; lanes 32-63 repeat
-// lanes 0-31).  The slots come from the set the score bounds settled, which
-// the exact top-4 must equal (else the status word reads 2 and the block
-// aborts).  Wave 0 publishes the token's idx, weights and slots.  False if
-// the block aborts or the wait times out.
+// lanes 0-31).  The slots come from the block's plan of the experts the
+// score bounds left possible, which must hold every expert of the exact
+// top-4 (else the status word reads 2 and the block aborts).  Wave 0
+// publishes the token's idx and weights.  False if the block aborts or the
+// wait times out.
 __device__ __forceinline__ bool ring_route_exact(const ExpertArgs &a, RingShared &sh, int tok,
                                                  RingRoute *out, int *abort_flag, int *err,
                                                  long long ticks) {
@@ -1867,7 +1865,7 @@ __device__ __forceinline__ bool ring_route_exact(const ExpertArgs &a, RingShared
   for (int k = 0; k < kTopK; ++k) {
     out->w[k] = pk[k] * scale * 1.0f;
     out->slot[k] = ek[k] >= 0 ? sh.slotmap[tok][ek[k]] : -1;
-    same = same && out->slot[k] >= 0;  // the settled set has four experts
+    same = same && (ek[k] < 0 || out->slot[k] >= 0);  // every expert has a planned slot
   }
   if (!same) {
     if (lane == 0) {
@@ -1877,27 +1875,25 @@ __device__ __forceinline__ bool ring_route_exact(const ExpertArgs &a, RingShared
     return false;
   }
   if (w == 0 && lane < kTopK) {
-    int ev = ek[0], sv = out->slot[0];
+    int ev = ek[0];
     float wv = out->w[0];
 #pragma unroll
     for (int k = 1; k < kTopK; ++k)
       if (lane == k) {
         ev = ek[k];
-        sv = out->slot[k];
         wv = out->w[k];
       }
     st_agent(&a.s.idx[(size_t)tok * kTopK + lane], ev);
     a.s.wts[(size_t)tok * kTopK + lane] = wv;
-    st_agent(&a.s.pos[(size_t)tok * kTopK + lane], sv);
   }
   return true;
 }
 
 // The token's routing as the block that finished the chain jobs published
-// it (coherent loads; one round trip), checked against the set the bounds
-// settled (else the status word reads 2 and the block aborts); if it is not
-// there yet, ring_route_exact.
-__device__ __forceinline__ bool ring_route_settled(const ExpertArgs &a, RingShared &sh, int tok,
+// it (coherent loads; one round trip), each expert's slot from this block's
+// plan, which must hold it (else the status word reads 2 and the block
+// aborts); if it is not there yet, ring_route_exact.
+__device__ __forceinline__ bool ring_route_planned(const ExpertArgs &a, RingShared &sh, int tok,
                                                    RingRoute *out, int *abort_flag, int *err,
                                                    long long ticks) {
   int ex[kTopK], sl[kTopK];
@@ -1906,16 +1902,14 @@ __device__ __forceinline__ bool ring_route_settled(const ExpertArgs &a, RingShar
   for (int k = 0; k < kTopK; ++k) {
     const size_t i = (size_t)tok * kTopK + k;
     ex[k] = __hip_atomic_load(&a.s.idx[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sl[k] = __hip_atomic_load(&a.s.pos[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     wv[k] = __hip_atomic_load(&a.s.wts[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   bool there = true, same = true;
 #pragma unroll
   for (int k = 0; k < kTopK; ++k) {
-    there = there && ex[k] != kRouteUnset && sl[k] != kRouteUnset &&
-            __builtin_bit_cast(uint32_t, wv[k]) != kUnwritten;
-    same = same && ex[k] >= 0 && ex[k] < kExperts && sl[k] >= 0 &&
-           sh.slotmap[tok][ex[k] & (kExperts - 1)] == sl[k];
+    there = there && ex[k] != kRouteUnset && __builtin_bit_cast(uint32_t, wv[k]) != kUnwritten;
+    sl[k] = ex[k] >= 0 && ex[k] < kExperts ? sh.slotmap[tok][ex[k]] : -1;
+    same = same && ex[k] < kExperts && (ex[k] < 0 || sl[k] >= 0);
   }
   if (!__builtin_amdgcn_readfirstlane((int)there))
     return ring_route_exact(a, sh, tok, out, abort_flag, err, ticks);
@@ -2141,7 +2135,7 @@ __device__ void ring_streamer(const ExpertArgs &a, RingShared &sh, float *res, c
   // registers free
   for (int tok = blockIdx.x; ok && tok < pl.ncomb; tok += pl.grid) {
     RingRoute r;
-    if (sh.local == 2) ok = ring_route_settled(a, sh, tok, &r, &sh.abort, err, ticks);
+    if (sh.local == 2) ok = ring_route_planned(a, sh, tok, &r, &sh.abort, err, ticks);
     else r = ring_route(a, sh, tok);
     if (ok) ok = ring_combine(a, tok, r, (int)threadIdx.x, &sh.abort, err, ticks);
   }
@@ -2353,15 +2347,19 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
     const int tl = (tid >> 5) & (kDecRT - 1), e = tid & (kExperts - 1);
     const bool pair = tid < kDecRT * kExperts;
-    bool settled = false, chosen = false;
+    bool planned = false, chosen = false;
     float l = 0.0f;
     {
-      // The bounds settle a token when four of its experts each have fewer
-      // than four others whose upper bound reaches their lower bound: those
-      // four are then its exact top-4 whatever the logits' rounding, and the
-      // slots, which depend on the sets only, follow.  The logits (chain
-      // jobs) are needed only by the combine, for the weights and rank
-      // order.
+      // Expert e stays possible for a token unless four experts' lower
+      // bounds exceed e's upper bound: then four experts beat e strictly,
+      // whatever the logits' rounding, and the strict-'>' insertion of
+      // layer.cu:465-476 cannot keep it.  So the possible set holds the
+      // token's exact top-4; it is usually exactly the top-4, sometimes one
+      // or two experts more (a 4th/5th score gap inside the bounds).  Every
+      // possible expert gets a slot, and the combine, which needs the logits
+      // (chain jobs) for the weights and the rank order anyway, uses the
+      // exact top-4's.  The slots depend on the sets only, so the block
+      // streams at once.
       float lo = 0.0f, hi = 0.0f;
       if (pair && tl < a.T) {
         lo = c->sbound[0][tl][e];
@@ -2371,31 +2369,29 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
       __syncthreads();
       claim_late = s_job < kChainJobs;
       if (claim_late) ring_chain_job(a, sh, rsh, &s_fin, s_job, res);
-      if (pair) rsh.prob[tl][e] = hi;
+      if (pair) rsh.prob[tl][e] = lo;
       __syncthreads();
-      bool fin = true;
       if (pair && tl < a.T) {
-        fin = __builtin_isfinite(lo) && __builtin_isfinite(hi) && lo > -1e30f;
-        int above = 0;
+        int beat = 0;
 #pragma unroll
         for (int j0 = 0; j0 < kExperts; j0 += 8) {
-          float hv[8];
+          float lv[8];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) hv[j] = rsh.prob[tl][j0 + j];
+          for (int j = 0; j < 8; ++j) lv[j] = rsh.prob[tl][j0 + j];
 #pragma unroll
-          for (int j = 0; j < 8; ++j) above += (int)((j0 + j != e) & (hv[j] >= lo));
+          for (int j = 0; j < 8; ++j) beat += (int)(lv[j] > hi);
         }
-        chosen = fin && above < kTopK;
+        chosen = beat < kTopK;
       }
       const int half = (tid & 63) >> 5;
       const uint32_t gin = (uint32_t)(__ballot(chosen) >> (32 * half));
-      const uint32_t gfin = (uint32_t)(__ballot(fin) >> (32 * half));
-      const bool tok_ok = !pair || tl >= a.T || (__popc(gin) == kTopK && gfin == 0xffffffffu);
-      settled = __syncthreads_and(tok_ok) != 0;
-      if (!settled) {
-        // some token's top-4 is open: run the chain jobs nobody has claimed,
-        // wait for the others (all claimed by running blocks, and a job
-        // never waits), then route from the logits
+      const bool tok_ok = !pair || tl >= a.T || __popc(gin) <= kSpecSlots;
+      planned = __syncthreads_and(tok_ok) != 0;
+      if (!planned) {
+        // a token with more than kSpecSlots possible experts (non-finite
+        // inputs or bias): run the chain jobs nobody has claimed, wait for
+        // the others (all claimed by running blocks, and a job never
+        // waits), then route from the logits
         for (;;) {
           // a read first: most blocks find every job claimed and take no
           // atomic on the counter
@@ -2428,9 +2424,9 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
           l = __hip_atomic_load(&a.s.logits[tid], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    if (settled) {
-      // per-expert counts and each chosen pair's rank among the block's
-      // tokens, from the settled sets
+    if (planned) {
+      // per-expert counts and each possible pair's rank among the block's
+      // tokens
       if (pair) rsh.sel[tl][e] = chosen ? 1 : 0;
       __syncthreads();
       int before = 0;

@@ -125,6 +125,13 @@ class SparseMoeBlock:
                       "moe_route")
         self._routed_T = int(num_tokens)
 
+    def route_forward(self, x, num_tokens: int, stream=None) -> None:
+        """forward_gpu's routing launch (timing): follow with experts() on the
+        same stream, x and num_tokens; together they are forward_gpu."""
+        _native.check(_native.lib().moe_route_forward(self._ctx, _ptr(x), int(num_tokens),
+                                                      _stream(stream)), "moe_route_forward")
+        self._routed_T = int(num_tokens)
+
     def route_logits(self, logits, num_tokens: int, stream=None) -> None:
         _native.check(_native.lib().moe_route_logits(self._ctx, _ptr(logits), int(num_tokens),
                                                      _stream(stream)), "moe_route_logits")
@@ -157,6 +164,14 @@ class SparseMoeBlock:
             self._ctx, idx.ctypes.data, w.ctypes.data, counts.ctypes.data, logits.ctypes.data,
             T, _stream(stream)), "moe_last_routing")
         return {"idx": idx, "w": w, "counts": counts, "logits": logits}
+
+    def last_plan_counts(self, stream=None):
+        """Slots per expert of the last plan (the routing's counts, plus the
+        speculative slots of a deferred decode routing)."""
+        c = np.empty((self.num_experts,), np.int32)
+        _native.check(_native.lib().moe_last_plan_counts(self._ctx, c.ctypes.data, _stream(stream)),
+                      "moe_last_plan_counts")
+        return c
 
     def check_device(self, stream=None) -> None:
         _native.check(_native.lib().moe_device_status(self._ctx, _stream(stream)), "device status")

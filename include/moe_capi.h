@@ -115,6 +115,13 @@ int moe_route(moe_ctx *ctx, const float *x, int num_tokens, moe_stream_t stream)
 int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
                 int num_tokens, moe_stream_t stream);
 
+/* Timing hook: moe_forward's own routing launch, which for decode batches
+ * leaves the gate logits (and, for the MFMA plans up to 256 tokens, the exact
+ * routing) to the experts launch that follows.  It must be followed by
+ * moe_experts on the same stream with the same x and num_tokens and a y that
+ * is not x; together they run exactly moe_forward's two kernels. */
+int moe_route_forward(moe_ctx *ctx, const float *x, int num_tokens, moe_stream_t stream);
+
 /* Routing from caller-supplied logits [num_tokens][E] (device): the sigmoid,
  * bias, top-4 and histogram of moe_router_topk_kernel (layer.cu:439-499)
  * without the gate GEMM.  Used by SparseMoeBlock::route_tokens (layer.h:91-93)
@@ -200,6 +207,14 @@ int moe_last_routing(moe_ctx *ctx, int *idx, float *w, int *counts,
  * MOE_ERR_INTERNAL if a kernel met an out-of-range slot (and skipped it), else
  * MOE_OK.  Synchronises `stream`. */
 int moe_device_status(moe_ctx *ctx, moe_stream_t stream);
+
+/* Diagnostics: the slots per expert of the last expert-kernel plan (counts,
+ * [E] host ints).  They equal the routing's counts, except after a deferred
+ * decode routing (moe_forward of up to 8 tokens under the weight-streaming
+ * plan), which gives a token a slot for every expert its score bounds leave
+ * possible: a 5th or 6th one when two scores nearly tie at the 4th place.
+ * Synchronises `stream`. */
+int moe_last_plan_counts(moe_ctx *ctx, int *counts, moe_stream_t stream);
 
 /* Which expert kernel moe_forward picks for num_tokens: 0 = weight-streaming
  * (small T), 32/64/128 = MFMA grouped GEMM with that many rows per tile. */

@@ -387,9 +387,10 @@ def _check_same(y1, rt1, y2, rt2):
 def test_forward_routes_in_expert_kernel(T, lazy, block, real_weights, oracle_mod):
     """One decode token block under the streaming plan: moe_forward's router
     writes only bounds of each score (double sums of the gate products and a
-    bound of the FMA chain's rounding), the expert kernel takes each token's
-    top-4 set from them, streams, computes the logits in chain jobs meanwhile
-    and ranks and weights each token from its logits in the combine.  Its
+    bound of the FMA chain's rounding), the expert kernel plans a slot for
+    every expert they leave possible for a token, streams, computes the
+    logits in chain jobs meanwhile and ranks and weights each token from its
+    logits in the combine.  Its
     routing (idx, w, counts, logits) and y must be bit-identical to moe_route
     + moe_experts, where the router computes the logits and routes, and
     match the oracle.  A hot expert (bias +10) makes several tokens share an
@@ -420,10 +421,12 @@ def test_forward_routes_in_expert_kernel(T, lazy, block, real_weights, oracle_mo
 def test_forward_routing_random_batches(block, real_weights, oracle_mod):
     """48 random decode batches of 1-8 tokens through moe_forward's routing
     from score bounds: with these weights about 4 % of random tokens have a
-    4th/5th score gap inside the bounds, so the batches mix the settled path
-    and the fallback (10 of these 48 fall back, by the bound restated on the
-    CPU).  Each must give the routing (idx, w, counts, logits)
-    and y of moe_route + moe_experts bit for bit, and the oracle's routing."""
+    4th/5th score gap inside the bounds and get a slot for a 5th (or 6th)
+    possible expert, so 10 of these 48 batches plan more slots than their
+    top-4 (by the bound restated on the CPU).  Each must give the routing
+    (idx, w, counts, logits) and y of moe_route + moe_experts bit for bit
+    (a row's arithmetic does not depend on its slot), and the oracle's
+    routing."""
     from final_amd import workloads as W
     w = real_weights
     rng = np.random.default_rng(2024)
@@ -439,14 +442,14 @@ def test_forward_routing_random_batches(block, real_weights, oracle_mod):
 @pytest.mark.gpu
 @pytest.mark.parametrize("lazy", [False, True])
 @pytest.mark.parametrize("T", [1, 8])
-def test_forward_routing_tie_waits_for_logits(T, lazy, block, real_weights, oracle_mod):
-    """A score tie at the top-4 boundary, which no bound can settle: token 0's
-    fifth expert gets the gate row and bias of its fourth, so their logits
-    and scores are equal and each has four experts whose upper bound reaches
-    its lower bound.  The expert kernel must then wait for the chain jobs
-    (running any that are unclaimed, all of them when lazy) and route every
-    token from the logits, with the reference's tie rule (the lower index
-    wins), bit-identical to moe_route + moe_experts and to the oracle."""
+def test_forward_routing_tie_plans_both(T, lazy, block, real_weights, oracle_mod):
+    """A score tie at the top-4 boundary, which no bound can separate: token
+    0's fifth expert gets the gate row and bias of its fourth, so their
+    logits and scores are equal.  The expert kernel plans slots for both,
+    and the combine keeps the lower index once the chain jobs (run by the
+    waits when lazy) give the logits: the reference's tie rule (strict '>'
+    insertion), bit-identical to moe_route + moe_experts and to the
+    oracle."""
     from final_amd import workloads as W
     x = W.gen_x(T, seed=90 + T)
     r = W.gen_x(T, seed=95 + T)
@@ -471,6 +474,86 @@ def test_forward_routing_tie_waits_for_logits(T, lazy, block, real_weights, orac
     lg = rt1["logits"]
     assert lg[0, e4] == lg[0, e5]
     assert min(e4, e5) in rt1["idx"][0].tolist() and max(e4, e5) not in rt1["idx"][0].tolist()
+    ref = oracle_forward(oracle_mod, w, x, residual=r)
+    check_routing(rt1, ref)
+    np.testing.assert_allclose(y1, ref["y"], rtol=RTOL, atol=ATOL)
+
+
+def _ref_scores(O, w, x):
+    """The reference's scores sigmoid(logit) + bias in float32 (layer.cu:434,
+    462) from the oracle's bit-exact logits."""
+    lg = O.gate_logits(x, w["gate"]).astype(np.float64)
+    e = np.exp(-lg).astype(np.float32)
+    p = (np.float32(1.0) / (np.float32(1.0) + e)).astype(np.float32)
+    return (p + np.asarray(w["bias"], np.float32)).astype(np.float32)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T", [49, 64, 100, 129, 200, 256])
+def test_forward_random_batches_mfma(T, block, real_weights, oracle_mod):
+    """Random N(0, 1) batches under the 64-row MFMA plan, routed by several
+    token blocks of the decode router: routing (idx, w, counts, logits) and y
+    of moe_forward bit-identical to moe_route + moe_experts, and matching the
+    oracle."""
+    from final_amd import workloads as W
+    w = real_weights
+    assert block.plan(T) == 64
+    rng = np.random.default_rng(700 + T)
+    x = rng.standard_normal((T, W.H)).astype(np.float32)
+    r = rng.standard_normal((T, W.H)).astype(np.float32)
+    y1, rt1, y2, rt2 = _forward_vs_route_experts(block, w, T, x, r, "random batch mfma")
+    _check_same(y1, rt1, y2, rt2)
+    ref = oracle_forward(oracle_mod, w, x, residual=r)
+    check_routing(rt1, ref)
+    np.testing.assert_allclose(y1, ref["y"], rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("T,plan", [(64, -1), (256, -1), (16, 64), (5, 128), (40, 32)])
+def test_forward_routing_ties_many_blocks(T, plan, block, real_weights, oracle_mod):
+    """Exact 4th-place ties in several token blocks: expert b gets the gate
+    row and bias of expert a, the pair chosen on the oracle's scores so that
+    a and b share the 4th place for as many tokens as possible.  Each tied
+    token keeps the lower index (the strict '>' insertion of
+    layer.cu:465-476), under the 64-row plan of the decode router's several
+    token blocks and under forced MFMA plans at small T."""
+    from final_amd import workloads as W
+    rng = np.random.default_rng(800 + T)
+    x = rng.standard_normal((T, W.H)).astype(np.float32)
+    r = rng.standard_normal((T, W.H)).astype(np.float32)
+    w = dict(real_weights)
+    sc = _ref_scores(oracle_mod, w, x)
+    best = None
+    for a in range(32):
+        for b in range(32):
+            if a == b:
+                continue
+            others = np.ones(32, bool)
+            others[[a, b]] = False
+            above = (sc[:, others] > sc[:, a:a + 1]).sum(1)
+            n = int((above == 3).sum())
+            if best is None or n > best[0]:
+                best = (n, a, b)
+    n, a, b = best
+    gate = np.array(w["gate"], np.float32).copy()
+    bias = np.array(w["bias"], np.float32).copy()
+    gate[b] = gate[a]
+    bias[b] = bias[a]
+    w["gate"], w["bias"] = gate, bias
+    sc2 = _ref_scores(oracle_mod, w, x)
+    tied = [t for t in range(T) if (sc2[t] > sc2[t, a]).sum() == 3]
+    say(f"[ties] T={T} plan={plan} pair=({a},{b}) tied tokens={tied}")
+    assert len(tied) >= 1 and (T < 64 or len({t // 8 for t in tied}) >= 2)
+    block.force_tile_rows(plan)
+    try:
+        y1, rt1, y2, rt2 = _forward_vs_route_experts(block, w, T, x, r, "ties")
+    finally:
+        block.force_tile_rows(-1)
+        rw = real_weights
+        block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
+    _check_same(y1, rt1, y2, rt2)
+    for t in tied:
+        assert min(a, b) in rt1["idx"][t].tolist() and max(a, b) not in rt1["idx"][t].tolist()
     ref = oracle_forward(oracle_mod, w, x, residual=r)
     check_routing(rt1, ref)
     np.testing.assert_allclose(y1, ref["y"], rtol=RTOL, atol=ATOL)

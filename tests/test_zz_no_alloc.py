@@ -1,10 +1,12 @@
 """moe_forward_noalloc (the entry point that allocates nothing) against
 moe_forward through the C-ABI.
 
-Same kernels and plan on a per-GPU device array instead of the context's
-scratch, so y must equal moe_forward's bit for bit.  Two calls in a row, the
-second with fewer tokens (the array keeps the first call's contents), and the
-size limit.
+moe_forward_noalloc runs the router and expert kernels of moe_route +
+moe_experts on a per-GPU device array instead of the context's scratch, so
+its y must equal theirs bit for bit, and moe_forward's too (which routes a
+decode batch of up to 8 tokens from score bounds inside the experts launch,
+with the same arithmetic per row).  Two calls in a row, the second with fewer
+tokens (the array keeps the first call's contents), and the size limit.
 """
 import sys
 
@@ -35,15 +37,24 @@ def test_noalloc_matches_forward(real_weights):
             dx = hip.DeviceArray.from_numpy(x)
             dr = hip.DeviceArray.from_numpy(r)
             dy = hip.DeviceArray((T, W.H))
+            dv = hip.DeviceArray((T, W.H))
             dz = hip.DeviceArray((T, W.H))
             blk.forward_gpu(dx, dy, T, residual=dr)
+            hip.synchronize()
+            rt_fwd = blk.last_routing()
+            blk.route(dx, T)
+            blk.experts(dx, dv, T, residual=dr)
             _native.check(L.moe_forward_noalloc(blk._ctx, dx.ptr, dz.ptr, dr.ptr, T, None),
                           "moe_forward_noalloc")
             hip.synchronize()
             blk.check_device()
-            y, z = dy.download(), dz.download()
+            y, v, z = dy.download(), dv.download(), dz.download()
             assert np.isfinite(z).all()
+            assert np.array_equal(bits(z), bits(v)), f"T={T}: noalloc y differs from route + experts"
             assert np.array_equal(bits(z), bits(y)), f"T={T}: noalloc y differs from moe_forward"
+            rt = blk.last_routing()  # moe_route's, the same as moe_forward's
+            assert np.array_equal(rt["idx"], rt_fwd["idx"])
+            assert np.array_equal(bits(rt["w"]), bits(rt_fwd["w"]))
         # a forced MFMA plan on the same array, after the streaming calls
         blk.force_tile_rows(64)
         try:
@@ -52,12 +63,16 @@ def test_noalloc_matches_forward(real_weights):
             x = W.gen_x(T, seed=500)
             dx = hip.DeviceArray.from_numpy(x)
             dy = hip.DeviceArray((T, W.H))
+            dv = hip.DeviceArray((T, W.H))
             dz = hip.DeviceArray((T, W.H))
             blk.forward_gpu(dx, dy, T)
+            blk.route(dx, T)
+            blk.experts(dx, dv, T)
             _native.check(L.moe_forward_noalloc(blk._ctx, dx.ptr, dz.ptr, None, T, None),
                           "moe_forward_noalloc")
             hip.synchronize()
             blk.check_device()
+            assert np.array_equal(bits(dz.download()), bits(dv.download()))
             assert np.array_equal(bits(dz.download()), bits(dy.download()))
         finally:
             blk.force_tile_rows(-1)
