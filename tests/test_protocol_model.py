@@ -30,6 +30,32 @@ before finishing its current one (the shape of a removed ring-kernel variant
 that parked down tasks until their expert's values had landed and ended in a
 device-side wait timeout: its block could hold the gate/up task that its own
 next down task needed).
+
+The ring kernel's routing of a decode batch from score bounds (Ctrl::deferred
+2) adds the gate-logit chain jobs and their waits, modelled by
+explore_chain:
+
+* J jobs on a counter of their own (chain_head).  As it starts, each of the
+  first C blocks claims one (none in lazy mode) and runs it in block form,
+  and claims its first row task only after it; every other block claims its
+  first row task at once.  A job never waits; it counts itself in
+  chain_done when it is stored.
+* Prologue (every block plans from the bounds): when a token has more
+  possible experts than the plan holds (the fallback), the block claims and
+  runs in block form every job still unclaimed, then waits until all J are
+  done, holding the row task it may have claimed; otherwise it goes on at
+  once.
+* After its row tasks, a block's combine of a token (planned path) first
+  needs the exact routing: all J jobs done, and while any job is
+  unclaimed the waiting wave claims and runs it (wave form,
+  ring_route_exact); then the token's expert outputs (its down tasks).  The
+  fallback's combine routes from the logits it already has.
+
+Both modes, lazy or not, are shown free of stuck states under partial
+residency; the model reaches one when the waits do not run unclaimed jobs
+(lazy mode: no block ever would), and when a job waits for another (the
+block that holds job 0 waits for job 1, which only a block that is not
+resident could claim).
 """
 from __future__ import annotations
 
@@ -195,3 +221,139 @@ def test_parking_on_the_next_task_sticks():
     r = explore(ring_plan(experts=1, p1=1, p2=1, tokens=()), "ring", 1, 1, park=True)
     assert r is not None and "stuck" in r
     assert explore(ring_plan(experts=1, p1=1, p2=1, tokens=()), "ring", 1, 1) is None
+
+
+# Chain-job protocol of the deferred decode routing (explore_chain).
+# block: (status, phase, cur, nxt, flags, comb_i, job)
+#   phase 1 block-form job at start (first row task claimed after it), 2
+#   prologue, 6 block-form job in the fallback's prologue, 3 row tasks, 4
+#   combines, 5 wave-form job in a combine's routing wait
+def explore_chain(plan: Plan, G: int, R: int, J: int, claim_blocks: int, lazy=False,
+                  fallback=False, waits_run_jobs=True, job_waits_next=False):
+    n = plan.n_row
+    ncomb = len(plan.combine_deps)
+    all_jobs = (1 << J) - 1
+    seen = set()
+
+    def deps_done(done, deps):
+        return all((done >> d) & 1 for d in deps)
+
+    def job_can_finish(jdone, j):
+        return not job_waits_next or j + 1 >= J or (jdone >> (j + 1)) & 1
+
+    def repl(blocks, i, b):
+        nb = list(blocks)
+        nb[i] = b
+        return tuple(nb)
+
+    def moves(state):
+        head, done, chead, jdone, blocks = state
+        running = sum(1 for b in blocks if b[0] == RUNNING)
+        out = []
+        for i, (st, ph, cur, nxt, fl, ci, job) in enumerate(blocks):
+            if st == PENDING:
+                if running < R and all(b[0] != PENDING for b in blocks[:i]):
+                    if not lazy and i < claim_blocks and chead < J:
+                        out.append((head, done, chead + 1, jdone,
+                                    repl(blocks, i, (RUNNING, 1, -1, -1, 0, 0, chead))))
+                    else:
+                        t, h = (head, head + 1) if head < n else (n, head)
+                        out.append((h, done, chead, jdone,
+                                    repl(blocks, i, (RUNNING, 2, t, -1, 0, 0, -1))))
+                continue
+            if st != RUNNING:
+                continue
+            if ph in (1, 6, 5):  # a job in progress: it never waits (unless the variant)
+                if job_can_finish(jdone, job):
+                    nph = 2 if ph in (1, 6) else 4
+                    out.append((head, done, chead, jdone | (1 << job),
+                                repl(blocks, i, (st, nph, cur, nxt, fl, ci, -1))))
+                continue
+            if ph == 2:  # prologue
+                if fallback and chead < J:
+                    out.append((head, done, chead + 1, jdone,
+                                repl(blocks, i, (st, 6, cur, nxt, fl, ci, chead))))
+                elif not fallback or jdone == all_jobs:
+                    t, h = cur, head
+                    if t < 0:  # claimed late, after a job
+                        t, h = (head, head + 1) if head < n else (n, head)
+                    out.append((h, done, chead, jdone, repl(blocks, i, (st, 3, t, -1, 0, ci, -1))))
+                continue
+            if ph == 3:  # row tasks (ring kernel: the next claim before or after the wait)
+                if cur < n:
+                    awaited, claimed = fl & 1, fl & 2
+                    if not awaited and deps_done(done, plan.deps[cur]):
+                        out.append((head, done, chead, jdone,
+                                    repl(blocks, i, (st, ph, cur, nxt, fl | 1, ci, job))))
+                    if not claimed:
+                        t, h = (head, head + 1) if head < n else (n, head)
+                        out.append((h, done, chead, jdone,
+                                    repl(blocks, i, (st, ph, cur, t, fl | 2, ci, job))))
+                    if awaited and claimed:
+                        out.append((head, done | (1 << cur), chead, jdone,
+                                    repl(blocks, i, (st, ph, nxt, -1, 0, ci, job))))
+                else:
+                    out.append((head, done, chead, jdone, repl(blocks, i, (st, 4, cur, nxt, 0, ci, job))))
+                continue
+            if ph == 4:  # combines: routing first (planned path), then the outputs
+                tok = i + ci * G
+                if tok >= ncomb:
+                    out.append((head, done, chead, jdone, repl(blocks, i, (EXITED, ph, cur, nxt, fl, ci, job))))
+                    continue
+                routed = fallback or jdone == all_jobs
+                if not routed:
+                    if waits_run_jobs and chead < J:
+                        out.append((head, done, chead + 1, jdone,
+                                    repl(blocks, i, (st, 5, cur, nxt, fl, ci, chead))))
+                    continue
+                if deps_done(done, plan.combine_deps[tok]):
+                    out.append((head, done, chead, jdone, repl(blocks, i, (st, ph, cur, nxt, fl, ci + 1, job))))
+        return out
+
+    stack = [(0, 0, 0, 0, tuple((PENDING, 0, -1, -1, 0, 0, -1) for _ in range(G)))]
+    while stack:
+        s = stack.pop()
+        if s in seen:
+            continue
+        seen.add(s)
+        nxt_states = moves(s)
+        if not nxt_states:
+            if not all(b[0] == EXITED for b in s[4]):
+                return f"stuck: jobs done={bin(s[3])} tasks done={bin(s[1])} blocks={s[4]}"
+        stack.extend(nxt_states)
+    return None
+
+
+CHAIN_PLANS = [ring_plan(), ring_plan(experts=1, p1=2, p2=1, tokens=((0,),)),
+               ring_plan(experts=3, p1=1, p2=1, tokens=((0, 2), (1,), (2, 1)))]
+
+
+@pytest.mark.parametrize("G,R", CASES)
+@pytest.mark.parametrize("fallback", [False, True])
+def test_chain_job_protocol_never_sticks(G, R, fallback):
+    for plan in CHAIN_PLANS:
+        for J in (1, 2, 3):
+            for claim_blocks in range(0, G + 1):
+                assert explore_chain(plan, G, R, J, claim_blocks, fallback=fallback) is None
+            assert explore_chain(plan, G, R, J, G, lazy=True, fallback=fallback) is None
+
+
+def test_chain_waits_that_do_not_run_jobs_stick():
+    plan = ring_plan(experts=1, p1=1, p2=1, tokens=((0,),))
+    # with jobs claimed at the start the waits never need to run one ...
+    assert explore_chain(plan, 2, 2, 2, 2, waits_run_jobs=False) is None
+    # ... but when no block claims them (lazy mode, or blocks 0..C-1 not yet
+    # resident when the combines wait) someone must
+    r = explore_chain(plan, 2, 2, 2, 2, lazy=True, waits_run_jobs=False)
+    assert r is not None and "stuck" in r
+    r = explore_chain(plan, 2, 1, 2, 1, waits_run_jobs=False)
+    assert r is not None and "stuck" in r
+
+
+def test_a_job_that_waits_for_another_sticks():
+    plan = ring_plan(experts=1, p1=1, p2=1, tokens=((0,),))
+    # block 0 claims job 0, which waits for job 1; with one block resident
+    # nobody else can claim it
+    r = explore_chain(plan, 2, 1, 2, 2, job_waits_next=True)
+    assert r is not None and "stuck" in r
+    assert explore_chain(plan, 2, 1, 2, 2) is None
