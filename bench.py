@@ -391,6 +391,8 @@ def measure_model(steps, warmup, batch=64, seq=512):
                          "unit": "TFLOP/s", "frac": round(a / PEAK_MFMA_F32_TFLOPS, 4),
                          "scope": "whole forward (every GEMM, attention and the MoE experts)",
                          "per_launch": {"flop": flops}, "traffic": None},
+            "ffn": "the MoE block in all 24 layers, as the benchmark config specifies (the "
+                   "reference's model has dense FFNs in layers 0-1)",
             "data": "synthetic (seeded N(0,0.02) weights on the device, RMSNorm weights 1, "
                     "uniform random token ids)"}
 

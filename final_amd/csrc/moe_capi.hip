@@ -9,6 +9,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <new>
 #include <vector>
@@ -69,6 +70,9 @@ static_assert(kNoAllocTbDone + sizeof(int) * (kNoAllocMaxTokens / kMinRouterToke
 
 std::mutex g_noalloc_mu;
 char *g_noalloc_ptr[kMaxDevices] = {};  // device address of `scratch` per device
+// set by moe_forward_noalloc, cleared by the moe_device_status that reads the
+// array's status word: status checks read it only after a no-alloc call
+std::atomic<bool> g_noalloc_used[kMaxDevices] = {};
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
@@ -654,6 +658,7 @@ int moe_forward_noalloc(moe_ctx *ctx, const float *x, float *y, const float *res
   ea.I = ctx->d.inter;
   ea.wait_limit = kDefaultWaitLimit / (ctx->wait_div > 0 ? ctx->wait_div : 1);
   if (ea.wait_limit < 1) ea.wait_limit = 1;
+  g_noalloc_used[ctx->device].store(true, std::memory_order_relaxed);
   if (launch_experts(ea, ra.tile_rows, ctx->grid[pi], st) != hipSuccess) return MOE_ERR_HIP;
   return MOE_OK;
 }
@@ -893,9 +898,12 @@ int moe_device_status(moe_ctx *ctx, moe_stream_t stream) {
   hipStream_t st = static_cast<hipStream_t>(stream);
   int err = 0, err_na = 0;
   if (take_status(&ctx->s.ctrl->err, st, &err)) return MOE_ERR_HIP;
-  // the status word of the device's moe_forward_noalloc scratch
-  if (char *base = noalloc_ptr(ctx->device))
-    if (take_status(&reinterpret_cast<Ctrl *>(base)->err, st, &err_na)) return MOE_ERR_HIP;
+  // the status word of the device's moe_forward_noalloc scratch, after a
+  // no-alloc call on this device since the last check
+  const int dev = ctx->device;
+  if (dev >= 0 && dev < kMaxDevices && g_noalloc_used[dev].exchange(false))
+    if (char *base = noalloc_ptr(dev))
+      if (take_status(&reinterpret_cast<Ctrl *>(base)->err, st, &err_na)) return MOE_ERR_HIP;
   const int e = err ? err : err_na;
   if (e) return e == 1 ? MOE_ERR_DEVICE_TIMEOUT : MOE_ERR_INTERNAL;
   return MOE_OK;

@@ -92,15 +92,18 @@ int moe_forward(moe_ctx *ctx, const float *x, float *y, const float *residual,
 /* moe_forward without allocating: no counterpart in the reference.  For
  * callers that cannot allocate device memory during a forward (code under HIP
  * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * kernels, plan and results as moe_forward (bit for bit), but the routing,
+ * kernels, plan and results as moe_route + moe_experts (bit for bit, and so
+ * moe_forward's, which may route a decode batch of up to 8 tokens inside the
+ * experts launch with the same arithmetic), but the routing,
  * intermediate and expert-output scratch is one file-scope device array per
  * GPU (8 MiB, set up by moe_create on that GPU) instead of the context's.
  * num_tokens <= 128 (and the rows must fit the array: 128 tokens at hidden
  * 2048 / inter 1792); larger returns MOE_ERR_TOO_MANY_TOKENS.  Calls no
  * hipMalloc/hipFree.  Every call on a GPU shares that GPU's array: calls that
  * overlap on one GPU (two streams, or two contexts) race; calls ordered on
- * one stream do not.  Its device status is reported by moe_device_status of
- * any context on that GPU.  moe_last_routing does not see its routing. */
+ * one stream do not.  Its device status (the array's own status word) is
+ * read and cleared by the first moe_device_status of any context on that GPU
+ * after a no-alloc call there.  moe_last_routing does not see its routing. */
 int moe_forward_noalloc(moe_ctx *ctx, const float *x, float *y, const float *residual,
                         int num_tokens, moe_stream_t stream);
 

@@ -340,7 +340,8 @@ def decoder_layer(h, w, batch, seq, cos, sin, guide=None, eps=0.0):
     q_norm, k_norm | conv, in_proj, out_proj; gate, bias, w1, w3, w2 for a MoE
     FFN with w1/w3 [E][I][H] and w2 [E][H][I], or dense_w1/w3/w2).  guide:
     routing of another implementation to follow on near-ties (MoE only).
-    Returns (h', info) with the routing used and the near-tie counts."""
+    Returns (h', info) with the routing used and the near-tie counts; with a
+    guide also the oracle's own routing (own_idx) and its gate logits."""
     h = _c32(h)
     xn = rmsnorm(h, w["op_norm"])
     if "q" in w:
@@ -363,6 +364,8 @@ def decoder_layer(h, w, batch, seq, cos, sin, guide=None, eps=0.0):
             r = moe_forward(x2, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"], residual=h)
             h, info["idx"], info["adopted"], info["hard"] = r["y"], r["idx"], 0, 0
         else:
+            info["logits"] = gate_logits(x2, w["gate"])
+            info["own_idx"] = route(info["logits"], w["bias"])[0]
             h, info["idx"], info["adopted"], info["hard"] = moe_forward_guided(
                 x2, w["gate"], w["bias"], w["w1"], w["w3"], w["w2"], h, guide, eps)
     else:

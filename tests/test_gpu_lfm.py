@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 
 from conftest import bits
+from test_gpu_lfm_model import near_tie_gaps
 
 RTOL, ATOL = 1e-3, 1e-4
 TIE_EPS = 1e-5
@@ -165,9 +166,12 @@ def _layer_check(model, O, layer, h_in, h_out_gpu, batch, seq, cos, sin):
     guide = model.last_routing(layer, batch * seq) if model.is_moe(layer) else None
     ref, info = O.decoder_layer(h_in, w, batch, seq, cos, sin, guide=guide, eps=TIE_EPS)
     if guide is not None:
-        say(f"[layer {layer}] near-ties followed: {info['adopted']}, not near-ties: {info['hard']}")
+        gaps = near_tie_gaps(info, w["bias"])
+        say(f"[layer {layer}] near-ties followed: {info['adopted']} (gaps {gaps.tolist()}), "
+            f"not near-ties: {info['hard']}")
         assert info["hard"] == 0, "GPU routing differs from the oracle's beyond a near-tie"
-        assert info["adopted"] <= max(2, batch * seq // 200)
+        assert len(gaps) == info["adopted"] and (gaps >= -TIE_EPS).all()
+        assert info["adopted"] <= 2
     np.testing.assert_allclose(h_out_gpu, ref, rtol=RTOL, atol=ATOL)
 
 
