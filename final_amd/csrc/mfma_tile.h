@@ -109,9 +109,11 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 //   kWide: the config's WAVES_M x WAVES_N grid of 32x32 blocks.
 //   kFull: kWide for a tile whose rows are all valid, with no row checks in
 //     its inner loop (straight-line MFMA code).
-//   kNarrow (64-row tiles whose valid rows fit the first 32-row block):
-//     instead of the second block's two waves idling on their SIMDs, each of
-//     the 4 waves takes all rows and one 32-column block.
+//   kNarrow (64-row tiles whose valid rows fit the first 32-row block, and
+//     128-row tiles with 65-96 valid rows): instead of the waves of the
+//     empty row blocks idling on their SIMDs, each of the 4 waves takes one
+//     32-column block and every row block that holds rows (a 128-row tile
+//     with 3 of its 4 row blocks then costs 3/4 of a full one).
 //   kSkinny1 / kSkinny2 / kSkinny3 (64-row tiles with 1-16, 17-32 or 33-48
 //     valid rows, which 32-row blocks pad to twice or 4/3 the rows):
 //     v_mfma_f32_16x16x4_f32 over 1, 2 or 3 16-row blocks, each wave taking
@@ -120,11 +122,12 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 // Same tile, LDS layout and products in every layout.
 enum TileLayout { kWide = 0, kNarrow = 1, kSkinny1 = 2, kSkinny3 = 3, kFull = 4, kSkinny2 = 5 };
 
-// 64x128 tiles: the 2 x 2 grid of 32x64 wave tiles.  (A 128-row tile with
-// at most 64 valid rows runs as a 64-row tile; its caller decides.)
+// 64x128 tiles (the 2 x 2 grid of 32x64 wave tiles) and 128x128 tiles (2 x 2
+// of 64x64): four 32-column blocks, one per wave.  (A 128-row tile with at
+// most 64 valid rows runs as a 64-row tile; its caller decides.)
 template <typename TL>
 constexpr bool tile_narrowable() {
-  return TL::WAVES_M == 2 && TL::WAVES_N == 2 && TL::WM == 1 && TL::WN == 2;
+  return TL::WAVES_M == 2 && TL::WAVES_N == 2 && TL::WN == 2 && TL::BN == 128;
 }
 // 64-row tiles of 4 waves whose columns split into 16-column blocks per wave
 // (64x128 and the half-width 64x64): the 16-row layouts.
@@ -156,14 +159,15 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform branches
 
-  // 32x32 layouts: this wave's row block, first 32-column block, column
-  // blocks, and rows that hold data (0 = skip the MFMAs, <= 32 with WM == 2 =
-  // only the first row block; wave-uniform branches)
+  // 32x32 layouts: this wave's row blocks (AM from wrow0) and column blocks
+  // (AN from cb0), and rows that hold data (0 = skip the MFMAs; a row block
+  // starting at or past wrows is skipped; wave-uniform branches)
+  constexpr int AM = NARROW ? TL::WAVES_M * WM : WM;
+  constexpr int AN = NARROW ? 1 : WN;
   const int wm = NARROW ? 0 : wave % TL::WAVES_M;
   const int cb0 = NARROW ? wave : (wave / TL::WAVES_M) * WN;
-  constexpr int ncb = NARROW ? 1 : WN;
   const int wrow0 = wm * WM * 32;
-  const int wrows = LAYOUT == kFull ? WM * 32 : min(max(rows_valid - wrow0, 0), WM * 32);
+  const int wrows = LAYOUT == kFull ? AM * 32 : min(max(rows_valid - wrow0, 0), AM * 32);
   const int lr = lane & 31, lh = (lane >> 5) * 4;
   const float *a_rd = As + (wrow0 + lr) * PITCH + lh;
   const float *b_rd = Bs + (cb0 * 32 + lr) * PITCH + lh;
@@ -176,7 +180,7 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   const float *a16 = As + l16 * PITCH + k16;
   const float *b16 = Bs + (wave * 16 * SKC + l16) * PITCH + k16;
 
-  floatx16 acc[SKINNY ? 1 : WM][SKINNY ? 1 : WN];
+  floatx16 acc[SKINNY ? 1 : AM][SKINNY ? 1 : AN];
   f32x4 acc16[SRB][SKINNY ? SKC : 1];
   if constexpr (SKINNY) {
 #pragma unroll
@@ -185,9 +189,9 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
       for (int c = 0; c < SKC; ++c) acc16[i][c] = f32x4{0.f, 0.f, 0.f, 0.f};
   } else {
 #pragma unroll
-    for (int i = 0; i < WM; ++i)
+    for (int i = 0; i < AM; ++i)
 #pragma unroll
-      for (int c = 0; c < WN; ++c)
+      for (int c = 0; c < AN; ++c)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][c][r] = 0.0f;
   }
@@ -245,18 +249,17 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
         const float *Bc = b_rd + (u & 1) * BN * PITCH;
 #pragma unroll
         for (int g8 = 0; g8 < BK / 8; ++g8) {
-          f32x4 af[WM], bf[WN];
+          f32x4 af[AM], bf[AN];
 #pragma unroll
-          for (int i = 0; i < WM; ++i) af[i] = ld4(Ac + i * 32 * PITCH + g8 * 8);
+          for (int i = 0; i < AM; ++i)
+            if (i == 0 || wrows > i * 32) af[i] = ld4(Ac + i * 32 * PITCH + g8 * 8);
 #pragma unroll
-          for (int c = 0; c < WN; ++c)
-            if (c < ncb) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
+          for (int c = 0; c < AN; ++c) bf[c] = ld4(Bc + c * 32 * PITCH + g8 * 8);
 #pragma unroll
-          for (int i = 0; i < WM; ++i) {
-            if (i > 0 && wrows <= 32) break;
+          for (int i = 0; i < AM; ++i) {
+            if (i > 0 && wrows <= i * 32) break;
 #pragma unroll
-            for (int c = 0; c < WN; ++c) {
-              if (c >= ncb) break;
+            for (int c = 0; c < AN; ++c) {
 #pragma unroll
               for (int q = 0; q < 4; ++q)
                 acc[i][c] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[i][q], bf[c][q], acc[i][c], 0, 0, 0);
@@ -292,13 +295,12 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
     // 32x32 f32 MFMA result layout: lane l holds column l % 32 and rows
     // 8*(r/4) + 4*(l/32) + r%4 for r = 0..15
 #pragma unroll
-    for (int i = 0; i < WM; ++i) {
+    for (int i = 0; i < AM; ++i) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int row = wrow0 + i * 32 + 8 * (r >> 2) + (lane >> 5) * 4 + (r & 3);
 #pragma unroll
-        for (int c = 0; c < WN; ++c)
-          if (c < ncb) Cs[row * CP + (cb0 + c) * 32 + lr] = acc[i][c][r];
+        for (int c = 0; c < AN; ++c) Cs[row * CP + (cb0 + c) * 32 + lr] = acc[i][c][r];
       }
     }
   }
@@ -359,7 +361,7 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   else if (kSk && rows_valid > 32 && rows_valid <= 48)
     next = tile_slabs<TL, kS3>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
-  else if (kNa && rows_valid <= 32)
+  else if (kNa && (BM == 64 ? rows_valid <= 32 : rows_valid > 64 && rows_valid <= 96))
     next = tile_slabs<TL, kNw>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
   else if (kSk && rows_valid <= 32)
