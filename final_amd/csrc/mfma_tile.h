@@ -110,7 +110,7 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 //   kFull: kWide for a tile whose rows are all valid, with no row checks in
 //     its inner loop (straight-line MFMA code).
 //   kNarrow (64-row tiles whose valid rows fit the first 32-row block, and
-//     128-row tiles with 65-96 valid rows): instead of the waves of the
+//     128-row tiles with 81-96 valid rows): instead of the waves of the
 //     empty row blocks idling on their SIMDs, each of the 4 waves takes one
 //     32-column block and every row block that holds rows (a 128-row tile
 //     with 3 of its 4 row blocks then costs 3/4 of a full one).
@@ -119,8 +119,14 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 //     v_mfma_f32_16x16x4_f32 over 1, 2 or 3 16-row blocks, each wave taking
 //     a quarter of the columns as 16-column blocks (the 2-block form serves
 //     the half-width tiles, which the narrow layout cannot split in four).
+//     kSkinny5 / kSkinny7: the same over 5 or 7 16-row blocks, for 128-row
+//     tiles with 65-80 or 97-112 valid rows (5/8 and 7/8 of a full tile's
+//     MFMAs, where 32-row blocks take 3/4 and all of it).
 // Same tile, LDS layout and products in every layout.
-enum TileLayout { kWide = 0, kNarrow = 1, kSkinny1 = 2, kSkinny3 = 3, kFull = 4, kSkinny2 = 5 };
+enum TileLayout {
+  kWide = 0, kNarrow = 1, kSkinny1 = 2, kSkinny3 = 3, kFull = 4, kSkinny2 = 5, kSkinny5 = 6,
+  kSkinny7 = 7
+};
 
 // 64x128 tiles (the 2 x 2 grid of 32x64 wave tiles) and 128x128 tiles (2 x 2
 // of 64x64): four 32-column blocks, one per wave.  (A 128-row tile with at
@@ -129,11 +135,11 @@ template <typename TL>
 constexpr bool tile_narrowable() {
   return TL::WAVES_M == 2 && TL::WAVES_N == 2 && TL::WN == 2 && TL::BN == 128;
 }
-// 64-row tiles of 4 waves whose columns split into 16-column blocks per wave
-// (64x128 and the half-width 64x64): the 16-row layouts.
+// 64- and 128-row tiles of 4 waves whose columns split into 16-column blocks
+// per wave (64x128, the half-width 64x64, 128x128): the 16-row layouts.
 template <typename TL>
 constexpr bool tile_skinnyable() {
-  return TL::BM == 64 && TL::WAVES_M * TL::WAVES_N == 4 && TL::BN % 64 == 0;
+  return (TL::BM == 64 || TL::BM == 128) && TL::WAVES_M * TL::WAVES_N == 4 && TL::BN % 64 == 0;
 }
 
 // Slab loop of one tile: global loads NS slabs ahead in registers, LDS
@@ -150,7 +156,8 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
   constexpr int ROWS_PER_PASS = kThreads / TL::KV;
-  constexpr bool SKINNY = LAYOUT == kSkinny1 || LAYOUT == kSkinny2 || LAYOUT == kSkinny3;
+  constexpr bool SKINNY = LAYOUT == kSkinny1 || LAYOUT == kSkinny2 || LAYOUT == kSkinny3 ||
+                          LAYOUT == kSkinny5 || LAYOUT == kSkinny7;
   constexpr bool NARROW = LAYOUT == kNarrow;
   static_assert(!NARROW || tile_narrowable<TL>(), "narrow layout of 64x128 tiles");
   static_assert(!SKINNY || tile_skinnyable<TL>(), "16-row layouts of 64-row tiles");
@@ -174,7 +181,9 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   // skinny layout: lane l supplies row l % 16 at k offset 4 * (l / 16) of each
   // 16-wide k group, as a float4 whose component q feeds the q-th MFMA (the
   // same k permutation in A and B)
-  constexpr int SRB = LAYOUT == kSkinny3 ? 3 : LAYOUT == kSkinny2 ? 2 : 1;
+  constexpr int SRB = LAYOUT == kSkinny7 ? 7 : LAYOUT == kSkinny5 ? 5 : LAYOUT == kSkinny3 ? 3
+                      : LAYOUT == kSkinny2 ? 2 : 1;
+  static_assert(SRB * 16 <= BM, "16-row blocks of the tile");
   constexpr int SKC = BN / 64;  // 16-column blocks per wave
   const int l16 = lane & 15, k16 = (lane >> 4) * 4;
   const float *a16 = As + l16 * PITCH + k16;
@@ -351,17 +360,25 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   const uint32_t bsrc = (uint32_t)(lrow * K + lc4) * 4u;
   const int lds_st = lrow * TL::PITCH + lc4;
 
-  constexpr bool kNa = tile_narrowable<TL>(), kSk = tile_skinnyable<TL>();
+  constexpr bool kNa = tile_narrowable<TL>(), kSk = tile_skinnyable<TL>() && BM == 64;
+  constexpr bool kSkL = tile_skinnyable<TL>() && BM == 128;
   constexpr TileLayout kS1 = kSk ? kSkinny1 : kWide, kS2 = kSk ? kSkinny2 : kWide;
   constexpr TileLayout kS3 = kSk ? kSkinny3 : kWide, kNw = kNa ? kNarrow : kWide;
+  constexpr TileLayout kS5 = kSkL ? kSkinny5 : kWide, kS7 = kSkL ? kSkinny7 : kWide;
   int next;
-  if (kSk && rows_valid <= 16)
+  if (kSkL && rows_valid > 64 && rows_valid <= 80)
+    next = tile_slabs<TL, kS5>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head);
+  else if (kSkL && rows_valid > 96 && rows_valid <= 112)
+    next = tile_slabs<TL, kS7>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head);
+  else if (kSk && rows_valid <= 16)
     next = tile_slabs<TL, kS1>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
   else if (kSk && rows_valid > 32 && rows_valid <= 48)
     next = tile_slabs<TL, kS3>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
-  else if (kNa && (BM == 64 ? rows_valid <= 32 : rows_valid > 64 && rows_valid <= 96))
+  else if (kNa && (BM == 64 ? rows_valid <= 32 : rows_valid > 80 && rows_valid <= 96))
     next = tile_slabs<TL, kNw>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head);
   else if (kSk && rows_valid <= 32)
