@@ -95,6 +95,10 @@ def test_rmsnorm_rows_bit_exact(dim, rows, stride, oracle_mod):
 @pytest.mark.gpu
 @pytest.mark.parametrize("batch,seq", [(2, 512), (3, 37), (1, 1)])
 def test_qk_norm_rope_bit_exact(batch, seq, oracle_mod):
+    """GPU vs oracle bit for bit.  Both read `q1*c1 - q2*s1` (layer.cu:225-226)
+    the same way (q1*c1 fused into an FMA with the rounded product q2*s1), so
+    this shows that the two implementations agree, not that they match the
+    reference's nvcc build, whose contraction choice nothing pins."""
     from final_amd import lfm
     say(f"[qk_norm_rope] batch={batch} seq={seq}")
     T = batch * seq
