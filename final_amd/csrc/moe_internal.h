@@ -19,6 +19,11 @@ constexpr int kRouterSlotTokens = 1024;  // MFMA plans up to this many tokens: t
 // half-width gate/up tiles (T=56-128: 1.2-2 % faster; 160 equal; 192-256: 1 % slower)
 constexpr int kGateUpTailTokens = 128;
 constexpr int kGateUpTailUnits = 8;
+// 128-row plan up to this many tokens: the same for its last kGateUpTailUnits
+// units (a unit's 128-row gate/up tiles are long there, and its down tiles
+// wait for the last of them: T=832 755 -> 732 us, T=1024 868 -> 862; at
+// 2048 and 4096 tokens, where the down phase is long, 0.4-0.7 % slower)
+constexpr int kGateUpTailTokens128 = 1024;
 constexpr int kStreamRows = 16;  // weight rows per streaming-plan task (small batches)
 constexpr int kStreamWideTokens = 32;  // batches from this size use 64-row tasks
 // Streaming kernel shapes: tokens per MFMA pass; token passes of 16- and

@@ -285,10 +285,13 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
                               ? min(units, kRingTailUnits) : 0);
       const int tail_mult = tr > 0 ? 2 : kRingWideGroups;
       ctrl->tail_units = tail;
-      // 64-row plan of small batches (units of few rows, memory-bound
-      // tiles): the last units' gate/up tiles run at half width too, so the
-      // last gate/up tiles end sooner and the down tiles after them wait less
-      const int gtail = tr == 64 && T <= kGateUpTailTokens ? min(units, kGateUpTailUnits) : 0;
+      // small batches (the 64-row plan's units of few rows, memory-bound
+      // tiles; the 128-row plan's long tiles up to 1024 tokens): the last
+      // units' gate/up tiles run at half width too, so the last gate/up tiles
+      // end sooner and the down tiles after them wait less
+      const int gtail = tr == 64 && T <= kGateUpTailTokens ? min(units, kGateUpTailUnits)
+                        : tr == 128 && T <= kGateUpTailTokens128 ? min(units, kGateUpTailUnits)
+                                                                 : 0;
       ctrl->gu_tail = gtail;
       ctrl->n_p1 = (units + gtail) * p1u;
       ctrl->n_p2 = (units - tail + tail * tail_mult) * p2u;
@@ -1236,7 +1239,7 @@ void expert_mfma_kernel(ExpertArgs a) {
   if (tid < kExperts) s_counts[tid] = c->counts[tid];
   const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
   const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
-  const int gtail = BM == 64 ? c->gu_tail : 0;
+  const int gtail = BM >= 64 ? c->gu_tail : 0;
   const int nunits = n1 / p1u - gtail, tail = c->tail_units;
   const int H = a.H, I = a.I;
   const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
@@ -1285,7 +1288,7 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (tid == 0) next = claim(&c->head);
     } else if (task < nb + n1) {
       // gate/up tiles: full width for the first units, two half-width tiles
-      // per column range for the last gtail units (64-row plan)
+      // per column range for the last gtail units (small batches of either plan)
       const int q = task - nb;
       const int gfull = (nunits - gtail) * p1u;
       const bool ghalf = q >= gfull;
@@ -1312,6 +1315,16 @@ void expert_mfma_kernel(ExpertArgs a) {
           next = mfma_tile<TL, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
                                      I, nt * (TL::BN / 2), &c->head);
         }
+      } else if (BM == 128 && ghalf) {  // one W1/W3 row group: 32 intermediate columns
+        static_assert(TileHalf<64>::BN == TileHalf<128>::BN, "a half tile's columns");
+        using TH = TileHalf<128>;
+        const float *hrow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TH::BN) * H;
+        if (rows <= 64)
+          next = mfma_tile<TileHalf<64>, true>(lds, a.x, xbytes, s_aoff, rows, hrow0, H, inter_out,
+                                               slot0, I, nt * (TH::BN / 2), &c->head);
+        else
+          next = mfma_tile<TH, true>(lds, a.x, xbytes, s_aoff, rows, hrow0, H, inter_out, slot0, I,
+                                     nt * (TH::BN / 2), &c->head);
       } else if (BM == 128 && rows <= 64) {
         next = mfma_tile<Tile<64>, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
                                          I, nt * (TL::BN / 2), &c->head);

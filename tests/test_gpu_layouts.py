@@ -6,9 +6,12 @@ experts get logits 2..5, the others -4, so the per-expert counts are exactly
 the ones asked for.  Under the forced 64-row plan the counts 1-16, 17-32,
 33-48, 49-64 take the 16-row skinny, narrow, 3-block skinny and wide layouts
 (and counts above 64 add units of each size); under the forced 128-row plan
-units of at most 64 rows run as 64-row tiles, 65-96 rows as wide tiles with
-one row block of the lower half, 97-127 rows as wide tiles, 128 as full tiles,
-and the last units' down tiles as half-width tiles.  A second count set, with
+units of at most 64 rows run as 64-row tiles, 65-80 rows as 5-block 16-row
+skinny tiles, 81-96 as narrow tiles over three row blocks, 97-112 as 7-block
+skinny tiles, 113-127 as wide tiles, 128 as full tiles, and the last units'
+gate/up and down tiles as half-width tiles (the 128-row plan splits the
+last units' gate/up tiles up to 1024 tokens, the 64-row plan up to 128).  A
+second count set, with
 every expert under 64 tokens, takes the longest-first unit order of the
 64-row plan.  The reference y comes from the oracle's own routing of the same
 logits, dispatch, expert and combine functions.
