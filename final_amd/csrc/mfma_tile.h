@@ -104,6 +104,59 @@ __device__ __forceinline__ void slab_store(const f32x4 (&ra)[A_PER], const f32x4
 }
 
 
+// A-operand readiness of a tile's slabs.  NoWait: A is complete before the
+// tile starts.  SlabReady: A is the intermediate rows of one unit, whose
+// gate/up tiles each set one bit of a mask when their stores have completed
+// (tile n wrote columns [n w, n w + w)); wave 0 waits for the bits a slab's
+// columns need before the barrier that precedes the slab's loads, and keeps
+// the bits it has seen (wave-uniform, so the state stays in scalar
+// registers).  The rows are written once with agent-scope
+// stores and read by no one before their bit is set, so the loads after the
+// wait need no fence (the caches start the kernel invalidated).
+struct NoWait {
+  static constexpr bool kActive = false;
+  __device__ void wait(int) {}
+};
+// Slow path of SlabReady: polls mask word w until it holds bit mask m (or
+// the wait gives up and reports a timeout); returns the word.  Out of line
+// and with scalar arguments, so the slab loop keeps its registers and its
+// state stays out of memory.
+__device__ __attribute__((noinline)) unsigned slab_poll(const int *w, unsigned m, int limit,
+                                                         int *err) {
+  unsigned seen = 0;
+  for (int spins = 0;; ++spins) {
+    seen = (unsigned)__builtin_amdgcn_readfirstlane(load_relaxed(w));
+    if ((seen & m) == m) return seen;
+    if (spins >= limit) {
+      if ((threadIdx.x & 63) == 0) __hip_atomic_store(err, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return seen | m;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+struct SlabReady {
+  static constexpr bool kActive = true;
+  const int *bits;   // mask words of the unit (bit n: word n / 32)
+  int shift;         // log2 of the slabs one gate/up tile's columns span
+  int nslab;
+  int limit;         // polls before the wait gives up and reports a timeout
+  int *err;
+  int word = -1;     // the mask word last read (slabs come in order)
+  unsigned seen = 0;
+  // wave 0: wait until the gate/up tile behind the slab's columns is done
+  __device__ __forceinline__ void wait(int slab) {
+    if (slab >= nslab) return;
+    const int b = slab >> shift;
+    const unsigned m = 1u << (b & 31);
+    if (b >> 5 != word) {
+      word = b >> 5;
+      seen = 0;
+    }
+    if (!(seen & m)) seen = slab_poll(bits + word, m, limit, err);
+  }
+};
+
 // Wave layouts of the slab loop, chosen once per tile (each is its own
 // instantiation, so the inner loops have no runtime branches on the layout).
 //   kWide: the config's WAVES_M x WAVES_N grid of 32x32 blocks.
@@ -146,12 +199,12 @@ constexpr bool tile_skinnyable() {
 // double-buffered, one barrier per slab; then the block's next task is
 // claimed (thread 0; returned) and the products are written to the LDS
 // epilogue tile Cs [BM][CPITCH] in B-row order.
-template <typename TL, TileLayout LAYOUT>
+template <typename TL, TileLayout LAYOUT, typename Ready>
 __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL::A_PER],
                                           __amdgpu_buffer_rsrc_t abase_r,
                                           __amdgpu_buffer_rsrc_t bsrc_r,
                                           __amdgpu_buffer_rsrc_t none_r, uint32_t bsrc, int lds_st,
-                                          int lrow, int K, int rows_valid, int *head) {
+                                          int lrow, int K, int rows_valid, int *head, Ready &ready) {
   constexpr int BM = TL::BM, BN = TL::BN;
   constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
@@ -212,6 +265,13 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
   constexpr int NS = TL::NS;
   constexpr int L = NS % 2 == 0 ? NS : 2 * NS;  // steps per unrolled round
   f32x4 sa[NS][A_PER], sb[NS][B_PER];
+  if constexpr (Ready::kActive) {
+    // the A columns of the slabs loaded before the loop (0 .. NS - 1) and in
+    // its first step (NS); each later step waits for the one after it
+    if (wave == 0)
+      for (int j = 0; j <= NS; ++j) ready.wait(j);
+    __syncthreads();
+  }
 #pragma unroll
   for (int j = 0; j < NS; ++j) {
     const bool in = j < nslab;
@@ -280,6 +340,9 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
       slab_store<BM, A_PER, B_PER, ROWS_PER_PASS, PITCH>(
           sa[(u + 1) % NS], sb[(u + 1) % NS], As + ((u + 1) & 1) * BM * PITCH,
           Bs + ((u + 1) & 1) * BN * PITCH, lds_st, lrow);
+      // the next step loads slab t + 1 + NS: its A columns before the barrier
+      if constexpr (Ready::kActive)
+        if (wave == 0) ready.wait(t + 1 + NS);
       __syncthreads();
     }
   }
@@ -330,11 +393,12 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
 // trip, and a block commits to its next task only near the end of this one.
 // head == nullptr: no claim (grids of one tile per block).  `out` stores the
 // epilogue's float4s: out.store(byte offset into [rows][ldo], value).
-template <typename TL, bool GATED, typename Out = AgentOut>
+template <typename TL, bool GATED, typename Out = AgentOut, typename Ready = NoWait>
 __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_t abytes,
                                          const int *aoff, int rows_valid,
                                          const float *brow0, int K, const Out &out,
-                                         int row0, int ldo, int col0, int *head) {
+                                         int row0, int ldo, int col0, int *head,
+                                         Ready ready = Ready{}) {
   constexpr int BM = TL::BM;
   constexpr int KV = TL::KV, A_PER = TL::A_PER;
   constexpr int ROWS_PER_PASS = kThreads / KV;  // rows one pass of loads covers
@@ -367,29 +431,29 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   constexpr TileLayout kS5 = kSkL ? kSkinny5 : kWide, kS7 = kSkL ? kSkinny7 : kWide;
   int next;
   if (kSkL && rows_valid > 64 && rows_valid <= 80)
-    next = tile_slabs<TL, kS5>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                               rows_valid, head);
+    next = tile_slabs<TL, kS5, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head, ready);
   else if (kSkL && rows_valid > 96 && rows_valid <= 112)
-    next = tile_slabs<TL, kS7>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                               rows_valid, head);
+    next = tile_slabs<TL, kS7, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head, ready);
   else if (kSk && rows_valid <= 16)
-    next = tile_slabs<TL, kS1>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                               rows_valid, head);
+    next = tile_slabs<TL, kS1, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head, ready);
   else if (kSk && rows_valid > 32 && rows_valid <= 48)
-    next = tile_slabs<TL, kS3>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                               rows_valid, head);
+    next = tile_slabs<TL, kS3, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head, ready);
   else if (kNa && (BM == 64 ? rows_valid <= 32 : rows_valid > 80 && rows_valid <= 96))
-    next = tile_slabs<TL, kNw>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                               rows_valid, head);
+    next = tile_slabs<TL, kNw, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head, ready);
   else if (kSk && rows_valid <= 32)
-    next = tile_slabs<TL, kS2>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                               rows_valid, head);
+    next = tile_slabs<TL, kS2, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                               rows_valid, head, ready);
   else if (rows_valid >= BM)
-    next = tile_slabs<TL, kFull>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                                 rows_valid, head);
+    next = tile_slabs<TL, kFull, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                                 rows_valid, head, ready);
   else
-    next = tile_slabs<TL, kWide>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
-                                 rows_valid, head);
+    next = tile_slabs<TL, kWide, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+                                 rows_valid, head, ready);
 
   // Epilogue: the [BM][BN] tile in LDS is stored as whole-row float4s;
   // gate/up tiles store silu(W1 x) * (W3 x) of each 64-row group's two halves.

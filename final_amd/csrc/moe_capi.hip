@@ -64,7 +64,8 @@ constexpr size_t kNoAllocHeader = 8192;   // Ctrl + dep[], then tb_done[]
 constexpr size_t kNoAllocTbDone = 4096;   // offset of tb_done in the header
 constexpr int kNoAllocMaxUnits = kNoAllocMaxTokens * kTopK / 32 + kExperts + 1;
 constexpr int kMaxDevices = 64;
-static_assert(sizeof(Ctrl) + sizeof(int) * kNoAllocMaxUnits <= kNoAllocTbDone, "ctrl + dep fit");
+static_assert(sizeof(Ctrl) + 2 * sizeof(int) * kNoAllocMaxUnits <= kNoAllocTbDone,
+              "ctrl + dep fit for intermediates up to 2048 (noalloc_layout checks larger ones)");
 static_assert(kNoAllocTbDone + sizeof(int) * (kNoAllocMaxTokens / kMinRouterTokens) <=
                   kNoAllocHeader, "tb_done fits");
 
@@ -130,7 +131,8 @@ static bool noalloc_layout(char *base, int T, int H, int I, Scratch *s, int *max
   s->sout_bytes = (uint32_t)(S * H * sizeof(float));
   s->slot_cap = (int)S;
   *max_units = (int)(S / 32 + E + 1);
-  return off <= kNoAllocBytes;
+  return off <= kNoAllocBytes &&
+         sizeof(Ctrl) + sizeof(int) * (size_t)dep_words(I) * (size_t)*max_units <= kNoAllocTbDone;
 }
 
 struct moe_ctx {
@@ -329,8 +331,8 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
   ctx->s.sout_bytes = (uint32_t)(S * H * sizeof(float));
   ctx->s.slot_cap = (int)S;
   char *ctrl_mem = nullptr;
-  // Ctrl, then dep[max_units]
-  const size_t ctrl_bytes = sizeof(Ctrl) + sizeof(int) * (size_t)ctx->max_units;
+  // Ctrl, then dep[max_units][dep_words(I)]
+  const size_t ctrl_bytes = sizeof(Ctrl) + sizeof(int) * (size_t)dep_words((int)I) * ctx->max_units;
   if ((rc = dev_alloc(ctx, &ctrl_mem, ctrl_bytes))) {
     free_all(ctx);
     delete ctx;

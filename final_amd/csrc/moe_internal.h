@@ -87,8 +87,14 @@ struct Ctrl {
   // own: atomics on one line serialise, and head takes one per block
   alignas(128) int chain_head;
   int chain_done;
-  // followed in memory by int dep[max_units]: W1W3 tasks finished per unit
+  // followed in memory by int dep[max_units][dep_words(I)]: bit n of a
+  // unit's mask is set once its W1W3 (gate/up) tile n has stored its
+  // intermediate columns
 };
+
+// Mask words per unit of Scratch::dep: one bit per gate/up tile, at most
+// 2 I / 64 of them (half-width tiles of 32 intermediate columns).
+__host__ __device__ constexpr int dep_words(int inter) { return (inter + 1023) / 1024; }
 
 struct Weights {
   const float *gate;     // [E][H]
@@ -111,7 +117,7 @@ struct Scratch {
   uint32_t sout_bytes;
   int slot_cap;          // slot rows of slot_token, inter and sout
   Ctrl *ctrl;
-  int *dep;              // [max_units]
+  int *dep;              // [max_units][dep_words(I)]: gate/up tiles done per unit (bit masks)
   int *ccount;           // [Tmax][H/64]: expert outputs landed per (token, column tile)
 };
 

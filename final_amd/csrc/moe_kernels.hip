@@ -30,6 +30,8 @@
 // order, so the smallest unfinished task is always running and every wait
 // ends; each wait is still bounded and reports MOE_ERR_DEVICE_TIMEOUT instead
 // of spinning forever.
+#include <type_traits>
+
 #include "gpu_common.h"
 #include "mfma_tile.h"
 
@@ -328,7 +330,7 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
     }
   }
   const int units = min(ps.units, a.max_units);
-  for (int i = tid; i < units; i += kThreads) a.s.dep[i] = 0;
+  for (int i = tid; i < dep_words(a.inter) * units; i += kThreads) a.s.dep[i] = 0;
   // The streaming plan takes its slots from here, and so do the MFMA plans of
   // small batches (a few slots per thread): their gate/up tiles then start
   // without waiting for the expert kernel's dispatch tasks (T=256: ~7 us).
@@ -1332,7 +1334,12 @@ void expert_mfma_kernel(ExpertArgs a) {
         next = mfma_tile<Tile<BM>, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
                                          I, nt * (TL::BN / 2), &c->head);
       }
-      block_signal(&a.s.dep[u]);
+      // this tile's intermediate columns are stored: its bit of the unit's mask
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0)
+        __hip_atomic_fetch_or(&a.s.dep[(size_t)dep_words(I) * u + (nt >> 5)], (int)(1u << (nt & 31)),
+                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else if (task < nb + n1 + n2) {
       // down tiles: full width for the first units, two half-width tiles per
       // column range for the last tail units
@@ -1345,25 +1352,67 @@ void expert_mfma_kernel(ExpertArgs a) {
       unit_rows<BM>(u, uo, e, m0, rows);
       const int slot0 = s_offsets[e] + m0;
       block_wait(&c->assign_done, nb, a.wait_limit, &c->err);  // combine counters cleared
-      block_wait(&a.s.dep[u], u >= nunits - gtail ? 2 * p1u : p1u, a.wait_limit, &c->err);
       if (tid < BM) s_aoff[tid] = tid < rows ? tid * I : -1;
       __syncthreads();
+      // 32- and 64-row plans above 128 tokens: each slab of the tile waits
+      // for the gate/up tile that wrote its intermediate columns (half-width
+      // ones for the last gtail units), so the tile starts once its unit's
+      // first gate/up tiles have landed (T=256 320.7 -> 316.2 us, T=512
+      // 514.4 -> 507.4).  At 64-128 tokens, whose down tiles seldom wait (the
+      // per-slab form was 0.5 % slower there), and in the 128-row plan, whose
+      // slab loop has no registers to spare, the tile waits for all of them
+      // first.
+      static_assert(TL::BK == TileHalf<BM>::BK && (BM != 128 || Tile<64>::BK == TL::BK),
+                    "one slab width");
+      using Ready = typename std::conditional<BM == 128, NoWait, SlabReady>::type;
+      Ready ready{};
+      const bool whole = BM == 128 || a.T <= kGateUpTailTokens;
+      if (whole) {
+        if (tid == 0) {
+          const int *bits = a.s.dep + (size_t)dep_words(I) * u;
+          const int gbits = u >= nunits - gtail ? 2 * p1u : p1u;
+          for (int b = 0; b < gbits; b += 32) {
+            const unsigned m = gbits - b >= 32 ? ~0u : (1u << (gbits - b)) - 1u;
+            int spins = 0;
+            while (((unsigned)load_relaxed(bits + b / 32) & m) != m) {
+              __builtin_amdgcn_s_sleep(8);
+              if (++spins > a.wait_limit) {
+                st_agent(&c->err, 1);
+                break;
+              }
+            }
+          }
+        }
+        __syncthreads();
+      }
+      if constexpr (BM != 128) if (!whole) {
+        // a gate/up tile writes BN / 2 intermediate columns (a power of two,
+        // at least a slab's BK): slab s needs tile s >> shift
+        constexpr int kFullShift = __builtin_ctz(TL::BN / 2 / TL::BK);
+        constexpr int kHalfShift = __builtin_ctz(TileHalf<BM>::BN / 2 / TL::BK);
+        static_assert((TL::BN / 2) % TL::BK == 0 && (TileHalf<BM>::BN / 2) % TL::BK == 0 &&
+                          (1 << kFullShift) * TL::BK == TL::BN / 2 &&
+                          (1 << kHalfShift) * TL::BK == TileHalf<BM>::BN / 2,
+                      "gate/up tiles cover whole slabs");
+        ready = Ready{a.s.dep + (size_t)dep_words(I) * u, u >= nunits - gtail ? kHalfShift : kFullShift,
+                      I / TL::BK, a.wait_limit, &c->err};
+      }
       const float *abase = a.s.inter + (size_t)slot0 * I;
       const uint32_t abytes = a.s.inter_bytes - (uint32_t)((size_t)slot0 * I * sizeof(float));
       if (half) {
         using TH = TileHalf<BM>;
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TH::BN) * I;
         next = mfma_tile<TH, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
-                                    H, ht * TH::BN, &c->head);
+                                    H, ht * TH::BN, &c->head, ready);
         tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb);
       } else {
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
         if (BM == 128 && rows <= 64)
           next = mfma_tile<Tile<64>, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out,
-                                            slot0, H, ht * TL::BN, &c->head);
+                                            slot0, H, ht * TL::BN, &c->head, ready);
         else
           next = mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
-                                      H, ht * TL::BN, &c->head);
+                                      H, ht * TL::BN, &c->head, ready);
         tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb);
       }
     }
