@@ -9,8 +9,12 @@ What is modelled (final_amd/csrc/moe_kernels.hip):
   tasks, down tiles / down row tasks for their unit's or expert's gate/up
   tasks, the ring kernel's combine tasks for their token's down tasks.
 * expert_mfma_kernel: a block claims its first task as it starts, then per
-  task waits for the task's inputs (block_wait), computes, claims its next
-  task after the MFMAs and finishes the epilogue (which never waits).
+  task waits for the task's inputs, computes, claims its next task after the
+  MFMAs and finishes the epilogue (which never waits).  A down tile above
+  128 tokens waits slab by slab for the gate/up tile behind each slab
+  (SlabReady) rather than for all of its unit's at once; the model keeps the
+  all-at-once wait, which holds the block at least as long on the same set
+  of gate/up tasks, so every state the slab waits reach is covered.
 * expert_ring_kernel: a block claims its first task as it starts; streaming
   wave 0 claims the next one at an early step of the current task, which may
   come before or after the current task's wait for its inputs (the model
