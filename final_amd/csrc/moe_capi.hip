@@ -180,16 +180,16 @@ static int plan_index(int rows) {
 // Crossovers measured on MI355X with the seed-0 workload (whole-step times,
 // four weight copies cycled, clocks settled): weight streaming is fastest up
 // to 48 tokens (266 vs 276 us at 32, 279 vs 284 at 40, 284 vs 284 at 48),
-// 64-row MFMA tiles from 49 to 831 tokens (285 vs 288 us at 56, 286 vs 294
-// at 64, 782 vs 790 at 768), 128-row tiles from 832 (806 vs 822 us; 902 vs
-// 935 at 1024).
+// 64-row MFMA tiles from 49 to 1024 tokens (285 vs 288 us at 56, 286 vs 294
+// at 64; equal at 640-768; 720 vs 726 at 832, 846 vs 854 at 1024), 128-row
+// tiles from 1025 (990 vs 1023 us at 1280, 1478 vs 1540 at 2048).
 // The dense FFN's 4 chunk experts each hold every token, so its MFMA plans
 // have few tiles at small T: streaming stays fastest up to 192 tokens (214
 // vs 217 us at 128, 280 vs 283 at 192), 64-row tiles at 256 (290 vs 349 us),
 // 128-row tiles from 384 (433 vs 495 us at 512).
 static int auto_plan(int T, bool stream_ok, bool dense) {
   if (T <= (dense ? 192 : 48) && stream_ok) return 0;
-  if (T < (dense ? 384 : 832)) return 64;
+  if (T < (dense ? 384 : 1025)) return 64;
   return 128;
 }
 
