@@ -18,6 +18,9 @@ constexpr int kRouterSlotTokens = 1024;  // MFMA plans up to this many tokens: t
 // 64-row plan up to this many tokens: the last kGateUpTailUnits units run
 // half-width gate/up tiles (T=56-128: 1.2-2 % faster; 160 equal; 192-256: 1 % slower)
 constexpr int kGateUpTailTokens = 128;
+// 32/64-row plans: batches above this many tokens run their down tiles'
+// per-slab waits (below it a down tile waits for its whole unit first)
+constexpr int kSlabWaitMinTokens = 128;
 constexpr int kGateUpTailUnits = 8;
 // 128-row plan up to this many tokens: the same for its last kGateUpTailUnits
 // units (a unit's 128-row gate/up tiles are long there, and its down tiles

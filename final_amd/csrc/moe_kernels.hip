@@ -1366,7 +1366,7 @@ void expert_mfma_kernel(ExpertArgs a) {
                     "one slab width");
       using Ready = typename std::conditional<BM == 128, NoWait, SlabReady>::type;
       Ready ready{};
-      const bool whole = BM == 128 || a.T <= kGateUpTailTokens;
+      const bool whole = BM == 128 || a.T <= kSlabWaitMinTokens;
       if (whole) {
         if (tid == 0) {
           const int *bits = a.s.dep + (size_t)dep_words(I) * u;
