@@ -907,31 +907,35 @@ void router_decode_kernel(RouterArgs a) {
     // 2'. score bounds in place of the chains (score_bounds): 8 threads per
     // (token, expert) pair, k interleaved in float4s, four float sums of
     // products and four of magnitudes each (H / 32 FMAs per sum, then 2
-    // adds and 3 shuffle levels)
+    // adds and 3 shuffle levels).  The 8 threads of a pair are 8 consecutive
+    // lanes, so the pairs of tokens past the batch are skipped whole: at
+    // T=1 only wave 0's first half reads LDS (the sums were LDS-bound)
     const int pr = tid >> 3, part = tid & 7;
     const int tl = pr / kDecEPB, el = pr % kDecEPB;
-    const float *gp = gs + el * P, *xp = xs + min(tl, nt - 1) * P;
-    float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (tl < nt) {
+      const float *gp = gs + el * P, *xp = xs + tl * P;
+      float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 8
-    for (int k = part * 4; k < H; k += 32) {
-      const f32x4 g = ld4(gp + k), xv = ld4(xp + k);
+      for (int k = part * 4; k < H; k += 32) {
+        const f32x4 g = ld4(gp + k), xv = ld4(xp + k);
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        sq[q] = __builtin_fmaf(g[q], xv[q], sq[q]);
-        mq[q] = __builtin_fmaf(__builtin_fabsf(g[q]), __builtin_fabsf(xv[q]), mq[q]);
+        for (int q = 0; q < 4; ++q) {
+          sq[q] = __builtin_fmaf(g[q], xv[q], sq[q]);
+          mq[q] = __builtin_fmaf(__builtin_fabsf(g[q]), __builtin_fabsf(xv[q]), mq[q]);
+        }
       }
-    }
-    float sum = (sq[0] + sq[1]) + (sq[2] + sq[3]), mag = (mq[0] + mq[1]) + (mq[2] + mq[3]);
+      float sum = (sq[0] + sq[1]) + (sq[2] + sq[3]), mag = (mq[0] + mq[1]) + (mq[2] + mq[3]);
 #pragma unroll
-    for (int o = 1; o < 8; o <<= 1) {
-      sum += __shfl_xor(sum, o, 8);
-      mag += __shfl_xor(mag, o, 8);
-    }
-    if (part == 0 && tl < nt) {
-      float lo, hi;
-      score_bounds(sum, mag, H, H / 32 + 5, s_bias[e0 + el], &lo, &hi);
-      a.s.ctrl->sbound[0][tl][e0 + el] = lo;
-      a.s.ctrl->sbound[1][tl][e0 + el] = hi;
+      for (int o = 1; o < 8; o <<= 1) {
+        sum += __shfl_xor(sum, o, 8);
+        mag += __shfl_xor(mag, o, 8);
+      }
+      if (part == 0) {
+        float lo, hi;
+        score_bounds(sum, mag, H, H / 32 + 5, s_bias[e0 + el], &lo, &hi);
+        a.s.ctrl->sbound[0][tl][e0 + el] = lo;
+        a.s.ctrl->sbound[1][tl][e0 + el] = hi;
+      }
     }
     return;
   }
