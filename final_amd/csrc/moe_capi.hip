@@ -273,11 +273,15 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
   ctx->dense = dense;
   const size_t H = d.hidden, I = d.inter, E = kExperts;
   const size_t Tm = d.max_tokens;
-  // slot rows: the top-4 of every token, or the slots of every possible
-  // expert of a deferred decode routing (moe_forward up to kDeferTokens
-  // tokens), whichever is more
+  // slot rows: the top-4 of every token, the slots of every possible expert
+  // of a deferred decode routing (moe_forward up to kDeferTokens tokens), or
+  // of a routing from bounds under an MFMA plan (moe_forward up to
+  // kBoundTokens tokens; all 32 experts for a token whose bounds are
+  // infinite), whichever is most
   const size_t Ts = Tm < (size_t)kDeferTokens ? Tm : (size_t)kDeferTokens;
-  const size_t S = Tm * kTopK > Ts * kSpecSlots ? Tm * kTopK : Ts * kSpecSlots;
+  const size_t Tb = Tm < (size_t)kBoundTokens ? Tm : (size_t)kBoundTokens;
+  size_t S = Tm * kTopK > Ts * kSpecSlots ? Tm * kTopK : Ts * kSpecSlots;
+  if (!dense && S < Tb * kExperts) S = Tb * kExperts;
   const size_t nb = (Tm + kMinRouterTokens - 1) / kMinRouterTokens;
   ctx->max_units = (int)(S / 32 + E + 1);
   // inter and sout are addressed with 32-bit byte offsets, and the MFMA
@@ -322,7 +326,9 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
       (rc = dev_alloc(ctx, &ctx->s.slot_token, S)) ||
       (rc = dev_alloc(ctx, &ctx->s.inter, S * I)) ||
       (rc = dev_alloc(ctx, &ctx->s.sout, S * H)) ||
-      (rc = dev_alloc(ctx, &ctx->s.ccount, Tm * (H / 64)))) {
+      (rc = dev_alloc(ctx, &ctx->s.ccount, Tm * (H / 64))) ||
+      (!dense && (rc = dev_alloc(ctx, &ctx->s.bounds, Tb * 2 * E))) ||
+      (!dense && (rc = dev_alloc(ctx, &ctx->s.smap, Tb * kSmapStride)))) {
     free_all(ctx);
     delete ctx;
     return rc;
@@ -533,7 +539,14 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   a.max_units = ctx->max_units;
   // deferred decode routing: the router writes score bounds, the streaming
   // kernel computes the logits and routes
-  a.defer = defer && !logits && router_can_defer(T, a.tile_rows, a.bn) ? 2 : 0;
+  // MFMA plans of up to kBoundTokens tokens: the router writes score bounds
+  // and plans a slot for every expert they leave possible, and the expert
+  // kernel's dispatch tasks compute the logits and the exact top-4
+  const bool bound_room = ctx->s.bounds && ctx->s.smap &&
+                          (size_t)T * kExperts <= (size_t)ctx->s.slot_cap;
+  a.defer = !defer || logits ? 0
+            : router_can_defer(T, a.tile_rows, a.bn) ? 2
+            : bound_room && router_can_bound(T, a.tile_rows, a.H) ? 3 : 0;
   a.lazy_chains = ctx->lazy_chains ? 1 : 0;
   a.norm_w = norm_w;
   a.xn = xn;

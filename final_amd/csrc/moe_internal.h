@@ -49,6 +49,14 @@ constexpr int kChainJobs = kExperts / 4;
 // score bounds leave possible (usually exactly its top-4, sometimes 5 or 6),
 // at most kSpecSlots; a batch with a token past that waits for its logits.
 constexpr int kSpecSlots = 8;
+// MFMA plans: moe_forward of up to this many tokens routes from score bounds
+// (Ctrl::deferred == 3): the router plans a slot for every expert a token's
+// bounds leave possible, and the expert kernel's dispatch tasks compute the
+// logits and each token's exact top-4 while the gate/up tiles run.
+constexpr int kBoundTokens = 256;
+// Scratch::smap row: the slot of each (token, expert) pair the bounds leave
+// possible (the other entries are never read), then the mask of those experts
+constexpr int kSmapStride = kExperts + 1;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset
@@ -83,6 +91,8 @@ struct Ctrl {
   int offsets[kExperts + 1];
   int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)
   int active[kExperts];
+  // 3: the router planned from score bounds (MFMA plans), the expert kernel's
+  // dispatch tasks compute the logits and each token's exact top-4
   // deferred == 2: lower and upper bound of each (token, expert) score
   // sigmoid(logit) + bias, whatever order the logit's FMA chain ran in
   float sbound[2][kDeferTokens][kExperts];
@@ -122,6 +132,10 @@ struct Scratch {
   Ctrl *ctrl;
   int *dep;              // [max_units][dep_words(I)]: gate/up tiles done per unit (bit masks)
   int *ccount;           // [Tmax][H/64]: expert outputs landed per (token, column tile)
+  // routing from score bounds (Ctrl::deferred == 3), min(Tmax, kBoundTokens)
+  // tokens; null where a context has no room for it
+  float *bounds;         // [T][2][E]: lower, then upper bound of each score
+  int *smap;             // [T][kSmapStride]: slot of each possible pair, then the possible mask
 };
 
 struct RouterArgs {
@@ -135,7 +149,8 @@ struct RouterArgs {
   int bn;                // MFMA n-tile width (columns of the B tile)
   int tail_units;        // MFMA plans: last units whose down tiles run at half width
   int max_units;
-  int defer;             // 2: score bounds instead of the logits (router_can_defer); else 0
+  int defer;             // 2: score bounds instead of the logits (router_can_defer); 3: the
+                         // same for an MFMA plan (router_can_bound); else 0
   int lazy_chains;       // defer == 2: Ctrl::chain_lazy
   const float *norm_w;   // post-attention RMSNorm weight [H]: x is h, normalise it (decode router only)
   float *xn;             // [T][H]: the normalised rows, for the expert kernel
@@ -179,6 +194,9 @@ int expert_bn(int tile_rows, int T);
 // Whether a forward may leave routing and planning to the expert kernel: one
 // decode-router token block under the weight-streaming plan with 16-row tasks.
 bool router_can_defer(int T, int tile_rows, int bn);
+// Whether a forward under an MFMA plan may route from score bounds (the
+// context's Scratch must also hold bounds and smap, and T * kExperts slots).
+bool router_can_bound(int T, int tile_rows, int H);
 // Weight rows per streaming task for the dense FFN, whose chunks all hold T
 // tokens: 32-row tasks with 4 token passes above 32 tokens.
 int stream_rows_dense(int T);

@@ -184,7 +184,7 @@ struct PlanShared {
 // A planning block that routed the only token block itself passes its
 // routing from LDS instead of reading it back from memory.
 struct PlanLocal {
-  const int *cnt;              // [kExperts] tokens per expert
+  const int *cnt;              // [nb][kExperts] tokens (or possible pairs) per block and expert
   const int (*ids)[kTopK];     // [token][k] expert ids (-1: none)
   const int (*rank)[kTopK];    // [token][k] in-block ranks
 };
@@ -203,7 +203,8 @@ __device__ __forceinline__ int lane_scan32(int v, int lane, int *total) {
 
 template <int RT>
 __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
-                            const PlanLocal *loc = nullptr) {
+                            PlanLocal loc = PlanLocal{nullptr, nullptr, nullptr},
+                            const uint32_t *pmask = nullptr) {
   Ctrl *ctrl = a.s.ctrl;
   const int tid = threadIdx.x;
   const int e = tid & (kExperts - 1);
@@ -220,7 +221,9 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
     for (int b0 = lo; b0 < hi; b0 += kPlanRegBlocks) {
 #pragma unroll
       for (int i = 0; i < kPlanRegBlocks; ++i)
-        bv[i] = b0 + i < hi ? (loc ? loc->cnt[e] : a.s.blk[(b0 + i) * kExperts + e]) : 0;
+        bv[i] = b0 + i < hi ? (loc.cnt ? loc.cnt[(b0 + i) * kExperts + e]
+                                       : a.s.blk[(b0 + i) * kExperts + e])
+                            : 0;
 #pragma unroll
       for (int i = 0; i < kPlanRegBlocks; ++i) sum += bv[i];
     }
@@ -305,7 +308,7 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
       ctrl->tile_rows = tr;
       ctrl->head = 0;
       ctrl->assign_done = 0;
-      ctrl->deferred = 0;
+      ctrl->deferred = a.defer == 3 ? 3 : 0;
       ps.units = units;
     }
   }
@@ -340,15 +343,43 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
     // slot = token block base + in-block rank (stable by token), as the
     // dispatch tasks of the tiled plans compute it
     const int n = T * kTopK;
-    if (bases_lds && n <= kThreads * kPlanSlotsPerThread) {
+    if (pmask) {
+      // routing from bounds: a slot for every possible (token, expert) pair
+      // (bit e of the token's mask, LDS), a thread per token; smap takes
+      // the slots of the possible pairs (the others are never read)
+      const int total = ps.off[kExperts];
+      if (RT != kDeferTokens || !bases_lds || T > kBoundTokens) {
+        if (tid == 0)  // routing from bounds is planned for 8-token blocks only
+          __hip_atomic_store(&ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      } else if (tid < T) {
+        const int t = tid, b = t / RT;
+        uint32_t prev[RT];  // masks of the token block's earlier tokens
+#pragma unroll
+        for (int j = 0; j < RT; ++j) prev[j] = b * RT + j < t ? pmask[b * RT + j] : 0u;
+        for (uint32_t m = pmask[t]; m != 0; m &= m - 1) {
+          const int e = __builtin_ctz(m);
+          int rk = 0;
+#pragma unroll
+          for (int j = 0; j < RT; ++j) rk += (int)((prev[j] >> e) & 1u);
+          int slot = ps.base[b][e] + rk;
+          if (slot >= 0 && slot < total && slot < a.s.slot_cap) {
+            a.s.slot_token[slot] = t;
+          } else {  // inconsistent plan: flag it, never write out of range
+            slot = -1;
+            __hip_atomic_store(&ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          a.s.smap[(size_t)t * kSmapStride + e] = slot;
+        }
+      }
+    } else if (bases_lds && n <= kThreads * kPlanSlotsPerThread) {
       // every thread's (expert, rank) pairs loaded at once, bases from LDS
       int id[kPlanSlotsPerThread], rk[kPlanSlotsPerThread];
 #pragma unroll
       for (int i = 0; i < kPlanSlotsPerThread; ++i) {
         const int f = tid + i * kThreads;
-        if (loc) {
-          id[i] = f < n ? loc->ids[f / kTopK][f % kTopK] : -1;
-          rk[i] = f < n ? loc->rank[f / kTopK][f % kTopK] : 0;
+        if (loc.ids) {
+          id[i] = f < n ? loc.ids[f / kTopK][f % kTopK] : -1;
+          rk[i] = f < n ? loc.rank[f / kTopK][f % kTopK] : 0;
         } else {
           id[i] = f < n ? a.s.idx[f] : -1;
           rk[i] = f < n ? a.s.pos[f] : 0;
@@ -810,14 +841,79 @@ __device__ __forceinline__ void route_token_block(RouteShared &rs, int nt, const
   __syncthreads();
 }
 
+// Planning of a routing from score bounds (MFMA plans, up to kBoundTokens
+// tokens), by the last of the router's blocks, one thread per token:
+//  - the token's 32 lower and 32 upper bounds (one 256-byte row), and lo4,
+//    the 4th-largest lower bound;
+//  - expert e stays possible unless lo4 > hi(e): then four experts beat e
+//    strictly whatever the logits' rounding, and the strict-'>' insertion
+//    of layer.cu:465-476 cannot keep it.  So the set holds the token's
+//    exact top-4: usually exactly those 4, a 5th or 6th on a near-tie at
+//    the 4th place, all 32 where the bounds are infinite (non-finite
+//    inputs).  Its mask goes to LDS and to smap[t][kExperts];
+//  - counts per (token block, expert) of the possible pairs, the counts
+//    routing computes for the top-4 (layer.cu:494-497).
+// Then router_plan plans from those counts (loc) and the masks: a slot for
+// every possible pair, slot = token block base + in-block rank (the block's
+// earlier tokens with the same expert possible), stable by token.
+__host__ __device__ constexpr size_t bounds_plan_lds(int T) {
+  return ((size_t)kBoundTokens + (size_t)((T + kDecRT - 1) / kDecRT) * kExperts) * sizeof(int);
+}
+
+__device__ void bounds_plan(const RouterArgs &a, int T, float *lds, PlanLocal *loc,
+                            const uint32_t **pmask) {
+  static_assert(kBoundTokens <= kThreads, "a thread per token");
+  const int tid = threadIdx.x, nb = (T + kDecRT - 1) / kDecRT;
+  uint32_t *mask = reinterpret_cast<uint32_t *>(lds);               // [kBoundTokens]
+  int *cnt = reinterpret_cast<int *>(mask + kBoundTokens);          // [nb][kExperts]
+  if (tid < T) {
+    const float *b = a.s.bounds + (size_t)tid * 2 * kExperts;
+    f32x4 v[2 * kExperts / 4];
+#pragma unroll
+    for (int j = 0; j < 2 * kExperts / 4; ++j) v[j] = ld4(b + 4 * j);
+    // the four largest lower bounds (an insertion network)
+    float m0 = -__builtin_inff(), m1 = m0, m2 = m0, m3 = m0;
+#pragma unroll
+    for (int j = 0; j < kExperts; ++j) {
+      const float lo = v[j / 4][j % 4];
+      m3 = fmaxf(m3, fminf(m2, lo));
+      m2 = fmaxf(m2, fminf(m1, lo));
+      m1 = fmaxf(m1, fminf(m0, lo));
+      m0 = fmaxf(m0, lo);
+    }
+    uint32_t m = 0;
+#pragma unroll
+    for (int j = 0; j < kExperts; ++j) m |= (uint32_t)!(m3 > v[kExperts / 4 + j / 4][j % 4]) << j;
+    mask[tid] = m;
+    a.s.smap[(size_t)tid * kSmapStride + kExperts] = (int)m;
+  }
+  __syncthreads();
+  for (int i = tid; i < nb * kExperts; i += kThreads) {
+    const int b = i / kExperts, e = i % kExperts;
+    int run = 0;
+#pragma unroll
+    for (int r = 0; r < kDecRT; ++r) {
+      const int t = b * kDecRT + r;
+      if (t < T) run += (int)((mask[t] >> e) & 1u);
+    }
+    cnt[i] = run;
+  }
+  __syncthreads();
+  loc->cnt = cnt;
+  *pmask = mask;
+}
+
 // Expert-split router (T <= 256).  A token block is 8 tokens; its 32 experts are
 // split over 8 blocks of 4, so 8x more CUs share the gate.  Each block copies
 // its 4 gate rows and the token rows whole into LDS with direct-to-LDS loads
 // (no chunk loop) and runs one FMA chain per (token, expert) lane (the
 // reference's order, layer.cu:109-127).  The last of a token block's blocks
 // finishes it (route_token_block) and the last token block plans.  With
-// defer set (one token block, weight-streaming plan) the blocks stop after
-// the logits and the expert kernel routes and plans in its own blocks.
+// defer 2 (one token block, weight-streaming plan) the blocks write score
+// bounds in place of the chains and the expert kernel routes and plans in
+// its own blocks; with defer 3 (MFMA plans) they write the bounds and the
+// last block of all plans from them (bounds_plan), and the expert kernel's
+// dispatch tasks compute the logits and route.
 __host__ __device__ constexpr size_t router_decode_lds(int H) {
   return (size_t)(kDecEPB + kDecRT) * (size_t)(H + 4) * sizeof(float);
 }
@@ -840,7 +936,7 @@ void router_decode_kernel(RouterArgs a) {
   float *gs = lds, *xs = lds + kDecEPB * P;
   // the score bias, read now so the finishing block finds it in LDS
   if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
-  if (a.defer && blockIdx.x == 0 && tid == 0) {
+  if (a.defer == 2 && blockIdx.x == 0 && tid == 0) {
     // the streaming kernel routes and plans: its queues start at 0
     Ctrl *ctrl = a.s.ctrl;
     ctrl->head = 0;
@@ -903,7 +999,7 @@ void router_decode_kernel(RouterArgs a) {
     }
     __syncthreads();
   }
-  if (a.defer == 2) {
+  if (a.defer >= 2) {
     // 2'. score bounds in place of the chains (score_bounds): 8 threads per
     // (token, expert) pair, k interleaved in float4s, four float sums of
     // products and four of magnitudes each (H / 32 FMAs per sum, then 2
@@ -933,14 +1029,19 @@ void router_decode_kernel(RouterArgs a) {
       if (part == 0) {
         float lo, hi;
         score_bounds(sum, mag, H, H / 32 + 5, s_bias[e0 + el], &lo, &hi);
-        a.s.ctrl->sbound[0][tl][e0 + el] = lo;
-        a.s.ctrl->sbound[1][tl][e0 + el] = hi;
+        if (a.defer == 2) {
+          a.s.ctrl->sbound[0][tl][e0 + el] = lo;
+          a.s.ctrl->sbound[1][tl][e0 + el] = hi;
+        } else {  // read by the planning block (bounds_plan)
+          float *b = a.s.bounds + (size_t)(t0 + tl) * 2 * kExperts + e0 + el;
+          st_agent(b, lo);
+          st_agent(b + kExperts, hi);
+        }
       }
     }
-    return;
-  }
-  // 2. chains: wave 0, lane = (token l / 4, expert l % 4)
-  if (wave == 0) {
+    if (a.defer == 2) return;
+  } else if (wave == 0) {
+    // 2. chains: wave 0, lane = (token l / 4, expert l % 4)
     const int tl = lane >> 2, el = lane & 3;
     const float *gp = gs + el * P;
     const float *xp = xs + min(tl, nt - 1) * P;
@@ -950,54 +1051,70 @@ void router_decode_kernel(RouterArgs a) {
     // waves 1-3, idle during the chains, prepare the expert kernel's rows
     fill_unwritten(a, blockIdx.x, gridDim.x, tid - 64, kThreads - 64);
   }
-  // 3. the last of the token block's 8 blocks finishes it
-  __builtin_amdgcn_s_waitcnt(0);  // this block's logits are stored
-  __syncthreads();
-  if (tid == 0) {
-    s_flag = fetch_add(&a.s.tb_done[tb], 1) == kDecES - 1;
-    if (s_flag) {
-      a.s.tb_done[tb] = 0;  // all blocks counted in: reset
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
-  }
-  __syncthreads();
-  if (!s_flag) return;
-  // 4-7. probabilities, top-4, weights, in-block ranks and counts
-  {
-    const int tl = tid >> 5;  // thread = (token tl, expert tid % 32)
-    const float l = tl < nt ? a.s.logits[(size_t)(t0 + tl) * kExperts + (tid & (kExperts - 1))] : 0.0f;
-    route_token_block(rs, nt, s_bias, l);
-  }
   const int nb = gridDim.x / kDecES;
-  if (tid < nt) {
+  // the plan's input from LDS (one token block, or a routing from bounds)
+  PlanLocal loc{nullptr, nullptr, nullptr};
+  const uint32_t *pmask = nullptr;
+  if (a.defer == 3) {
+    // 3'. the last of all the router's blocks plans from the bounds
+    __builtin_amdgcn_s_waitcnt(0);  // this block's bounds are stored
+    __syncthreads();
+    if (tid == 0) {
+      s_flag = fetch_add(&a.s.ctrl->router_done, 1) == (int)gridDim.x - 1;
+      if (s_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    if (!s_flag) return;
+    bounds_plan(a, T, lds, &loc, &pmask);
+  } else {
+    // 3. the last of the token block's 8 blocks finishes it
+    __builtin_amdgcn_s_waitcnt(0);  // this block's logits are stored
+    __syncthreads();
+    if (tid == 0) {
+      s_flag = fetch_add(&a.s.tb_done[tb], 1) == kDecES - 1;
+      if (s_flag) {
+        a.s.tb_done[tb] = 0;  // all blocks counted in: reset
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      }
+    }
+    __syncthreads();
+    if (!s_flag) return;
+    // 4-7. probabilities, top-4, weights, in-block ranks and counts
+    {
+      const int tl = tid >> 5;  // thread = (token tl, expert tid % 32)
+      const float l = tl < nt ? a.s.logits[(size_t)(t0 + tl) * kExperts + (tid & (kExperts - 1))] : 0.0f;
+      route_token_block(rs, nt, s_bias, l);
+    }
+    if (tid < nt) {
 #pragma unroll
-    for (int i = 0; i < kTopK; ++i) {
-      st_agent(&a.s.idx[(size_t)(t0 + tid) * kTopK + i], rs.ti[tid][i]);
-      a.s.wts[(size_t)(t0 + tid) * kTopK + i] = rs.tw[tid][i];
+      for (int i = 0; i < kTopK; ++i) {
+        st_agent(&a.s.idx[(size_t)(t0 + tid) * kTopK + i], rs.ti[tid][i]);
+        a.s.wts[(size_t)(t0 + tid) * kTopK + i] = rs.tw[tid][i];
+      }
+    }
+    if (nb == 1) {
+      // a single token block plans from LDS (its plan writes pos and blk)
+      static_assert(kDecRT <= kRouterSlotTokens, "one token block: the plan assigns every slot");
+      loc = PlanLocal{rs.cnt, rs.ti, rs.rank};
+    } else {
+      {
+        const int tl = tid >> 5, e = tid & (kExperts - 1);
+        const int sel = rs.sel[tl][e];
+        if (sel >= 0) st_agent(&a.s.pos[(size_t)(t0 + tl) * kTopK + sel], rs.rank[tl][sel]);
+        if (tl == 0) st_agent(&a.s.blk[tb * kExperts + e], rs.cnt[e]);
+      }
+      // 8. the token block that finishes last plans
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0) {
+        s_flag = fetch_add(&a.s.ctrl->router_done, 1) == nb - 1;
+        if (s_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      }
+      __syncthreads();
+      if (!s_flag) return;
     }
   }
-  if (nb == 1) {  // a single token block plans from LDS (its plan writes pos and blk)
-    static_assert(kDecRT <= kRouterSlotTokens, "one token block: the plan assigns every slot");
-    const PlanLocal loc{rs.cnt, rs.ti, rs.rank};
-    router_plan<kDecRT>(a, 1, T, ps, &loc);
-    return;
-  }
-  {
-    const int tl = tid >> 5, e = tid & (kExperts - 1);
-    const int sel = rs.sel[tl][e];
-    if (sel >= 0) st_agent(&a.s.pos[(size_t)(t0 + tl) * kTopK + sel], rs.rank[tl][sel]);
-    if (tl == 0) st_agent(&a.s.blk[tb * kExperts + e], rs.cnt[e]);
-  }
-  // 8. the token block that finishes last plans
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (tid == 0) {
-    s_flag = nb == 1 || (fetch_add(&a.s.ctrl->router_done, 1) == nb - 1);
-    if (s_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-  }
-  __syncthreads();
-  if (!s_flag) return;
-  router_plan<kDecRT>(a, nb, T, ps);
+  router_plan<kDecRT>(a, nb, T, ps, loc, pmask);
 }
 
 // Dense SwiGLU FFN (MLP::forward_gpu, layer.cu:1231-1269) as the block with
@@ -1108,9 +1225,14 @@ __device__ __forceinline__ int slot_tok(const ExpertArgs &a, int slot) {
 // The tile's stores have completed before it counts (agent-scope stores), and
 // the completing block acquires before it reads the other tiles' outputs.
 // y may alias the residual: a thread reads its columns before it writes them.
+// bounds: the plan has a slot for every expert a token's score bounds leave
+// possible (Ctrl::deferred == 3, the token's mask in smap), so its outputs
+// are complete once all of its slots have landed; the sum takes its exact
+// top-4 (pos, wts), which the dispatch tasks published before any down tile
+// started.
 template <int BN>
 __device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int col0, int *s_list,
-                             int *s_n) {
+                             int *s_n, bool bounds) {
 #pragma clang fp contract(off)
   constexpr int NJ = BN / kCombineCols;  // counters the tile's columns cover
   const int tid = threadIdx.x;
@@ -1121,8 +1243,12 @@ __device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int col0,
   if (tid < rows) {
     const int t = slot_tok(a, slot0 + tid);
     int nvalid = 0;
+    if (bounds) {
+      nvalid = __popc((uint32_t)a.s.smap[(size_t)t * kSmapStride + kExperts]);
+    } else {
 #pragma unroll
-    for (int k = 0; k < kTopK; ++k) nvalid += a.s.pos[(size_t)t * kTopK + k] >= 0;
+      for (int k = 0; k < kTopK; ++k) nvalid += a.s.pos[(size_t)t * kTopK + k] >= 0;
+    }
 #pragma unroll
     for (int j = 0; j < NJ; ++j)
       if (fetch_add(&a.s.ccount[(size_t)t * ncc + j0 + j], 1) == nvalid - 1)
@@ -1172,6 +1298,130 @@ __device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int col0,
 }
 
 
+
+// Gate logits of TB token blocks (nt <= TB * kDecRT tokens from row t0) in
+// the MFMA kernel: thread (token tid / 32, expert tid % 32) runs the FMA
+// chains of that token of each of the TB blocks, each over k ascending,
+// chain_dot's order (layer.cu:109-127), on operands staged through LDS in
+// KC-wide chunks (the 32 gate rows, then the token rows), double-buffered,
+// with the global loads of the next NR chunks in flight in registers (the
+// weight tiles keep HBM busy meanwhile, so a load waits several
+// microseconds).  acc[j]: the logit of token block j's token (tokens past nt:
+// a copy of the last token's).  Ends with a barrier, after which lds is free.
+template <int KC, int TB> constexpr int bc_floats() {
+  return 2 * (kExperts + kDecRT * TB) * (KC + 4);
+}
+
+template <int KC, int NR, int TB>
+__device__ void block_chains(const float *x, const float *gate, int t0, int nt, int H,
+                             float *lds, float (&acc)[TB]) {
+#pragma clang fp contract(off)
+  constexpr int ROWS = kExperts + kDecRT * TB, P = KC + 4, F4 = ROWS * KC / 4;
+  constexpr int PERT = (F4 + kThreads - 1) / kThreads;
+  const int tid = threadIdx.x, tl = tid >> 5, e = tid & (kExperts - 1);
+  const int nc = H / KC;
+  f32x4 v[NR][PERT];
+  auto load = [&](int c, f32x4 (&d)[PERT]) {
+    if (c >= nc) return;
+#pragma unroll
+    for (int i = 0; i < PERT; ++i) {
+      const int f = tid + i * kThreads;
+      if (f < F4) {
+        const int r = f / (KC / 4), c4 = f % (KC / 4);
+        const float *row = r < kExperts ? gate + (size_t)r * H
+                                        : x + (size_t)(t0 + min(r - kExperts, nt - 1)) * H;
+        d[i] = ld4(row + c * KC + 4 * c4);
+      }
+    }
+  };
+  auto store = [&](const f32x4 (&d)[PERT], float *b) {
+#pragma unroll
+    for (int i = 0; i < PERT; ++i) {
+      const int f = tid + i * kThreads;
+      if (f < F4) st4(b + (f / (KC / 4)) * P + 4 * (f % (KC / 4)), d[i]);
+    }
+  };
+  // chunk 0 in LDS, chunks 1 .. NR - 1 in registers v[1 ..]
+  load(0, v[0]);
+  store(v[0], lds);
+#pragma unroll
+  for (int j = 1; j < NR; ++j) load(j, v[j]);
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < TB; ++j) acc[j] = 0.0f;
+  for (int c0 = 0; c0 < nc; c0 += NR) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int c = c0 + r;
+      if (c >= nc) break;
+      // v[r] held chunk c (in LDS since the last step): chunk c + NR
+      load(c + NR, v[r]);
+      const float *b = lds + (c & 1) * ROWS * P;
+      const float *gp = b + e * P, *xp = b + (kExperts + tl) * P;
+#pragma unroll 4
+      for (int k = 0; k < KC; k += 4) {
+        const f32x4 g = ld4(gp + k);
+#pragma unroll
+        for (int j = 0; j < TB; ++j) {
+          const f32x4 xv = ld4(xp + j * kDecRT * P + k);
+          acc[j] = __builtin_fmaf(xv.x, g.x, acc[j]);
+          acc[j] = __builtin_fmaf(xv.y, g.y, acc[j]);
+          acc[j] = __builtin_fmaf(xv.z, g.z, acc[j]);
+          acc[j] = __builtin_fmaf(xv.w, g.w, acc[j]);
+        }
+      }
+      // chunk c + 1 to the other buffer (last read in chunk c - 1)
+      if (c + 1 < nc) store(v[(r + 1) % NR], lds + ((c + 1) & 1) * ROWS * P);
+      __syncthreads();
+    }
+  }
+}
+
+// Routing job q of a routing from score bounds (Ctrl::deferred == 3), run by
+// the dispatch task of token block q * TB: the logits of token blocks q * TB
+// .. q * TB + TB - 1 (block_chains), each block's exact routing
+// (route_token_block: the reference's sigmoid, strict-'>' top-4 and
+// weights), and for each (token, rank) the slot the plan gave that expert
+// (the possible set holds the exact top-4: a miss, which the token's mask
+// shows, is an inconsistent plan, flagged).  Down tiles, whose combines read
+// idx / wts / pos, start only after every dispatch task has signalled.
+template <int KC, int NR, int TB>
+__device__ void route_task(const ExpertArgs &a, int q, float *lds) {
+  const int tid = threadIdx.x, tl = tid >> 5, e = tid & (kExperts - 1);
+  const int t0 = q * TB * kDecRT, nt = min(TB * kDecRT, a.T - t0);
+  float l[TB];
+  block_chains<KC, NR, TB>(a.x, a.w.gate, t0, nt, a.H, lds, l);
+  RouteShared &rs = *reinterpret_cast<RouteShared *>(lds);
+  float *bias = lds + (sizeof(RouteShared) + sizeof(float) - 1) / sizeof(float);
+  if (tid < kExperts) bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
+#pragma unroll
+  for (int j = 0; j < TB; ++j)
+    if (j * kDecRT + tl < nt) a.s.logits[(size_t)(t0 + j * kDecRT + tl) * kExperts + e] = l[j];
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < TB; ++j) {
+    const int tb0 = t0 + j * kDecRT, ntj = min(kDecRT, a.T - tb0);
+    if (ntj <= 0) break;
+    route_token_block(rs, ntj, bias, l[j]);
+    if (tid < ntj * kTopK) {
+      const int tt = tid / kTopK, k = tid % kTopK, t = tb0 + tt;
+      const int ee = rs.ti[tt][k];
+      int slot = -1;
+      if (ee >= 0 && ee < kExperts) {
+        const uint32_t m = (uint32_t)a.s.smap[(size_t)t * kSmapStride + kExperts];
+        slot = (m >> ee) & 1u ? a.s.smap[(size_t)t * kSmapStride + ee] : -1;
+        if (slot < 0 || slot >= a.s.slot_cap) {
+          slot = -1;
+          __hip_atomic_store(&a.s.ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      st_agent(&a.s.idx[(size_t)t * kTopK + k], ee);
+      st_agent(&a.s.wts[(size_t)t * kTopK + k], rs.tw[tt][k]);
+      st_agent(&a.s.pos[(size_t)t * kTopK + k], slot);
+    }
+    __syncthreads();  // rs is rewritten by the next block's routing
+  }
+}
 
 // Expert owning unit u: the largest e with unit_off[e] <= u (skips experts
 // without units, whose unit_off equals the next one's).
@@ -1278,21 +1528,40 @@ void expert_mfma_kernel(ExpertArgs a) {
   // tasks, which then only clear the combine counters (down tiles wait for
   // them) and write the rows of tokens without an expert
   const bool slots_ready = c->slots_assigned != 0;
+  const bool bounds = c->deferred == 3;
+  // routing jobs (routing from bounds): one token block each, 128-wide k
+  // chunks where the tiles' LDS holds two of them (else 64), six chunks of
+  // loads in flight
+  constexpr int kBcTB = 1, kBcNR = 6;
+  constexpr int kBcKC = bc_floats<128, kBcTB>() <= TL::LDS_FLOATS ? 128 : 64;
+  static_assert(bc_floats<kBcKC, kBcTB>() <= TL::LDS_FLOATS &&
+                    sizeof(RouteShared) + kExperts * sizeof(float) <= TL::LDS_FLOATS * sizeof(float),
+                "a routing job's chains and routing fit the kernel's LDS");
   int task = s_task;
+  // Dispatch tasks lead the queue and a block's claims only grow, so a block
+  // runs all of its dispatch tasks before its first tile (a loop of their
+  // own: the tiles' registers are allocated apart from the routing's).
+  while (task < nb && task < ntot) {
+    const int rt = c->rtokens;
+    if (!bounds)
+      assign_task(a, task, rt, slots_ready);
+    else if (task % kBcTB == 0)
+      route_task<kBcKC, kBcNR, kBcTB>(a, task / kBcTB, lds);
+    // this router block's tokens start with no expert outputs counted
+    const int ncc = H / kCombineCols;
+    for (int i = tid; i < rt * ncc; i += kThreads) {
+      const int tok = task * rt + i / ncc;
+      if (tok < a.T) st_agent(&a.s.ccount[(size_t)tok * ncc + i % ncc], 0);
+    }
+    block_signal(&c->assign_done);
+    if (tid == 0) s_task = claim(&c->head);
+    __syncthreads();
+    task = s_task;
+    __syncthreads();
+  }
   while (task < ntot) {
     int next = 0;  // the block's next task (thread 0), claimed near this one's end
-    if (task < nb) {
-      const int rt = c->rtokens;
-      assign_task(a, task, rt, slots_ready);
-      // this router block's tokens start with no expert outputs counted
-      const int ncc = H / kCombineCols;
-      for (int i = tid; i < rt * ncc; i += kThreads) {
-        const int tok = task * rt + i / ncc;
-        if (tok < a.T) st_agent(&a.s.ccount[(size_t)tok * ncc + i % ncc], 0);
-      }
-      block_signal(&c->assign_done);
-      if (tid == 0) next = claim(&c->head);
-    } else if (task < nb + n1) {
+    if (task < nb + n1) {
       // gate/up tiles: full width for the first units, two half-width tiles
       // per column range for the last gtail units (small batches of either plan)
       const int q = task - nb;
@@ -1408,7 +1677,7 @@ void expert_mfma_kernel(ExpertArgs a) {
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TH::BN) * I;
         next = mfma_tile<TH, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
                                     H, ht * TH::BN, &c->head, ready);
-        tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb);
+        tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb, bounds);
       } else {
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
         if (BM == 128 && rows <= 64)
@@ -1417,7 +1686,7 @@ void expert_mfma_kernel(ExpertArgs a) {
         else
           next = mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
                                       H, ht * TL::BN, &c->head, ready);
-        tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb);
+        tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb, bounds);
       }
     }
     __syncthreads();
@@ -2631,6 +2900,8 @@ constexpr int kLargeRT = 64, kLargeKC = 64;
 // that keeps the grid within about one block per CU (T=4096: 64 token blocks
 // x 4, router 90 -> 51 us; at T=16384 the unsplit 256 blocks are fastest).
 constexpr int kSplitRouterTokens = 256;  // 505 vs 527 us per step at 256 tokens, 563 vs 545 at 384
+static_assert(kBoundTokens <= kSplitRouterTokens && kBoundTokens / kDecRT <= kPlanLdsBlocks,
+              "routing from bounds runs in the decode router, its bases in LDS");
 
 int router_tokens_per_block(int T) { return T <= kSplitRouterTokens ? kSmallRT : kLargeRT; }
 
@@ -2659,7 +2930,8 @@ hipError_t launch_rmsnorm(const float *h, const float *w, float *out, int T, int
 hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) {
   const bool small = a.T <= 64;
   if (a.T <= kSplitRouterTokens && !from_logits) {
-    const size_t lds = router_decode_lds(a.H);
+    size_t lds = router_decode_lds(a.H);
+    if (a.defer == 3 && bounds_plan_lds(a.T) > lds) lds = bounds_plan_lds(a.T);
     if (lds > 65536) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&router_decode_kernel),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -2763,6 +3035,10 @@ hipError_t launch_experts(const ExpertArgs &a, int tile_rows, int grid,
 
 int stream_rows_dense(int T) {
   return T > 2 * kRingTokens ? kStreamRows * kRingDenseGroups : expert_bn(0, T);
+}
+
+bool router_can_bound(int T, int tile_rows, int H) {
+  return T >= 1 && T <= kBoundTokens && tile_rows > 0 && H % 256 == 0;
 }
 
 bool router_can_defer(int T, int tile_rows, int bn) {

@@ -361,6 +361,7 @@ def _forward_vs_route_experts(block, w, T, x, r, label, lazy=False):
         hip.synchronize()
         block.check_device()
         rt1 = block.last_routing()
+        rt1["plan_counts"] = block.last_plan_counts()
     finally:
         block.set_lazy_chains(False)
     say(f"[{label}] T={T} moe_route + moe_experts")
@@ -373,12 +374,23 @@ def _forward_vs_route_experts(block, w, T, x, r, label, lazy=False):
     return dy1.download(), rt1, dy2.download(), rt2
 
 
-def _check_same(y1, rt1, y2, rt2):
-    assert np.array_equal(bits(y1), bits(y2))
+def _check_same(y1, rt1, y2, rt2, tiled=False):
+    """The routing bit for bit; y bit for bit, except under an MFMA plan
+    (tiled) whose routing from score bounds planned a slot for an expert a
+    token did not take (a near-tie at the 4th place): that row changes its
+    expert's row count, and so possibly its tiles' MFMA shape, which sets the
+    rounding of the k-sums; y then agrees within the parity tolerance (and
+    each run matches the oracle, checked by the callers)."""
     for k in ("idx", "counts"):
         assert np.array_equal(rt1[k], rt2[k])
     for k in ("w", "logits"):
         assert np.array_equal(bits(rt1[k]), bits(rt2[k]))
+    extra = int(rt1["plan_counts"].sum()) - int(rt1["counts"].sum())
+    assert extra >= 0
+    if tiled and extra > 0:
+        np.testing.assert_allclose(y1, y2, rtol=RTOL, atol=ATOL)
+    else:
+        assert np.array_equal(bits(y1), bits(y2))
 
 
 @pytest.mark.gpu
@@ -491,10 +503,13 @@ def _ref_scores(O, w, x):
 @pytest.mark.gpu
 @pytest.mark.parametrize("T", [49, 64, 100, 129, 200, 256])
 def test_forward_random_batches_mfma(T, block, real_weights, oracle_mod):
-    """Random N(0, 1) batches under the 64-row MFMA plan, routed by several
-    token blocks of the decode router: routing (idx, w, counts, logits) and y
-    of moe_forward bit-identical to moe_route + moe_experts, and matching the
-    oracle."""
+    """Random N(0, 1) batches under the 64-row MFMA plan.  moe_forward's
+    router writes score bounds and plans a slot for every expert they leave
+    possible (several token blocks, each finished by its last block); the
+    expert kernel's dispatch tasks compute the logits and the exact top-4.
+    Its routing (idx, w, counts, logits) must be bit-identical to moe_route
+    + moe_experts, where the router computes the logits first, y too when no
+    extra slot was planned (_check_same), and both must match the oracle."""
     from final_amd import workloads as W
     w = real_weights
     assert block.plan(T) == 64
@@ -502,10 +517,13 @@ def test_forward_random_batches_mfma(T, block, real_weights, oracle_mod):
     x = rng.standard_normal((T, W.H)).astype(np.float32)
     r = rng.standard_normal((T, W.H)).astype(np.float32)
     y1, rt1, y2, rt2 = _forward_vs_route_experts(block, w, T, x, r, "random batch mfma")
-    _check_same(y1, rt1, y2, rt2)
+    say(f"[random batch mfma] T={T} slots planned {int(rt1['plan_counts'].sum())} "
+        f"for {int(rt1['counts'].sum())} routed")
+    _check_same(y1, rt1, y2, rt2, tiled=True)
     ref = oracle_forward(oracle_mod, w, x, residual=r)
     check_routing(rt1, ref)
     np.testing.assert_allclose(y1, ref["y"], rtol=RTOL, atol=ATOL)
+    np.testing.assert_allclose(y2, ref["y"], rtol=RTOL, atol=ATOL)
 
 
 @pytest.mark.gpu
@@ -516,7 +534,11 @@ def test_forward_routing_ties_many_blocks(T, plan, block, real_weights, oracle_m
     a and b share the 4th place for as many tokens as possible.  Each tied
     token keeps the lower index (the strict '>' insertion of
     layer.cu:465-476), under the 64-row plan of the decode router's several
-    token blocks and under forced MFMA plans at small T."""
+    token blocks and under forced MFMA plans at small T (one token block
+    for T=5: the finishing block plans from its own LDS).  No score bound
+    separates an exact tie, so moe_forward's routing from bounds plans a
+    slot for both experts of each tied token, and the dispatch tasks' exact
+    routing keeps one."""
     from final_amd import workloads as W
     rng = np.random.default_rng(800 + T)
     x = rng.standard_normal((T, W.H)).astype(np.float32)
@@ -551,7 +573,9 @@ def test_forward_routing_ties_many_blocks(T, plan, block, real_weights, oracle_m
         block.force_tile_rows(-1)
         rw = real_weights
         block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
-    _check_same(y1, rt1, y2, rt2)
+    # no bound separates an exact tie: each tied token has both experts planned
+    assert int(rt1["plan_counts"].sum()) >= int(rt1["counts"].sum()) + len(tied)
+    _check_same(y1, rt1, y2, rt2, tiled=True)
     for t in tied:
         assert min(a, b) in rt1["idx"][t].tolist() and max(a, b) not in rt1["idx"][t].tolist()
     ref = oracle_forward(oracle_mod, w, x, residual=r)
