@@ -10,7 +10,9 @@ What is modelled (final_amd/csrc/moe_kernels.hip):
   tasks, the ring kernel's combine tasks for their token's down tasks.
 * expert_mfma_kernel: a block claims its first task as it starts, then per
   task waits for the task's inputs, computes, claims its next task after the
-  MFMAs and finishes the epilogue (which never waits).  A down tile above
+  MFMAs and finishes the epilogue (which never waits).  Dispatch tasks never
+  wait (also when, routing from score bounds, they run the gate chains and
+  the exact routing); down tiles wait for every dispatch task.  A down tile above
   128 tokens waits slab by slab for the gate/up tile behind each slab
   (SlabReady) rather than for all of its unit's at once; the model keeps the
   all-at-once wait, which holds the block at least as long on the same set
@@ -78,13 +80,20 @@ class Plan:
     combine_deps: tuple    # ring kernel: per token, the tasks its combine waits for
 
 
-def mfma_plan(n_dispatch=2, units=2, p1=2, p2=2):
+def mfma_plan(n_dispatch=2, units=2, p1=2, p2=2, router_slots=False):
+    """router_slots: the router assigned the slots (batches of up to 1024
+    tokens; with routing from score bounds the dispatch tasks compute the
+    logits and exact routing instead), so gate/up tiles do not wait for the
+    dispatch tasks, and down tiles wait for all of them (their combine
+    counters, and the routing their combines read) and their unit's gate/up
+    tiles."""
     deps = [frozenset()] * n_dispatch
     g0 = n_dispatch
+    disp = frozenset(range(n_dispatch))
     for u in range(units):
-        deps += [frozenset(range(n_dispatch))] * p1
+        deps += [frozenset() if router_slots else disp] * p1
     for u in range(units):
-        deps += [frozenset(range(g0 + u * p1, g0 + (u + 1) * p1))] * p2
+        deps += [disp | frozenset(range(g0 + u * p1, g0 + (u + 1) * p1))] * p2
     return Plan(tuple(deps), len(deps), ())
 
 
@@ -201,6 +210,9 @@ CASES = [(G, R) for G in (1, 2, 3) for R in range(1, G + 1)]
 def test_mfma_kernel_protocol_never_sticks(G, R):
     assert explore(mfma_plan(), "mfma", G, R) is None
     assert explore(mfma_plan(n_dispatch=1, units=3, p1=1, p2=2), "mfma", G, R) is None
+    assert explore(mfma_plan(router_slots=True), "mfma", G, R) is None
+    assert explore(mfma_plan(n_dispatch=2, units=2, p1=1, p2=2, router_slots=True), "mfma",
+                   G, R) is None
 
 
 @pytest.mark.parametrize("G,R", CASES)
