@@ -153,6 +153,8 @@ struct moe_ctx {
   int routed_T = -1;
   bool route_pending = false;  // a routing not yet consumed by moe_experts
   int routed_plan = -1;
+  bool routed_bounds = false;  // the routing wrote score bounds (RouterArgs::defer 3)
+  int routed_tail = 0;         // its tail units
   // device memory
   float *gate = nullptr;
   float *bias = nullptr;
@@ -328,7 +330,7 @@ static int create_ctx(const moe_dims &d, size_t e_alloc, bool dense, moe_ctx **o
       (rc = dev_alloc(ctx, &ctx->s.sout, S * H)) ||
       (rc = dev_alloc(ctx, &ctx->s.ccount, Tm * (H / 64))) ||
       (!dense && (rc = dev_alloc(ctx, &ctx->s.bounds, Tb * 2 * E))) ||
-      (!dense && (rc = dev_alloc(ctx, &ctx->s.smap, Tb * kSmapStride)))) {
+      (!dense && (rc = dev_alloc(ctx, &ctx->s.bplan, (size_t)kPlanCopies * kPlanCopyInts)))) {
     free_all(ctx);
     delete ctx;
     return rc;
@@ -539,11 +541,12 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   a.max_units = ctx->max_units;
   // deferred decode routing: the router writes score bounds, the streaming
   // kernel computes the logits and routes
-  // MFMA plans of up to kBoundTokens tokens: the router writes score bounds
-  // and plans a slot for every expert they leave possible, and the expert
-  // kernel's dispatch tasks compute the logits and the exact top-4
-  const bool bound_room = ctx->s.bounds && ctx->s.smap &&
-                          (size_t)T * kExperts <= (size_t)ctx->s.slot_cap;
+  // 32- and 64-row MFMA plans of up to kBoundTokens tokens: the router writes
+  // score bounds, every block of the expert kernel plans a slot for every
+  // expert they leave possible, and its dispatch tasks compute the logits
+  // and the exact top-4
+  const bool bound_room =
+      ctx->s.bounds && ctx->s.bplan && (size_t)T * kExperts <= (size_t)ctx->s.slot_cap;
   a.defer = !defer || logits ? 0
             : router_can_defer(T, a.tile_rows, a.bn) ? 2
             : bound_room && router_can_bound(T, a.tile_rows, a.H) ? 3 : 0;
@@ -555,6 +558,8 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   ctx->routed_T = T;
   ctx->route_pending = true;
   ctx->routed_plan = a.tile_rows;
+  ctx->routed_bounds = a.defer == 3;
+  ctx->routed_tail = a.tail_units;
   return MOE_OK;
 }
 
@@ -600,6 +605,8 @@ int moe_experts(moe_ctx *ctx, const float *x, float *y, const float *residual,
   a.wait_limit = kDefaultWaitLimit / (ctx->wait_div > 0 ? ctx->wait_div : 1);
   if (a.wait_limit < 1) a.wait_limit = 1;
   const int plan = ctx->routed_plan;
+  a.bounds = ctx->routed_bounds ? 1 : 0;
+  a.tail_units = ctx->routed_tail;
   const int pi = plan_index(plan);
   if (pi < 0) return MOE_ERR_INVALID_ARG;
   // the routing (and, for the streaming plan, the rows the router prepared)
@@ -748,6 +755,7 @@ int moe_dense_forward(moe_ctx *ctx, const float *x, float *y, const float *resid
   ctx->routed_T = num_tokens;
   ctx->route_pending = true;
   ctx->routed_plan = a.tile_rows;
+  ctx->routed_bounds = false;
   return moe_experts(ctx, x, y, residual, num_tokens, stream);
 }
 

@@ -49,21 +49,20 @@ constexpr int kChainJobs = kExperts / 4;
 // score bounds leave possible (usually exactly its top-4, sometimes 5 or 6),
 // at most kSpecSlots; a batch with a token past that waits for its logits.
 constexpr int kSpecSlots = 8;
-// MFMA plans: moe_forward of up to this many tokens routes from score bounds
-// (Ctrl::deferred == 3): the router plans a slot for every expert a token's
-// bounds leave possible, and the expert kernel's dispatch tasks compute the
-// logits and each token's exact top-4 while the gate/up tiles run.
+// 32- and 64-row MFMA plans: moe_forward of up to this many tokens routes
+// from score bounds (Ctrl::deferred == 3): every block of the expert kernel
+// plans a slot for every expert a token's bounds leave possible, and its
+// dispatch tasks compute the logits and each token's exact top-4 while the
+// gate/up tiles run.
 constexpr int kBoundTokens = 256;
-// Scratch::smap row: the slot of each (token, expert) pair the bounds leave
-// possible (the other entries are never read), then the mask of those experts
-constexpr int kSmapStride = kExperts + 1;
+constexpr int kPlanCopies = 8;
+constexpr int kPlanCopyInts = kBoundTokens + kBoundTokens / kDeferTokens * kExperts;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset
 // by that router block, so a forward needs no memset (and no host round trip).
 struct Ctrl {
   int router_done;  // router blocks finished (last-block election)
-  int head;         // expert-kernel task queue head
   int assign_done;  // dispatch (slot assignment) tasks finished
   int err;          // sticky: 1 = a bounded wait expired
   int num_tokens;
@@ -91,8 +90,9 @@ struct Ctrl {
   int offsets[kExperts + 1];
   int unit_off[kExperts + 1];  // prefix of units (m-tiles or 1 per active expert)
   int active[kExperts];
-  // 3: the router planned from score bounds (MFMA plans), the expert kernel's
-  // dispatch tasks compute the logits and each token's exact top-4
+  // 3: the router wrote score bounds (MFMA plans); every block of the expert
+  // kernel plans from them, and its dispatch tasks compute the logits and
+  // each token's exact top-4
   // deferred == 2: lower and upper bound of each (token, expert) score
   // sigmoid(logit) + bias, whatever order the logit's FMA chain ran in
   float sbound[2][kDeferTokens][kExperts];
@@ -100,6 +100,10 @@ struct Ctrl {
   // own: atomics on one line serialise, and head takes one per block
   alignas(128) int chain_head;
   int chain_done;
+  // expert-kernel task queue head, on a cache line of its own: every block
+  // claims its first task at once as it starts, and loads of the plan's
+  // fields on the same line waited behind those atomics (~5 us at 512 blocks)
+  alignas(128) int head;
   // followed in memory by int dep[max_units][dep_words(I)]: bit n of a
   // unit's mask is set once its W1W3 (gate/up) tile n has stored its
   // intermediate columns
@@ -135,7 +139,12 @@ struct Scratch {
   // routing from score bounds (Ctrl::deferred == 3), min(Tmax, kBoundTokens)
   // tokens; null where a context has no room for it
   float *bounds;         // [T][2][E]: lower, then upper bound of each score
-  int *smap;             // [T][kSmapStride]: slot of each possible pair, then the possible mask
+  // [kPlanCopies][kPlanCopyInts]: copies of each token's possible-expert mask
+  // ([kBoundTokens]) and each token block's possible pairs per expert
+  // ([kBoundTokens / 8][E]), one per die: every block of the expert kernel
+  // reads them as it starts, and one copy read by all 512 blocks at once
+  // came back ~5 us late
+  uint32_t *bplan;
 };
 
 struct RouterArgs {
@@ -164,6 +173,11 @@ struct ExpertArgs {
   Scratch s;
   int T, H, I;
   int wait_limit;        // bounded-wait iterations before giving up
+  // routing from score bounds (RouterArgs::defer 3, MFMA plans): the blocks
+  // plan from the router's masks and counts, with this many tail units (the
+  // routing's own values, so a block reads no control field before its plan)
+  int bounds;
+  int tail_units;
 };
 
 // Launchers (moe_kernels.hip).  Return hipSuccess or the launch error.

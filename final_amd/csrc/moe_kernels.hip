@@ -203,8 +203,7 @@ __device__ __forceinline__ int lane_scan32(int v, int lane, int *total) {
 
 template <int RT>
 __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
-                            PlanLocal loc = PlanLocal{nullptr, nullptr, nullptr},
-                            const uint32_t *pmask = nullptr) {
+                            PlanLocal loc = PlanLocal{nullptr, nullptr, nullptr}) {
   Ctrl *ctrl = a.s.ctrl;
   const int tid = threadIdx.x;
   const int e = tid & (kExperts - 1);
@@ -308,7 +307,7 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
       ctrl->tile_rows = tr;
       ctrl->head = 0;
       ctrl->assign_done = 0;
-      ctrl->deferred = a.defer == 3 ? 3 : 0;
+      ctrl->deferred = 0;
       ps.units = units;
     }
   }
@@ -343,35 +342,7 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
     // slot = token block base + in-block rank (stable by token), as the
     // dispatch tasks of the tiled plans compute it
     const int n = T * kTopK;
-    if (pmask) {
-      // routing from bounds: a slot for every possible (token, expert) pair
-      // (bit e of the token's mask, LDS), a thread per token; smap takes
-      // the slots of the possible pairs (the others are never read)
-      const int total = ps.off[kExperts];
-      if (RT != kDeferTokens || !bases_lds || T > kBoundTokens) {
-        if (tid == 0)  // routing from bounds is planned for 8-token blocks only
-          __hip_atomic_store(&ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      } else if (tid < T) {
-        const int t = tid, b = t / RT;
-        uint32_t prev[RT];  // masks of the token block's earlier tokens
-#pragma unroll
-        for (int j = 0; j < RT; ++j) prev[j] = b * RT + j < t ? pmask[b * RT + j] : 0u;
-        for (uint32_t m = pmask[t]; m != 0; m &= m - 1) {
-          const int e = __builtin_ctz(m);
-          int rk = 0;
-#pragma unroll
-          for (int j = 0; j < RT; ++j) rk += (int)((prev[j] >> e) & 1u);
-          int slot = ps.base[b][e] + rk;
-          if (slot >= 0 && slot < total && slot < a.s.slot_cap) {
-            a.s.slot_token[slot] = t;
-          } else {  // inconsistent plan: flag it, never write out of range
-            slot = -1;
-            __hip_atomic_store(&ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          }
-          a.s.smap[(size_t)t * kSmapStride + e] = slot;
-        }
-      }
-    } else if (bases_lds && n <= kThreads * kPlanSlotsPerThread) {
+    if (bases_lds && n <= kThreads * kPlanSlotsPerThread) {
       // every thread's (expert, rank) pairs loaded at once, bases from LDS
       int id[kPlanSlotsPerThread], rk[kPlanSlotsPerThread];
 #pragma unroll
@@ -841,68 +812,6 @@ __device__ __forceinline__ void route_token_block(RouteShared &rs, int nt, const
   __syncthreads();
 }
 
-// Planning of a routing from score bounds (MFMA plans, up to kBoundTokens
-// tokens), by the last of the router's blocks, one thread per token:
-//  - the token's 32 lower and 32 upper bounds (one 256-byte row), and lo4,
-//    the 4th-largest lower bound;
-//  - expert e stays possible unless lo4 > hi(e): then four experts beat e
-//    strictly whatever the logits' rounding, and the strict-'>' insertion
-//    of layer.cu:465-476 cannot keep it.  So the set holds the token's
-//    exact top-4: usually exactly those 4, a 5th or 6th on a near-tie at
-//    the 4th place, all 32 where the bounds are infinite (non-finite
-//    inputs).  Its mask goes to LDS and to smap[t][kExperts];
-//  - counts per (token block, expert) of the possible pairs, the counts
-//    routing computes for the top-4 (layer.cu:494-497).
-// Then router_plan plans from those counts (loc) and the masks: a slot for
-// every possible pair, slot = token block base + in-block rank (the block's
-// earlier tokens with the same expert possible), stable by token.
-__host__ __device__ constexpr size_t bounds_plan_lds(int T) {
-  return ((size_t)kBoundTokens + (size_t)((T + kDecRT - 1) / kDecRT) * kExperts) * sizeof(int);
-}
-
-__device__ void bounds_plan(const RouterArgs &a, int T, float *lds, PlanLocal *loc,
-                            const uint32_t **pmask) {
-  static_assert(kBoundTokens <= kThreads, "a thread per token");
-  const int tid = threadIdx.x, nb = (T + kDecRT - 1) / kDecRT;
-  uint32_t *mask = reinterpret_cast<uint32_t *>(lds);               // [kBoundTokens]
-  int *cnt = reinterpret_cast<int *>(mask + kBoundTokens);          // [nb][kExperts]
-  if (tid < T) {
-    const float *b = a.s.bounds + (size_t)tid * 2 * kExperts;
-    f32x4 v[2 * kExperts / 4];
-#pragma unroll
-    for (int j = 0; j < 2 * kExperts / 4; ++j) v[j] = ld4(b + 4 * j);
-    // the four largest lower bounds (an insertion network)
-    float m0 = -__builtin_inff(), m1 = m0, m2 = m0, m3 = m0;
-#pragma unroll
-    for (int j = 0; j < kExperts; ++j) {
-      const float lo = v[j / 4][j % 4];
-      m3 = fmaxf(m3, fminf(m2, lo));
-      m2 = fmaxf(m2, fminf(m1, lo));
-      m1 = fmaxf(m1, fminf(m0, lo));
-      m0 = fmaxf(m0, lo);
-    }
-    uint32_t m = 0;
-#pragma unroll
-    for (int j = 0; j < kExperts; ++j) m |= (uint32_t)!(m3 > v[kExperts / 4 + j / 4][j % 4]) << j;
-    mask[tid] = m;
-    a.s.smap[(size_t)tid * kSmapStride + kExperts] = (int)m;
-  }
-  __syncthreads();
-  for (int i = tid; i < nb * kExperts; i += kThreads) {
-    const int b = i / kExperts, e = i % kExperts;
-    int run = 0;
-#pragma unroll
-    for (int r = 0; r < kDecRT; ++r) {
-      const int t = b * kDecRT + r;
-      if (t < T) run += (int)((mask[t] >> e) & 1u);
-    }
-    cnt[i] = run;
-  }
-  __syncthreads();
-  loc->cnt = cnt;
-  *pmask = mask;
-}
-
 // Expert-split router (T <= 256).  A token block is 8 tokens; its 32 experts are
 // split over 8 blocks of 4, so 8x more CUs share the gate.  Each block copies
 // its 4 gate rows and the token rows whole into LDS with direct-to-LDS loads
@@ -911,9 +820,10 @@ __device__ void bounds_plan(const RouterArgs &a, int T, float *lds, PlanLocal *l
 // finishes it (route_token_block) and the last token block plans.  With
 // defer 2 (one token block, weight-streaming plan) the blocks write score
 // bounds in place of the chains and the expert kernel routes and plans in
-// its own blocks; with defer 3 (MFMA plans) they write the bounds and the
-// last block of all plans from them (bounds_plan), and the expert kernel's
-// dispatch tasks compute the logits and route.
+// its own blocks; with defer 3 (MFMA plans of up to kBoundTokens tokens)
+// they write the bounds, and every block of the expert kernel plans from
+// them (bounds_local_plan) and its dispatch tasks compute the logits and
+// route.
 __host__ __device__ constexpr size_t router_decode_lds(int H) {
   return (size_t)(kDecEPB + kDecRT) * (size_t)(H + 4) * sizeof(float);
 }
@@ -936,6 +846,24 @@ void router_decode_kernel(RouterArgs a) {
   float *gs = lds, *xs = lds + kDecEPB * P;
   // the score bias, read now so the finishing block finds it in LDS
   if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
+  if (a.defer == 3) {
+    // the expert kernel's blocks plan the launch from the bounds: its queue
+    // and dispatch counter start at 0, the gate/up tiles' masks at 0
+    if (blockIdx.x == 0 && tid == 0) {
+      Ctrl *ctrl = a.s.ctrl;
+      ctrl->head = 0;
+      ctrl->assign_done = 0;
+      ctrl->deferred = 3;
+      ctrl->num_tokens = T;
+      ctrl->tile_rows = a.tile_rows;
+      ctrl->n_rblocks = (T + kDecRT - 1) / kDecRT;
+      ctrl->rtokens = kDecRT;
+      ctrl->slots_assigned = 1;
+      ctrl->router_done = 0;
+    }
+    const int ndep = dep_words(a.inter) * a.max_units;
+    for (int i = blockIdx.x * kThreads + tid; i < ndep; i += gridDim.x * kThreads) a.s.dep[i] = 0;
+  }
   if (a.defer == 2 && blockIdx.x == 0 && tid == 0) {
     // the streaming kernel routes and plans: its queues start at 0
     Ctrl *ctrl = a.s.ctrl;
@@ -1032,7 +960,7 @@ void router_decode_kernel(RouterArgs a) {
         if (a.defer == 2) {
           a.s.ctrl->sbound[0][tl][e0 + el] = lo;
           a.s.ctrl->sbound[1][tl][e0 + el] = hi;
-        } else {  // read by the planning block (bounds_plan)
+        } else {  // read by the token block's finishing block
           float *b = a.s.bounds + (size_t)(t0 + tl) * 2 * kExperts + e0 + el;
           st_agent(b, lo);
           st_agent(b + kExperts, hi);
@@ -1040,6 +968,59 @@ void router_decode_kernel(RouterArgs a) {
       }
     }
     if (a.defer == 2) return;
+    // 3'. the last of the token block's 8 blocks turns its tokens' bounds
+    // into their possible sets: expert e stays possible unless four experts'
+    // lower bounds exceed e's upper bound (then four experts beat e strictly
+    // whatever the logits' rounding, and the strict-'>' insertion of
+    // layer.cu:465-476 cannot keep it), so a set holds the token's exact
+    // top-4, usually just those, a 5th or 6th on a near-tie at the 4th
+    // place, all 32 where the bounds are infinite (non-finite inputs).  It
+    // writes each token's mask and the block's count per expert (a copy per
+    // die); every block of the expert kernel plans from them
+    // (bounds_local_plan).
+    __builtin_amdgcn_s_waitcnt(0);  // this block's bounds are stored
+    __syncthreads();
+    if (tid == 0) {
+      s_flag = fetch_add(&a.s.tb_done[tb], 1) == kDecES - 1;
+      if (s_flag) {
+        a.s.tb_done[tb] = 0;  // all blocks counted in: reset
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      }
+    }
+    __syncthreads();
+    if (!s_flag) return;
+    {
+      const int tl = tid >> 5, e = tid & (kExperts - 1);
+      const bool tv = tl < nt;
+      const float *b = a.s.bounds + (size_t)(t0 + min(tl, nt - 1)) * 2 * kExperts + e;
+      const float hi = b[kExperts];
+      rs.prob[tl][e] = b[0];
+      __syncthreads();
+      int beat = 0;
+#pragma unroll
+      for (int j0 = 0; j0 < kExperts; j0 += 8) {
+        float lv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) lv[j] = rs.prob[tl][j0 + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) beat += (int)(lv[j] > hi);
+      }
+      const bool poss = tv && beat < kTopK;
+      const uint32_t m = (uint32_t)(__ballot(poss) >> (32 * ((tid & 63) >> 5)));
+      rs.sel[tl][e] = poss ? 1 : 0;
+      // one copy per die (kPlanCopies): lane e < 8 of each token's row
+      if (tv && e < kPlanCopies) a.s.bplan[(size_t)e * kPlanCopyInts + t0 + tl] = m;
+      __syncthreads();
+      {
+        int cnt = 0;
+#pragma unroll
+        for (int t2 = 0; t2 < kDecRT; ++t2) cnt += rs.sel[t2][e];
+        // thread (copy tl, expert e)
+        static_assert(kPlanCopies == kDecRT, "a copy per token row of the block");
+        a.s.bplan[(size_t)tl * kPlanCopyInts + kBoundTokens + tb * kExperts + e] = (uint32_t)cnt;
+      }
+    }
+    return;
   } else if (wave == 0) {
     // 2. chains: wave 0, lane = (token l / 4, expert l % 4)
     const int tl = lane >> 2, el = lane & 3;
@@ -1052,21 +1033,9 @@ void router_decode_kernel(RouterArgs a) {
     fill_unwritten(a, blockIdx.x, gridDim.x, tid - 64, kThreads - 64);
   }
   const int nb = gridDim.x / kDecES;
-  // the plan's input from LDS (one token block, or a routing from bounds)
+  // the plan's input from LDS (one token block)
   PlanLocal loc{nullptr, nullptr, nullptr};
-  const uint32_t *pmask = nullptr;
-  if (a.defer == 3) {
-    // 3'. the last of all the router's blocks plans from the bounds
-    __builtin_amdgcn_s_waitcnt(0);  // this block's bounds are stored
-    __syncthreads();
-    if (tid == 0) {
-      s_flag = fetch_add(&a.s.ctrl->router_done, 1) == (int)gridDim.x - 1;
-      if (s_flag) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
-    __syncthreads();
-    if (!s_flag) return;
-    bounds_plan(a, T, lds, &loc, &pmask);
-  } else {
+  {
     // 3. the last of the token block's 8 blocks finishes it
     __builtin_amdgcn_s_waitcnt(0);  // this block's logits are stored
     __syncthreads();
@@ -1114,7 +1083,7 @@ void router_decode_kernel(RouterArgs a) {
       if (!s_flag) return;
     }
   }
-  router_plan<kDecRT>(a, nb, T, ps, loc, pmask);
+  router_plan<kDecRT>(a, nb, T, ps, loc);
 }
 
 // Dense SwiGLU FFN (MLP::forward_gpu, layer.cu:1231-1269) as the block with
@@ -1165,7 +1134,7 @@ __global__ __launch_bounds__(kThreads) void router_dense_kernel(RouterArgs a) {
 // Dispatch task q: slots of the 64 tokens of router block q (replaces
 // moe_scatter_kernel layer.cu:501-542: slot = block base + in-block rank, so
 // slots are stable by token; x itself is not copied, the GEMM gathers rows).
-__device__ void assign_task(const ExpertArgs &a, int q, int rt, bool slots_ready) {
+__device__ __forceinline__ void assign_task(const ExpertArgs &a, int q, int rt, bool slots_ready) {
   const int tl = threadIdx.x >> 2, k = threadIdx.x & 3;
   const int tok = q * rt + tl;
   if (tl < rt && tok < a.T) {
@@ -1225,14 +1194,15 @@ __device__ __forceinline__ int slot_tok(const ExpertArgs &a, int slot) {
 // The tile's stores have completed before it counts (agent-scope stores), and
 // the completing block acquires before it reads the other tiles' outputs.
 // y may alias the residual: a thread reads its columns before it writes them.
-// bounds: the plan has a slot for every expert a token's score bounds leave
-// possible (Ctrl::deferred == 3, the token's mask in smap), so its outputs
-// are complete once all of its slots have landed; the sum takes its exact
-// top-4 (pos, wts), which the dispatch tasks published before any down tile
-// started.
+// row_tok / mask (routing from score bounds, Ctrl::deferred == 3): the tile
+// rows' tokens and each token's mask of possible experts, in LDS; the plan
+// has a slot for every possible expert, so a token's outputs are complete
+// once all of its slots have landed, and the sum takes its exact top-4 (pos,
+// wts), which the dispatch tasks published before any down tile started.
 template <int BN>
-__device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int col0, int *s_list,
-                             int *s_n, bool bounds) {
+__device__ __forceinline__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int col0,
+                                             int *s_list, int *s_n, const int *row_tok = nullptr,
+                                             const uint32_t *mask = nullptr) {
 #pragma clang fp contract(off)
   constexpr int NJ = BN / kCombineCols;  // counters the tile's columns cover
   const int tid = threadIdx.x;
@@ -1241,10 +1211,10 @@ __device__ void tile_combine(const ExpertArgs &a, int slot0, int rows, int col0,
   if (tid == 0) *s_n = 0;
   __syncthreads();
   if (tid < rows) {
-    const int t = slot_tok(a, slot0 + tid);
+    const int t = row_tok ? row_tok[tid] : slot_tok(a, slot0 + tid);
     int nvalid = 0;
-    if (bounds) {
-      nvalid = __popc((uint32_t)a.s.smap[(size_t)t * kSmapStride + kExperts]);
+    if (mask) {
+      nvalid = __popc(mask[t]);
     } else {
 #pragma unroll
       for (int k = 0; k < kTopK; ++k) nvalid += a.s.pos[(size_t)t * kTopK + k] >= 0;
@@ -1377,16 +1347,121 @@ __device__ void block_chains(const float *x, const float *gate, int t0, int nt, 
   }
 }
 
+// Routing from score bounds under the MFMA plans (Ctrl::deferred == 3, up to
+// kBoundTokens tokens, 32- and 64-row tiles): every block of the expert
+// kernel plans the launch itself, in LDS, from the router's bounds.
+struct BoundPlan {
+  uint32_t mask[kBoundTokens];                    // possible experts of each token
+  int base[kBoundTokens / kDecRT][kExperts];      // slot of token block b's first pair of expert e
+  int tok[64];                                    // the current down tile's row tokens
+  int wcnt[kThreads / 64];                        // per-wave counts (unit_tokens)
+  int plan[8];                                    // nb, n1, n2, ntot, p1u, p2u, gtail, tail
+};
+
+// The plan of a routing from bounds, by every block (all threads), from the
+// router's possible sets (each token's mask, each token block's count per
+// expert: router_decode_kernel, defer 3):
+//  - the exclusive prefix of the counts over token blocks, the counts,
+//    offsets and units per expert, and the task plan router_plan writes for
+//    the MFMA plans (its arithmetic, for BM-row tiles);
+//  - base[b][e] = offsets[e] + expert e's pairs in token blocks before b, so
+//    pair (t, e)'s slot is base[t / 8][e] + the block's earlier tokens with
+//    e possible: the slots routing computes for the top-4 (layer.cu:494-542,
+//    stable by token), over the possible pairs.
+// Block 0 also publishes the counts (moe_last_plan_counts).
+template <int BM>
+__device__ __forceinline__ void bounds_local_plan(const ExpertArgs &a, Ctrl *c, BoundPlan &bp,
+                                                  int *s_counts, int *s_offsets, int *s_unit_off) {
+  constexpr int NBMAX = kBoundTokens / kDecRT;
+  static_assert(kBoundTokens <= 4 * 64 && kThreads >= 128 + 64, "masks in wave 0, counts in wave 1");
+  const int tid = threadIdx.x;
+  const int T = a.T, nb = (T + kDecRT - 1) / kDecRT;
+  // this die's copy of the router's masks and counts (blocks are dealt to
+  // the dies in turn); wave 0 loads the masks (4 tokens a thread), wave 1
+  // the counts (lane e: expert e's), each wave's loads in flight at once;
+  // wave 3 has claimed the block's first task, whose return would hold up a
+  // wave's later loads
+  const uint32_t *cp = a.s.bplan + (size_t)(blockIdx.x % kPlanCopies) * kPlanCopyInts;
+  if (4 * tid < T) {
+    const int t0 = 4 * tid;
+    if (t0 + 4 <= T) {
+      const uint4 m4 = *reinterpret_cast<const uint4 *>(cp + t0);
+      bp.mask[t0] = m4.x;
+      bp.mask[t0 + 1] = m4.y;
+      bp.mask[t0 + 2] = m4.z;
+      bp.mask[t0 + 3] = m4.w;
+    } else {
+      for (int t = t0; t < T; ++t) bp.mask[t] = cp[t];
+    }
+  }
+  const int e = tid - 64;
+  if (e >= 0 && e < kExperts) {
+    int v[NBMAX];
+#pragma unroll
+    for (int b = 0; b < NBMAX; ++b) v[b] = b < nb ? (int)cp[kBoundTokens + b * kExperts + e] : 0;
+    int run = 0;
+#pragma unroll
+    for (int b = 0; b < NBMAX; ++b) {
+      if (b < nb) bp.base[b][e] = run;
+      run += v[b];
+    }
+    const int cnt = run;
+    int total = 0, utotal = 0;
+    const int off = lane_scan32(cnt, e, &total);
+    const int uoff = lane_scan32((cnt + BM - 1) / BM, e, &utotal);
+    s_counts[e] = cnt;
+    s_offsets[e] = off;
+    s_unit_off[e] = uoff;
+    if (blockIdx.x == 0) c->counts[e] = cnt;
+    if (e == 0) {
+      s_offsets[kExperts] = total;
+      s_unit_off[kExperts] = utotal;
+      const int units = utotal;
+      const int p1u = a.I / (Tile<BM>::BN / 2), p2u = a.H / Tile<BM>::BN;
+      const int tail = min(units, a.tail_units);
+      const int gtail = BM == 64 && T <= kGateUpTailTokens ? min(units, kGateUpTailUnits) : 0;
+      const int n1 = (units + gtail) * p1u, n2 = (units - tail + 2 * tail) * p2u;
+      bp.plan[0] = nb;
+      bp.plan[1] = n1;
+      bp.plan[2] = n2;
+      bp.plan[3] = nb + n1 + n2;
+      bp.plan[4] = p1u;
+      bp.plan[5] = p2u;
+      bp.plan[6] = gtail;
+      bp.plan[7] = tail;
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < nb * kExperts; i += kThreads) bp.base[i / kExperts][i % kExperts] += s_offsets[i % kExperts];
+  __syncthreads();
+}
+
+// The tokens of rows m0 .. m0 + rows - 1 of expert e's slots (its possible
+// tokens in token order): out[r] = f(token of row r).  All threads; ends
+// before the caller's barrier that publishes out.
+template <typename F>
+__device__ __forceinline__ void unit_tokens(BoundPlan &bp, int T, int e, int m0, int rows, F f) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool has = tid < T && ((bp.mask[tid] >> e) & 1u);
+  const unsigned long long b = __ballot(has);
+  if (lane == 0) bp.wcnt[wave] = __popcll(b);
+  __syncthreads();
+  int r = __popcll(b & ((1ull << lane) - 1ull));
+  for (int w = 0; w < wave; ++w) r += bp.wcnt[w];
+  if (has && r >= m0 && r < m0 + rows) f(r - m0, tid);
+}
+
 // Routing job q of a routing from score bounds (Ctrl::deferred == 3), run by
 // the dispatch task of token block q * TB: the logits of token blocks q * TB
 // .. q * TB + TB - 1 (block_chains), each block's exact routing
 // (route_token_block: the reference's sigmoid, strict-'>' top-4 and
 // weights), and for each (token, rank) the slot the plan gave that expert
 // (the possible set holds the exact top-4: a miss, which the token's mask
-// shows, is an inconsistent plan, flagged).  Down tiles, whose combines read
-// idx / wts / pos, start only after every dispatch task has signalled.
+// shows, is an inconsistent plan, flagged); bp: the block's plan.  Down
+// tiles, whose combines read idx / wts / pos, start only after every
+// dispatch task has signalled.
 template <int KC, int NR, int TB>
-__device__ void route_task(const ExpertArgs &a, int q, float *lds) {
+__device__ __forceinline__ void route_task(const ExpertArgs &a, int q, float *lds, const BoundPlan &bp) {
   const int tid = threadIdx.x, tl = tid >> 5, e = tid & (kExperts - 1);
   const int t0 = q * TB * kDecRT, nt = min(TB * kDecRT, a.T - t0);
   float l[TB];
@@ -1408,8 +1483,12 @@ __device__ void route_task(const ExpertArgs &a, int q, float *lds) {
       const int ee = rs.ti[tt][k];
       int slot = -1;
       if (ee >= 0 && ee < kExperts) {
-        const uint32_t m = (uint32_t)a.s.smap[(size_t)t * kSmapStride + kExperts];
-        slot = (m >> ee) & 1u ? a.s.smap[(size_t)t * kSmapStride + ee] : -1;
+        // the plan's slot: token block base + the block's earlier tokens
+        // with ee possible
+        if ((bp.mask[t] >> ee) & 1u) {
+          slot = bp.base[t / kDecRT][ee];
+          for (int t2 = t - t % kDecRT; t2 < t; ++t2) slot += (int)((bp.mask[t2] >> ee) & 1u);
+        }
         if (slot < 0 || slot >= a.s.slot_cap) {
           slot = -1;
           __hip_atomic_store(&a.s.ctrl->err, 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1486,20 +1565,48 @@ void expert_mfma_kernel(ExpertArgs a) {
   __shared__ int s_aoff[BM];
   __shared__ int s_comb[BM * (Tile<BM>::BN / kCombineCols)];
   __shared__ int s_ncomb;
+  // routing from score bounds (Ctrl::deferred == 3): 32- and 64-row plans
+  // of up to kBoundTokens tokens, planned by every block (bounds_local_plan)
+  constexpr bool kBounds = BM <= 64;
+  struct NoPlan {};
+  __shared__ typename std::conditional<kBounds, BoundPlan, NoPlan>::type s_bp;
   Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
-  if (tid <= kExperts) {
-    s_unit_off[tid] = c->unit_off[tid];
-    s_offsets[tid] = c->offsets[tid];
+  const bool bounds = kBounds && a.bounds != 0;
+  // the last wave claims: the plan's loads are in the other waves
+  if (tid == kThreads - 1) s_task = claim(&c->head);
+  int pv[8];  // nb, n1, n2, ntot, p1u, p2u, gtail, tail
+  const int *row_tok = nullptr;
+  const uint32_t *pmask = nullptr;
+  if constexpr (kBounds) {
+    if (bounds) {
+      bounds_local_plan<BM>(a, c, s_bp, s_counts, s_offsets, s_unit_off);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) pv[i] = s_bp.plan[i];
+      row_tok = s_bp.tok;
+      pmask = s_bp.mask;
+    }
   }
-  if (tid < kExperts) s_counts[tid] = c->counts[tid];
-  const int nb = c->n_rblocks, n1 = c->n_p1, n2 = c->n_p2, ntot = c->n_total;
-  const int p1u = c->p1_per_unit, p2u = c->p2_per_unit;
-  const int gtail = BM >= 64 ? c->gu_tail : 0;
-  const int nunits = n1 / p1u - gtail, tail = c->tail_units;
+  if (!bounds) {
+    if (tid <= kExperts) {
+      s_unit_off[tid] = c->unit_off[tid];
+      s_offsets[tid] = c->offsets[tid];
+    }
+    if (tid < kExperts) s_counts[tid] = c->counts[tid];
+    pv[0] = c->n_rblocks;
+    pv[1] = c->n_p1;
+    pv[2] = c->n_p2;
+    pv[3] = c->n_total;
+    pv[4] = c->p1_per_unit;
+    pv[5] = c->p2_per_unit;
+    pv[6] = BM >= 64 ? c->gu_tail : 0;
+    pv[7] = c->tail_units;
+  }
+  const int nb = pv[0], n1 = pv[1], n2 = pv[2], ntot = pv[3], p1u = pv[4], p2u = pv[5];
+  const int gtail = pv[6];
+  const int nunits = n1 / p1u - gtail, tail = pv[7];
   const int H = a.H, I = a.I;
   const AgentOut inter_out(a.s.inter, a.s.inter_bytes), sout_out(a.s.sout, a.s.sout_bytes);
-  if (tid == 0) s_task = claim(&c->head);
   __syncthreads();
   if (BM <= 64 && tid < kExperts) {  // the unit order, from the counts (lanes 0-31 of wave 0)
     const int cnt = s_counts[tid];
@@ -1527,8 +1634,8 @@ void expert_mfma_kernel(ExpertArgs a) {
   // slots written by the router: gate/up tiles need not wait for the dispatch
   // tasks, which then only clear the combine counters (down tiles wait for
   // them) and write the rows of tokens without an expert
-  const bool slots_ready = c->slots_assigned != 0;
-  const bool bounds = c->deferred == 3;
+  // (routing from bounds: the blocks' own plan, no control field to read)
+  const bool slots_ready = bounds || c->slots_assigned != 0;
   // routing jobs (routing from bounds): one token block each, 128-wide k
   // chunks where the tiles' LDS holds two of them (else 64), six chunks of
   // loads in flight
@@ -1542,11 +1649,12 @@ void expert_mfma_kernel(ExpertArgs a) {
   // runs all of its dispatch tasks before its first tile (a loop of their
   // own: the tiles' registers are allocated apart from the routing's).
   while (task < nb && task < ntot) {
-    const int rt = c->rtokens;
-    if (!bounds)
+    const int rt = bounds ? kDecRT : c->rtokens;
+    if (!bounds) {
       assign_task(a, task, rt, slots_ready);
-    else if (task % kBcTB == 0)
-      route_task<kBcKC, kBcNR, kBcTB>(a, task / kBcTB, lds);
+    } else if (task % kBcTB == 0) {
+      if constexpr (kBounds) route_task<kBcKC, kBcNR, kBcTB>(a, task / kBcTB, lds, s_bp);
+    }
     // this router block's tokens start with no expert outputs counted
     const int ncc = H / kCombineCols;
     for (int i = tid; i < rt * ncc; i += kThreads) {
@@ -1573,7 +1681,14 @@ void expert_mfma_kernel(ExpertArgs a) {
       unit_rows<BM>(u, uo, e, m0, rows);
       const int slot0 = s_offsets[e] + m0;
       if (!slots_ready) block_wait(&c->assign_done, nb, a.wait_limit, &c->err);
-      if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
+      if (!bounds) {
+        if (tid < BM) s_aoff[tid] = tid < rows ? slot_tok(a, slot0 + tid) * H : -1;
+      } else {
+        if constexpr (kBounds) {
+          if (tid >= rows && tid < BM) s_aoff[tid] = -1;
+          unit_tokens(s_bp, a.T, e, m0, rows, [&](int r, int t) { s_aoff[r] = t * H; });
+        }
+      }
       __syncthreads();
       const float *brow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TL::BN) * H;
       const uint32_t xbytes = (uint32_t)((size_t)a.T * H * sizeof(float));
@@ -1626,6 +1741,9 @@ void expert_mfma_kernel(ExpertArgs a) {
       const int slot0 = s_offsets[e] + m0;
       block_wait(&c->assign_done, nb, a.wait_limit, &c->err);  // combine counters cleared
       if (tid < BM) s_aoff[tid] = tid < rows ? tid * I : -1;
+      if constexpr (kBounds) {  // the rows' tokens, for the combine
+        if (bounds) unit_tokens(s_bp, a.T, e, m0, rows, [&](int r, int t) { s_bp.tok[r] = t; });
+      }
       __syncthreads();
       // 32- and 64-row plans above 128 tokens: each slab of the tile waits
       // for the gate/up tile that wrote its intermediate columns (half-width
@@ -1677,7 +1795,7 @@ void expert_mfma_kernel(ExpertArgs a) {
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TH::BN) * I;
         next = mfma_tile<TH, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
                                     H, ht * TH::BN, &c->head, ready);
-        tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb, bounds);
+        tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb, row_tok, pmask);
       } else {
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
         if (BM == 128 && rows <= 64)
@@ -1686,7 +1804,7 @@ void expert_mfma_kernel(ExpertArgs a) {
         else
           next = mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
                                       H, ht * TL::BN, &c->head, ready);
-        tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb, bounds);
+        tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb, row_tok, pmask);
       }
     }
     __syncthreads();
@@ -2930,8 +3048,7 @@ hipError_t launch_rmsnorm(const float *h, const float *w, float *out, int T, int
 hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) {
   const bool small = a.T <= 64;
   if (a.T <= kSplitRouterTokens && !from_logits) {
-    size_t lds = router_decode_lds(a.H);
-    if (a.defer == 3 && bounds_plan_lds(a.T) > lds) lds = bounds_plan_lds(a.T);
+    const size_t lds = router_decode_lds(a.H);
     if (lds > 65536) {
       const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&router_decode_kernel),
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
@@ -3038,7 +3155,7 @@ int stream_rows_dense(int T) {
 }
 
 bool router_can_bound(int T, int tile_rows, int H) {
-  return T >= 1 && T <= kBoundTokens && tile_rows > 0 && H % 256 == 0;
+  return T >= 1 && T <= kBoundTokens && (tile_rows == 32 || tile_rows == 64) && H % 256 == 0;
 }
 
 bool router_can_defer(int T, int tile_rows, int bn) {

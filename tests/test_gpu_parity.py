@@ -534,11 +534,10 @@ def test_forward_routing_ties_many_blocks(T, plan, block, real_weights, oracle_m
     a and b share the 4th place for as many tokens as possible.  Each tied
     token keeps the lower index (the strict '>' insertion of
     layer.cu:465-476), under the 64-row plan of the decode router's several
-    token blocks and under forced MFMA plans at small T (one token block
-    for T=5: the finishing block plans from its own LDS).  No score bound
-    separates an exact tie, so moe_forward's routing from bounds plans a
-    slot for both experts of each tied token, and the dispatch tasks' exact
-    routing keeps one."""
+    token blocks and under forced MFMA plans at small T (the 128-row plan
+    keeps the full router).  No score bound separates an exact tie, so
+    moe_forward's routing from bounds plans a slot for both experts of each
+    tied token, and the dispatch tasks' exact routing keeps one."""
     from final_amd import workloads as W
     rng = np.random.default_rng(800 + T)
     x = rng.standard_normal((T, W.H)).astype(np.float32)
@@ -573,8 +572,10 @@ def test_forward_routing_ties_many_blocks(T, plan, block, real_weights, oracle_m
         block.force_tile_rows(-1)
         rw = real_weights
         block.set_weights(rw["gate"], rw["bias"], rw["w1"], rw["w3"], rw["w2"])
-    # no bound separates an exact tie: each tied token has both experts planned
-    assert int(rt1["plan_counts"].sum()) >= int(rt1["counts"].sum()) + len(tied)
+    # no bound separates an exact tie: under the 32- and 64-row plans, which
+    # route from score bounds, each tied token has both experts planned
+    if (plan if plan > 0 else block.plan(T)) in (32, 64):
+        assert int(rt1["plan_counts"].sum()) >= int(rt1["counts"].sum()) + len(tied)
     _check_same(y1, rt1, y2, rt2, tiled=True)
     for t in tied:
         assert min(a, b) in rt1["idx"][t].tolist() and max(a, b) not in rt1["idx"][t].tolist()
