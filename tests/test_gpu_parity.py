@@ -146,13 +146,13 @@ def test_streaming_four_experts(block, real_weights, oracle_mod):
 @pytest.mark.gpu
 @pytest.mark.parametrize("T", [32, 40, 48, 57, 64])
 def test_streaming_wide_tasks(T, block, real_weights, oracle_mod):
-    """32-64 tokens under the weight-streaming plan (the automatic plan up to
-    48 tokens, forced above): 64-row tasks, streamed as four 16-row groups
-    that reuse one load of the token rows when every expert holds at most 16
-    tokens, else as four row groups at once over two token passes (one expert
-    made hot by a bias so it holds all T tokens)."""
+    """32-64 tokens under the weight-streaming plan (forced: the automatic
+    plan takes 64-row MFMA tiles from 21 tokens): 64-row tasks, streamed as
+    four 16-row groups that reuse one load of the token rows when every
+    expert holds at most 16 tokens, else as four row groups at once over two
+    token passes (one expert made hot by a bias so it holds all T tokens)."""
     from final_amd import workloads as W
-    assert block.plan(T) == (0 if T <= 48 else 64)
+    assert block.plan(T) == 64
     block.force_tile_rows(0)
     try:
         x = W.gen_x(T, seed=40 + T)
@@ -501,7 +501,7 @@ def _ref_scores(O, w, x):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("T", [49, 64, 100, 129, 200, 256])
+@pytest.mark.parametrize("T", [21, 33, 48, 64, 100, 129, 200, 256])
 def test_forward_random_batches_mfma(T, block, real_weights, oracle_mod):
     """Random N(0, 1) batches under the 64-row MFMA plan.  moe_forward's
     router writes score bounds and plans a slot for every expert they leave
