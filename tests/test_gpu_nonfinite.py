@@ -9,6 +9,12 @@ selectable expert gets the empty combine sum: y = residual + 0.0f.
 
 Both routers are covered: the expert-split decode router (T <= 256, top-4 as a
 rank count) and the 64-token router (T > 256, and every moe_route_logits call).
+moe_forward of 21-256 tokens under the 32/64-row plans routes from score
+bounds: a row with a non-finite input or bias has infinite bounds, so every
+expert stays possible for it and gets a slot (up to 32 per token), and the
+expert kernel's exact routing picks from the logits (T=64, 200 and the forced
+plans below; all 32 for every token in test_forward_no_expert_selected at
+T=8 under the 64-row plan).
 Routing (idx, w, counts) is compared bit for bit; y within rtol 1e-3 /
 atol 1e-4 with NaN positions equal (rows of tokens whose inputs hold +-inf are
 NaN in both).
