@@ -212,15 +212,18 @@ static int ctx_plan(const moe_ctx *ctx, int T) {
 // MFMA plans: the last units' down tiles run as two half-width tiles, so the
 // last round of tiles is about half as long.  128-row plan: about one
 // block's worth of half tiles (T=4096: 3.01 -> 2.95 ms).  64-row plan: half
-// that many units (its units are few; with every expert in one unit, the
-// longest-first order puts the smallest experts last): T=256 expert launch
-// 329 -> 311 us; one block's worth, 16 units at T=256, took as much there
-// and lost 2 % at T=128.
-static int tail_units(const moe_ctx *ctx, int tile_rows, int bn) {
+// that many units above 64 tokens (its units are few; with every expert in
+// one unit, the longest-first order puts the smallest experts last): T=256
+// expert launch 329 -> 311 us; one block's worth, 16 units at T=256, took as
+// much there and lost 2 % at T=128.  Up to 64 tokens, where every unit is
+// one small expert, one block's worth (16 units): T=21 256.0 -> 251.6 us,
+// T=32 262.5 -> 258.2, T=48 269.9 -> 266.7, T=64 268.5 -> 267.1; equal at
+// 80-96.
+static int tail_units(const moe_ctx *ctx, int tile_rows, int bn, int T) {
   const int pi = plan_index(tile_rows);
   if ((tile_rows != 128 && tile_rows != 64) || pi < 0) return 0;
   const int half_tiles_per_unit = 2 * (ctx->d.hidden / bn);
-  const int k = ctx->grid[pi] / half_tiles_per_unit / (tile_rows == 64 ? 2 : 1);
+  const int k = ctx->grid[pi] / half_tiles_per_unit / (tile_rows == 64 && T > 64 ? 2 : 1);
   return k > 0 ? k : 1;
 }
 
@@ -545,7 +548,7 @@ static int do_route(moe_ctx *ctx, const float *x, const float *logits, int T,
   a.inter = ctx->d.inter;
   a.tile_rows = ctx_plan(ctx, T);
   a.bn = expert_bn(a.tile_rows, T);
-  a.tail_units = tail_units(ctx, a.tile_rows, a.bn);
+  a.tail_units = tail_units(ctx, a.tile_rows, a.bn, T);
   a.max_units = ctx->max_units;
   // deferred decode routing: the router writes score bounds, the streaming
   // kernel computes the logits and routes
@@ -672,7 +675,7 @@ int moe_forward_noalloc(moe_ctx *ctx, const float *x, float *y, const float *res
   ra.inter = ctx->d.inter;
   ra.tile_rows = ctx_plan(ctx, T);
   ra.bn = expert_bn(ra.tile_rows, T);
-  ra.tail_units = tail_units(ctx, ra.tile_rows, ra.bn);
+  ra.tail_units = tail_units(ctx, ra.tile_rows, ra.bn, T);
   ra.max_units = max_units;
   const int pi = plan_index(ra.tile_rows);
   if (pi < 0) return MOE_ERR_INVALID_ARG;
@@ -757,7 +760,7 @@ int moe_dense_forward(moe_ctx *ctx, const float *x, float *y, const float *resid
   a.inter = ctx->d.inter;
   a.tile_rows = ctx_plan(ctx, num_tokens);
   a.bn = a.tile_rows == 0 ? stream_rows_dense(num_tokens) : expert_bn(a.tile_rows, num_tokens);
-  a.tail_units = tail_units(ctx, a.tile_rows, a.bn);
+  a.tail_units = tail_units(ctx, a.tile_rows, a.bn, num_tokens);
   a.max_units = ctx->max_units;
   if (launch_router_dense(a, static_cast<hipStream_t>(stream)) != hipSuccess) return MOE_ERR_HIP;
   ctx->routed_T = num_tokens;
