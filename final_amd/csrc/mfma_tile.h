@@ -195,16 +195,25 @@ constexpr bool tile_skinnyable() {
   return (TL::BM == 64 || TL::BM == 128) && TL::WAVES_M * TL::WAVES_N == 4 && TL::BN % 64 == 0;
 }
 
+// The block's next task, claimed by thread 0 at the end of a tile's MFMAs:
+// from a queue head (null: none, 0 returned) or by a callable.
+__device__ __forceinline__ int claim_next(int *head) { return head ? claim(head) : 0; }
+__device__ __forceinline__ int claim_next(decltype(nullptr)) { return 0; }
+template <typename F>
+__device__ __forceinline__ int claim_next(F &next_task) {
+  return next_task();
+}
+
 // Slab loop of one tile: global loads NS slabs ahead in registers, LDS
 // double-buffered, one barrier per slab; then the block's next task is
 // claimed (thread 0; returned) and the products are written to the LDS
 // epilogue tile Cs [BM][CPITCH] in B-row order.
-template <typename TL, TileLayout LAYOUT, typename Ready>
+template <typename TL, TileLayout LAYOUT, typename Ready, typename Claim>
 __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL::A_PER],
                                           __amdgpu_buffer_rsrc_t abase_r,
                                           __amdgpu_buffer_rsrc_t bsrc_r,
                                           __amdgpu_buffer_rsrc_t none_r, uint32_t bsrc, int lds_st,
-                                          int lrow, int K, int rows_valid, int *head, Ready &ready) {
+                                          int lrow, int K, int rows_valid, Claim &head, Ready &ready) {
   constexpr int BM = TL::BM, BN = TL::BN;
   constexpr int WM = TL::WM, WN = TL::WN, BK = TL::BK, PITCH = TL::PITCH;
   constexpr int A_PER = TL::A_PER, B_PER = TL::B_PER;
@@ -347,7 +356,7 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
     }
   }
 
-  const int next = threadIdx.x == 0 && head ? claim(head) : 0;
+  const int next = threadIdx.x == 0 ? claim_next(head) : 0;
 
   // Products into the epilogue tile (the slab buffers are free after the
   // last barrier).
@@ -388,16 +397,18 @@ __device__ __forceinline__ int tile_slabs(float *lds, const uint32_t (&a_src)[TL
 //
 // Slab pipeline: global loads of slab s+1 are in flight while the MFMAs of
 // slab s run from LDS; one barrier per slab (double-buffered LDS).
-// Thread 0 claims the block's next task from `head` once the MFMAs are done
-// (returned; other threads return 0): the epilogue hides the claim's round
-// trip, and a block commits to its next task only near the end of this one.
-// head == nullptr: no claim (grids of one tile per block).  `out` stores the
+// Thread 0 claims the block's next task with `head` (a queue head, or a
+// callable that claims) once the MFMAs are done (returned; other threads
+// return 0): the epilogue hides the claim's round trip, and a block commits
+// to its next task only near the end of this one.  head == nullptr: no claim
+// (grids of one tile per block).  `out` stores the
 // epilogue's float4s: out.store(byte offset into [rows][ldo], value).
-template <typename TL, bool GATED, typename Out = AgentOut, typename Ready = NoWait>
+template <typename TL, bool GATED, typename Out = AgentOut, typename Ready = NoWait,
+          typename Claim = int *>
 __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_t abytes,
                                          const int *aoff, int rows_valid,
                                          const float *brow0, int K, const Out &out,
-                                         int row0, int ldo, int col0, int *head,
+                                         int row0, int ldo, int col0, Claim head,
                                          Ready ready = Ready{}) {
   constexpr int BM = TL::BM;
   constexpr int KV = TL::KV, A_PER = TL::A_PER;
@@ -431,28 +442,28 @@ __device__ __forceinline__ int mfma_tile(float *lds, const float *abase, uint32_
   constexpr TileLayout kS5 = kSkL ? kSkinny5 : kWide, kS7 = kSkL ? kSkinny7 : kWide;
   int next;
   if (kSkL && rows_valid > 64 && rows_valid <= 80)
-    next = tile_slabs<TL, kS5, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+    next = tile_slabs<TL, kS5, Ready, Claim>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head, ready);
   else if (kSkL && rows_valid > 96 && rows_valid <= 112)
-    next = tile_slabs<TL, kS7, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+    next = tile_slabs<TL, kS7, Ready, Claim>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head, ready);
   else if (kSk && rows_valid <= 16)
-    next = tile_slabs<TL, kS1, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+    next = tile_slabs<TL, kS1, Ready, Claim>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head, ready);
   else if (kSk && rows_valid > 32 && rows_valid <= 48)
-    next = tile_slabs<TL, kS3, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+    next = tile_slabs<TL, kS3, Ready, Claim>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head, ready);
   else if (kNa && (BM == 64 ? rows_valid <= 32 : rows_valid > 80 && rows_valid <= 96))
-    next = tile_slabs<TL, kNw, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+    next = tile_slabs<TL, kNw, Ready, Claim>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head, ready);
   else if (kSk && rows_valid <= 32)
-    next = tile_slabs<TL, kS2, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+    next = tile_slabs<TL, kS2, Ready, Claim>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                rows_valid, head, ready);
   else if (rows_valid >= BM)
-    next = tile_slabs<TL, kFull, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+    next = tile_slabs<TL, kFull, Ready, Claim>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                  rows_valid, head, ready);
   else
-    next = tile_slabs<TL, kWide, Ready>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
+    next = tile_slabs<TL, kWide, Ready, Claim>(lds, a_src, abase_r, bsrc_r, none_r, bsrc, lds_st, lrow, K,
                                  rows_valid, head, ready);
 
   // Epilogue: the [BM][BN] tile in LDS is stored as whole-row float4s;

@@ -60,8 +60,8 @@ namespace {
 
 constexpr size_t kNoAllocBytes = (size_t)8 << 20;  // 8 MiB per GPU
 constexpr int kNoAllocMaxTokens = 128;
-constexpr size_t kNoAllocHeader = 8192;   // Ctrl + dep[], then tb_done[]
-constexpr size_t kNoAllocTbDone = 4096;   // offset of tb_done in the header
+constexpr size_t kNoAllocHeader = 12288;  // Ctrl + dep[], then tb_done[]
+constexpr size_t kNoAllocTbDone = 8192;   // offset of tb_done in the header
 constexpr int kNoAllocMaxUnits = kNoAllocMaxTokens * kTopK / 32 + kExperts + 1;
 constexpr int kMaxDevices = 64;
 static_assert(sizeof(Ctrl) + 2 * sizeof(int) * kNoAllocMaxUnits <= kNoAllocTbDone,

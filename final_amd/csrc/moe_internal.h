@@ -57,6 +57,11 @@ constexpr int kSpecSlots = 8;
 constexpr int kBoundTokens = 256;
 constexpr int kPlanCopies = 8;
 constexpr int kPlanCopyInts = kBoundTokens + kBoundTokens / kDeferTokens * kExperts;
+// Counters the blocks of a routing from bounds claim their first tasks from
+// (Ctrl::gclaim): one counter serialises 512 claims at ~11 ns each, so the
+// last block of a launch had its first task ~6 us after the first block;
+// over 8 counters every block has its first task within ~1.3 us of starting.
+constexpr int kClaimGroups = 8;
 
 // Device control block.  Filled by the last router block of a forward and
 // consumed by the expert kernel of the same forward.  All counters are reset
@@ -104,6 +109,11 @@ struct Ctrl {
   // claims its first task at once as it starts, and loads of the plan's
   // fields on the same line waited behind those atomics (~5 us at 512 blocks)
   alignas(128) int head;
+  // routing from bounds (deferred == 3): the first round of claims, one
+  // counter per group of blocks (block b: group b % kClaimGroups), each on
+  // a 128-byte line of its own; group g's k-th claim is task
+  // k * kClaimGroups + g (expert_mfma_kernel, first_round_left)
+  alignas(128) int gclaim[kClaimGroups][32];
   // followed in memory by int dep[max_units][dep_words(I)]: bit n of a
   // unit's mask is set once its W1W3 (gate/up) tile n has stored its
   // intermediate columns

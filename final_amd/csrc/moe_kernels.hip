@@ -861,6 +861,7 @@ void router_decode_kernel(RouterArgs a) {
       ctrl->slots_assigned = 1;
       ctrl->router_done = 0;
     }
+    if (blockIdx.x == 0 && tid < kClaimGroups) a.s.ctrl->gclaim[tid][0] = 0;
     const int ndep = dep_words(a.inter) * a.max_units;
     for (int i = blockIdx.x * kThreads + tid; i < ndep; i += gridDim.x * kThreads) a.s.dep[i] = 0;
   }
@@ -1550,6 +1551,26 @@ __device__ __forceinline__ void unit_rows(int v, const UnitOrder &o, int &e, int
   }
 }
 
+// The first round of claims of a routing from bounds: tasks [0, f), group
+// g's k-th claim (Ctrl::gclaim) task k * kClaimGroups + g.  Thread 0, before
+// the block's first claim from the queue head: a first-round task that no
+// block has claimed yet, claimed now, or -1 once all of them are claimed
+// (the counters only grow, so a count at its quota is final).
+__device__ __forceinline__ int first_round_left(Ctrl *c, int f) {
+  int v[kClaimGroups];
+#pragma unroll
+  for (int g = 0; g < kClaimGroups; ++g) v[g] = load_relaxed(&c->gclaim[g][0]);
+#pragma unroll
+  for (int g = 0; g < kClaimGroups; ++g) {
+    const int quota = f > g ? (f - 1 - g) / kClaimGroups + 1 : 0;
+    if (v[g] < quota) {
+      const int t = claim(&c->gclaim[g][0]) * kClaimGroups + g;
+      if (t < f) return t;
+    }
+  }
+  return -1;
+}
+
 template <int BM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void expert_mfma_kernel(ExpertArgs a) {
@@ -1573,8 +1594,15 @@ void expert_mfma_kernel(ExpertArgs a) {
   Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
   const bool bounds = kBounds && a.bounds != 0;
-  // the last wave claims: the plan's loads are in the other waves
-  if (tid == kThreads - 1) s_task = claim(&c->head);
+  // the last wave claims: the plan's loads are in the other waves.  A
+  // routing from bounds draws the blocks' first tasks from kClaimGroups
+  // counters (Ctrl::gclaim): the first round of claims, in a grid of more
+  // blocks than dispatch tasks (a block that runs one late ends after it)
+  const bool groups = bounds && (int)gridDim.x > (a.T + kDecRT - 1) / kDecRT;
+  if (tid == kThreads - 1) {
+    const int g = (int)(blockIdx.x % kClaimGroups);
+    s_task = groups ? claim(&c->gclaim[g][0]) * kClaimGroups + g : claim(&c->head);
+  }
   int pv[8];  // nb, n1, n2, ntot, p1u, p2u, gtail, tail
   const int *row_tok = nullptr;
   const uint32_t *pmask = nullptr;
@@ -1644,11 +1672,34 @@ void expert_mfma_kernel(ExpertArgs a) {
   static_assert(bc_floats<kBcKC, kBcTB>() <= TL::LDS_FLOATS &&
                     sizeof(RouteShared) + kExperts * sizeof(float) <= TL::LDS_FLOATS * sizeof(float),
                 "a routing job's chains and routing fit the kernel's LDS");
+  // Claims.  The queue head hands out tasks nfirst + 0, 1, 2, ...  A routing
+  // from bounds hands out the first nfirst tasks (at most one per block, the
+  // dispatch and gate/up tasks, none of which waits for another task) from
+  // the group counters.  A block claims from the head only once every
+  // first-round task is claimed (first_round_left: it claims any left
+  // itself), so a block that has not started (another kernel holds its CU)
+  // holds no task that a running block's down tile waits for: claims then
+  // follow the task order, as with the head alone.
+  const int nfirst = groups ? min((int)gridDim.x, nb + n1) : 0;
+  int first_left = groups ? 1 : 0;  // thread 0: first-round tasks may be unclaimed
+  auto next_task = [&]() -> int {
+    if (first_left) {
+      const int t = first_round_left(c, nfirst);
+      if (t >= 0) return t;
+      first_left = 0;
+    }
+    return nfirst + claim(&c->head);
+  };
   int task = s_task;
-  // Dispatch tasks lead the queue and a block's claims only grow, so a block
-  // runs all of its dispatch tasks before its first tile (a loop of their
-  // own: the tiles' registers are allocated apart from the routing's).
-  while (task < nb && task < ntot) {
+  if (groups && task >= nfirst) {  // a group's claim past the first round
+    __syncthreads();
+    if (tid == 0) s_task = next_task();
+    __syncthreads();
+    task = s_task;
+  }
+  // A dispatch task: the routing of its token block (a routing from bounds)
+  // or its slots, and its tokens' combine counters cleared.
+  auto run_dispatch = [&](int task) {
     const int rt = bounds ? kDecRT : c->rtokens;
     if (!bounds) {
       assign_task(a, task, rt, slots_ready);
@@ -1662,12 +1713,18 @@ void expert_mfma_kernel(ExpertArgs a) {
       if (tok < a.T) st_agent(&a.s.ccount[(size_t)tok * ncc + i % ncc], 0);
     }
     block_signal(&c->assign_done);
-    if (tid == 0) s_task = claim(&c->head);
+  };
+  // Dispatch tasks lead the queue, so a block runs its dispatch tasks before
+  // its first tile (a loop of their own: the tiles' registers are allocated
+  // apart from the routing's).
+  while (task < nb && task < ntot) {
+    run_dispatch(task);
+    if (tid == 0) s_task = next_task();
     __syncthreads();
     task = s_task;
     __syncthreads();
   }
-  while (task < ntot) {
+  while (task >= nb && task < ntot) {
     int next = 0;  // the block's next task (thread 0), claimed near this one's end
     if (task < nb + n1) {
       // gate/up tiles: full width for the first units, two half-width tiles
@@ -1700,10 +1757,10 @@ void expert_mfma_kernel(ExpertArgs a) {
           using TH = TileHalf<64>;
           const float *hrow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TH::BN) * H;
           next = mfma_tile<TH, true>(lds, a.x, xbytes, s_aoff, rows, hrow0, H, inter_out, slot0,
-                                     I, nt * (TH::BN / 2), &c->head);
+                                     I, nt * (TH::BN / 2), next_task);
         } else {
           next = mfma_tile<TL, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
-                                     I, nt * (TL::BN / 2), &c->head);
+                                     I, nt * (TL::BN / 2), next_task);
         }
       } else if (BM == 128 && ghalf) {  // one W1/W3 row group: 32 intermediate columns
         static_assert(TileHalf<64>::BN == TileHalf<128>::BN, "a half tile's columns");
@@ -1711,16 +1768,16 @@ void expert_mfma_kernel(ExpertArgs a) {
         const float *hrow0 = a.w.w13 + ((size_t)e * 2 * I + (size_t)nt * TH::BN) * H;
         if (rows <= 64)
           next = mfma_tile<TileHalf<64>, true>(lds, a.x, xbytes, s_aoff, rows, hrow0, H, inter_out,
-                                               slot0, I, nt * (TH::BN / 2), &c->head);
+                                               slot0, I, nt * (TH::BN / 2), next_task);
         else
           next = mfma_tile<TH, true>(lds, a.x, xbytes, s_aoff, rows, hrow0, H, inter_out, slot0, I,
-                                     nt * (TH::BN / 2), &c->head);
+                                     nt * (TH::BN / 2), next_task);
       } else if (BM == 128 && rows <= 64) {
         next = mfma_tile<Tile<64>, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
-                                         I, nt * (TL::BN / 2), &c->head);
+                                         I, nt * (TL::BN / 2), next_task);
       } else {
         next = mfma_tile<Tile<BM>, true>(lds, a.x, xbytes, s_aoff, rows, brow0, H, inter_out, slot0,
-                                         I, nt * (TL::BN / 2), &c->head);
+                                         I, nt * (TL::BN / 2), next_task);
       }
       // this tile's intermediate columns are stored: its bit of the unit's mask
       __builtin_amdgcn_s_waitcnt(0);
@@ -1794,16 +1851,16 @@ void expert_mfma_kernel(ExpertArgs a) {
         using TH = TileHalf<BM>;
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TH::BN) * I;
         next = mfma_tile<TH, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
-                                    H, ht * TH::BN, &c->head, ready);
+                                    H, ht * TH::BN, next_task, ready);
         tile_combine<TH::BN>(a, slot0, rows, ht * TH::BN, s_comb, &s_ncomb, row_tok, pmask);
       } else {
         const float *brow0 = a.w.w2 + ((size_t)e * H + (size_t)ht * TL::BN) * I;
         if (BM == 128 && rows <= 64)
           next = mfma_tile<Tile<64>, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out,
-                                            slot0, H, ht * TL::BN, &c->head, ready);
+                                            slot0, H, ht * TL::BN, next_task, ready);
         else
           next = mfma_tile<TL, false>(lds, abase, abytes, s_aoff, rows, brow0, I, sout_out, slot0,
-                                      H, ht * TL::BN, &c->head, ready);
+                                      H, ht * TL::BN, next_task, ready);
         tile_combine<TL::BN>(a, slot0, rows, ht * TL::BN, s_comb, &s_ncomb, row_tok, pmask);
       }
     }
@@ -1812,6 +1869,11 @@ void expert_mfma_kernel(ExpertArgs a) {
     __syncthreads();
     task = s_task;
   }
+  // A first-round dispatch task that no block had claimed when this block's
+  // tile claimed (its group's blocks had not started: first_round_left)
+  // runs here, and the block ends: the blocks that claim on finish the
+  // queue (the grid holds more blocks than dispatch tasks).
+  if (task < nb) run_dispatch(task);
 }
 
 // ---------------------------------------------------------------------------

@@ -62,6 +62,17 @@ residency; the model reaches one when the waits do not run unclaimed jobs
 (lazy mode: no block ever would), and when a job waits for another (the
 block that holds job 0 waits for job 1, which only a block that is not
 resident could claim).
+
+When the MFMA kernel routes from score bounds, its blocks claim their first
+tasks from K group counters instead of the queue head (explore_groups):
+group g's k-th claim is task k * K + g, for the first F tasks (dispatch and
+gate/up tasks, which never wait); a block claims from the head (tasks F, F
++ 1, ...) only after it has found every first-round task claimed, claiming
+any left itself; a dispatch task it claims so after a tile it runs last,
+and then it ends.  The protocol is shown free of stuck states, with every
+task done, under partial residency; without the check before the first
+claim from the head the model reaches a stuck state (a down tile waiting
+for a gate/up tile whose group's blocks have not started).
 """
 from __future__ import annotations
 
@@ -373,3 +384,132 @@ def test_a_job_that_waits_for_another_sticks():
     r = explore_chain(plan, 2, 1, 2, 2, job_waits_next=True)
     assert r is not None and "stuck" in r
     assert explore_chain(plan, 2, 1, 2, 2) is None
+
+
+# First round of claims of the MFMA kernel's routing from score bounds
+# (explore_groups).  Group g of K counters (blocks b with b % K == g) hands
+# out tasks g, g + K, ... below F = min(G, dispatch + gate/up tasks), none of
+# which waits; later tasks come from the queue head, F + 0, 1, ...
+# block: (status, cur, nxt, flags, first_left, tiles, last)
+#   cur -2: first claim (its group's counter) not yet made, -1: a claim past
+#   the first round, next_task to be made; flags as in explore; tiles: the
+#   block has run a tile (task >= dispatch tasks); last: a dispatch task
+#   claimed after a tile, which the block runs and then ends.
+def explore_groups(plan: Plan, G: int, R: int, K: int, n_dispatch: int, n_first: int,
+                   check=True):
+    n = plan.n_row
+    F = min(G, n_first)
+    seen = set()
+
+    def quota(g):
+        return (F - 1 - g) // K + 1 if F > g else 0
+
+    def deps_done(done, deps):
+        return all((done >> d) & 1 for d in deps)
+
+    def next_task(head, gc, first_left):
+        """expert_mfma_kernel's next_task (first_round_left, then the head),
+        as one step: counters only grow, so the loads it makes first can
+        only show more tasks left than there are."""
+        gc = list(gc)
+        if check and first_left:
+            for g in range(K):
+                if gc[g] < quota(g):
+                    t = gc[g] * K + g
+                    gc[g] += 1
+                    if t < F:
+                        return t, head, tuple(gc), True
+            first_left = False
+        t, h = (F + head, head + 1) if F + head < n else (n, head)
+        return t, h, tuple(gc), first_left
+
+    def repl(blocks, i, b):
+        nb = list(blocks)
+        nb[i] = b
+        return tuple(nb)
+
+    def moves(state):
+        head, gc, done, blocks = state
+        running = sum(1 for b in blocks if b[0] == RUNNING)
+        out = []
+        for i, (st, cur, nxt, fl, fleft, tiles, last) in enumerate(blocks):
+            if st == PENDING:
+                if running < R and all(b[0] != PENDING for b in blocks[:i]):
+                    out.append((head, gc, done, repl(blocks, i, (RUNNING, -2, -1, 0, True, False, False))))
+                continue
+            if st != RUNNING:
+                continue
+            if cur == -2:  # the group claim
+                g = i % K
+                t = gc[g] * K + g
+                ngc = list(gc)
+                ngc[g] += 1
+                out.append((head, tuple(ngc), done,
+                            repl(blocks, i, (st, t if t < F else -1, -1, 0, fleft, tiles, last))))
+                continue
+            if cur == -1:  # past the first round: claim on
+                t, h, ngc, nfl = next_task(head, gc, fleft)
+                out.append((h, ngc, done, repl(blocks, i, (st, t, -1, 0, nfl, tiles, last))))
+                continue
+            if cur >= n:
+                out.append((head, gc, done, repl(blocks, i, (EXITED, cur, nxt, fl, fleft, tiles, last))))
+                continue
+            awaited, claimed = fl & 1, fl & 2
+            if not awaited and deps_done(done, plan.deps[cur]):
+                out.append((head, gc, done, repl(blocks, i, (st, cur, nxt, fl | 1, fleft, tiles, last))))
+            if awaited and not claimed and not last:
+                t, h, ngc, nfl = next_task(head, gc, fleft)
+                out.append((h, ngc, done, repl(blocks, i, (st, cur, t, fl | 2, nfl, tiles, last))))
+            if awaited and (claimed or last):
+                ndone = done | (1 << cur)
+                if last:
+                    out.append((head, gc, ndone, repl(blocks, i, (EXITED, n, -1, 0, fleft, tiles, last))))
+                else:
+                    nt = tiles or cur >= n_dispatch
+                    out.append((head, gc, ndone, repl(blocks, i, (st, nxt, -1, 0, fleft, nt,
+                                                                  nt and nxt < n_dispatch))))
+        return out
+
+    start = (0, tuple([0] * K), 0, tuple((PENDING, -1, -1, 0, True, False, False) for _ in range(G)))
+    stack = [start]
+    while stack:
+        s = stack.pop()
+        if s in seen:
+            continue
+        seen.add(s)
+        nxt_states = moves(s)
+        if not nxt_states:
+            if not all(b[0] == EXITED for b in s[3]):
+                return f"stuck: done={bin(s[2])} blocks={s[3]}"
+            if s[2] != (1 << n) - 1:
+                return f"unfinished: done={bin(s[2])}"
+        stack.extend(nxt_states)
+    return None
+
+
+GROUP_PLANS = [(dict(n_dispatch=1, units=2, p1=1, p2=1), 1, 2),
+               (dict(n_dispatch=2, units=1, p1=2, p2=1), 2, 2),
+               (dict(n_dispatch=1, units=1, p1=3, p2=1), 1, 1)]
+
+
+@pytest.mark.parametrize("G,R", [(G, R) for G in (2, 3, 4) for R in range(1, G + 1)])
+@pytest.mark.parametrize("K", [1, 2, 3])
+def test_first_round_group_claims_never_stick(G, R, K):
+    for kw, nd, units in GROUP_PLANS:
+        if G <= nd:  # the kernel uses the groups only in grids of more blocks than dispatch tasks
+            continue
+        plan = mfma_plan(router_slots=True, **kw)
+        n_first = nd + units * kw["p1"]
+        assert explore_groups(plan, G, R, K, nd, n_first) is None
+
+
+def test_first_round_without_the_check_sticks():
+    # one dispatch task, two gate/up tiles, a down tile: block 0 (group 0)
+    # runs task 0; claiming straight from the head it gets the down tile,
+    # which waits for gate/up tile 1 of group 1, whose blocks have not started
+    kw = dict(n_dispatch=1, units=1, p1=2, p2=1)
+    plan = mfma_plan(router_slots=True, **kw)
+    assert explore_groups(plan, 3, 1, 2, 1, 3) is None
+    r = explore_groups(plan, 3, 1, 2, 1, 3, check=False)
+    assert r is not None and "stuck" in r
+    assert explore_groups(plan, 3, 3, 2, 1, 3, check=False) is None
