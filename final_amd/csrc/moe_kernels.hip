@@ -1647,14 +1647,16 @@ void expert_mfma_kernel(ExpertArgs a) {
       s_nfull = nfull;
       s_lpt = 2 * nfull <= npart;
     }
-    if (part > 0) {
-      int r = 0;
-      for (int j = 0; j < kExperts; ++j) {
-        const int pj = s_counts[j] % BM;
-        r += pj > part || (pj == part && j < tid);
-      }
-      s_pexp[r] = tid;
+    // the rank from the other lanes' values, read from their registers
+    // (a loop of LDS reads, each waiting for the last: same box, T=256
+    // 307.2 -> 305.4 us, T=64-192 ~0.9 us)
+    int r = 0;
+#pragma unroll
+    for (int j = 0; j < kExperts; ++j) {
+      const int pj = __builtin_amdgcn_readlane(part, j);
+      r += pj > part || (pj == part && j < tid);
     }
+    if (part > 0) s_pexp[r] = tid;
   }
   __syncthreads();
   const UnitOrder uo{s_unit_off, s_full_off, s_pexp, s_counts, BM <= 64 ? s_nfull : 0,
