@@ -685,6 +685,9 @@ void router_kernel(RouterArgs a) {
 // Decode router shape: 8-token blocks, 4 experts per block, 8 blocks per token block.
 constexpr int kDecRT = 8, kDecEPB = 4, kDecES = kExperts / kDecEPB;
 static_assert(kDecRT == kDeferTokens && kDecES == kChainJobs, "a chain job is one router block's chains");
+// Blocks of a deferred decode routing's router that only fill the streaming
+// kernel's rows (kSpecSlots * T rows of I + H floats: 983 KB at T=8).
+constexpr int kDeferFillBlocks = 56;
 constexpr int kChainClaimBlocks = 16;  // streaming-kernel blocks that try for a chain job as they start
 
 // Bounds of the score fl(ref_sigmoid(l) + bias) of the float logit l that an
@@ -839,9 +842,26 @@ void router_decode_kernel(RouterArgs a) {
   __shared__ float s_bias[kExperts];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int T = a.T, H = a.H, P = H + 4;
+  if (a.defer == 2) {
+    // blocks past the token block's 8: the streaming kernel's rows to
+    // kUnwritten (its readers reload a value until it is written), and the
+    // token routing it publishes to "not yet" (kRouteUnset), apart from the
+    // blocks that stage rows, whose loads those stores would hold up
+    const int ncomp = kDecES * ((T + kDecRT - 1) / kDecRT);
+    if ((int)blockIdx.x >= ncomp) {
+      const int fb = (int)blockIdx.x - ncomp, nfb = (int)gridDim.x - ncomp;
+      fill_unwritten(a, fb, nfb, tid, kThreads);
+      if (fb == 0 && tid < T * kTopK) {
+        a.s.idx[tid] = kRouteUnset;
+        a.s.pos[tid] = kRouteUnset;
+        a.s.wts[tid] = __builtin_bit_cast(float, kUnwritten);
+      }
+      return;
+    }
+  }
   const int tb = blockIdx.x / kDecES, es = blockIdx.x % kDecES;
   const int t0 = tb * kDecRT, e0 = es * kDecEPB;
-  const int T = a.T, H = a.H, P = H + 4;
   const int nt = min(kDecRT, T - t0);
   float *gs = lds, *xs = lds + kDecEPB * P;
   // the score bias, read now so the finishing block finds it in LDS
@@ -890,16 +910,6 @@ void router_decode_kernel(RouterArgs a) {
                          c * 256 + lane * 4;
       float *dst = (r < kDecEPB ? gs + r * P : xs + (r - kDecEPB) * P) + c * 256;
       __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void *)dst, 16, 0, 0);
-    }
-    if (a.defer == 2) {
-      // while the rows land: the expert kernel's rows to kUnwritten, and the
-      // token routing it publishes to "not yet" (kRouteUnset)
-      fill_unwritten(a, blockIdx.x, gridDim.x, tid, kThreads);
-      if (blockIdx.x == 0 && tid < T * kTopK) {
-        a.s.idx[tid] = kRouteUnset;
-        a.s.pos[tid] = kRouteUnset;
-        a.s.wts[tid] = __builtin_bit_cast(float, kUnwritten);
-      }
     }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
@@ -3119,7 +3129,10 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
       if (e != hipSuccess) return e;
     }
     const int nb = (a.T + kDecRT - 1) / kDecRT;
-    hipLaunchKernelGGL(router_decode_kernel, dim3(nb * kDecES), dim3(kThreads), lds, st, a);
+    // a deferred routing: kDeferFillBlocks more blocks prepare the
+    // streaming kernel's rows
+    const int fill = a.defer == 2 ? kDeferFillBlocks : 0;
+    hipLaunchKernelGGL(router_decode_kernel, dim3(nb * kDecES + fill), dim3(kThreads), lds, st, a);
     return hipGetLastError();
   }
   const int rt = small ? kSmallRT : kLargeRT;
