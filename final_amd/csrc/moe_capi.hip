@@ -215,15 +215,20 @@ static int ctx_plan(const moe_ctx *ctx, int T) {
 // that many units above 64 tokens (its units are few; with every expert in
 // one unit, the longest-first order puts the smallest experts last): T=256
 // expert launch 329 -> 311 us; one block's worth, 16 units at T=256, took as
-// much there and lost 2 % at T=128.  Up to 64 tokens, where every unit is
-// one small expert, one block's worth (16 units): T=21 256.0 -> 251.6 us,
-// T=32 262.5 -> 258.2, T=48 269.9 -> 266.7, T=64 268.5 -> 267.1; equal at
-// 80-96.
+// much there and lost 2 % at T=128.  Up to 128 tokens, where every unit
+// is one small expert, two blocks' worth (32 units: every unit of such a
+// batch).  One block's worth up to 64 tokens had taken T=21 256.0 -> 251.6
+// us, T=32 262.5 -> 258.2, T=48 269.9 -> 266.7, T=64 268.5 -> 267.1 from
+// half of one; two, same box: T=21 252.6 -> 247.3 us, T=64 269.1 -> 266.5,
+// T=48 equal; then at 65-128 tokens (another box): T=80 271.6 -> 270.6,
+// T=128 273.4 -> 270.2, while T=192 lost 7 us and one block's worth lost 3
+// at T=128.  Twice as many in the 128-row plan: equal at T=2048-4096.
 static int tail_units(const moe_ctx *ctx, int tile_rows, int bn, int T) {
   const int pi = plan_index(tile_rows);
   if ((tile_rows != 128 && tile_rows != 64) || pi < 0) return 0;
   const int half_tiles_per_unit = 2 * (ctx->d.hidden / bn);
-  const int k = ctx->grid[pi] / half_tiles_per_unit / (tile_rows == 64 && T > 64 ? 2 : 1);
+  const int block = ctx->grid[pi] / half_tiles_per_unit;  // one block's worth of units
+  const int k = tile_rows == 128 ? block : T <= 128 ? 2 * block : block / 2;
   return k > 0 ? k : 1;
 }
 
