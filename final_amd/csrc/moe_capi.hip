@@ -180,19 +180,20 @@ static int plan_index(int rows) {
 }
 
 // Crossovers measured on MI355X with the seed-0 workload (moe_forward
-// whole-step times, four weight copies cycled, clocks settled; two boxes,
-// streaming vs 64-row tiles): weight streaming is fastest up to 20 tokens
-// (246.8 vs 249.8 us at 16; 249.8 vs 249.3 and 248.5 vs 255.3 at 18; 259.6
-// vs 255.4 and 258.8 vs 261.7 at 20), 64-row MFMA tiles, whose routing from
-// score bounds planned in every block takes the router's chains and
-// planning off the critical path, from 21 to 1024 tokens (271.9 vs 261.9
-// and 270.4 vs 268.3 at 24; 265.6 vs 261.0 and 264.4 vs 269.5 at 32, where
-// streaming takes 64-row tasks; 283.3 vs 269.8 and 282.0 vs 276.3 at 48;
+// whole-step times, four weight copies cycled, clocks settled; streaming vs
+// 64-row tiles): weight streaming is fastest up to 10 tokens (183.3 vs 198.5
+// us at 8, 207.9 vs 211.5 at 9, 223.4 vs 225.1 at 10), 64-row MFMA tiles,
+// whose routing from score bounds planned in every block takes the router's
+// chains and planning off the critical path and whose down tiles all run at
+// half width up to 128 tokens, from 11 to 1024 tokens (231.1 vs 228.9 at
+// 11, 233.1 vs 230.2 at 12, 245.6 vs 235.1 at 16, 258.2 vs 243.5 at 20;
+// before the half-width down tiles streaming led up to 20; 283.3 vs 269.8
+// and 282.0 vs 276.3 at 48, two boxes;
 // equal at 640-768; 720 vs 726 at 832, 846 vs 854 at 1024), 128-row tiles
 // from 1025 (990 vs 1023 us at 1280, 1478 vs 1540 at 2048).  moe_route +
 // moe_experts, which keep the full router, take the same plans (with it,
 // streaming led up to 48).
-constexpr int kStreamMaxTokens = 20;
+constexpr int kStreamMaxTokens = 10;
 // The dense FFN's 4 chunk experts each hold every token, so its MFMA plans
 // have few tiles at small T: streaming stays fastest up to 192 tokens (214
 // vs 217 us at 128, 280 vs 283 at 192), 64-row tiles at 256 (290 vs 349 us),

@@ -334,8 +334,8 @@ void gpu_full_shape_tests() {
                      Tensor({(size_t)kE}, bias.data(), true));
   blk.set_max_tokens(256);
   blk.init_gpu();
-  CHECK(moe_plan_tile_rows(blk.context(), 8) == 0 && moe_plan_tile_rows(blk.context(), 20) == 0 &&
-        moe_plan_tile_rows(blk.context(), 21) == 64 && moe_plan_tile_rows(blk.context(), 64) == 64);
+  CHECK(moe_plan_tile_rows(blk.context(), 8) == 0 && moe_plan_tile_rows(blk.context(), 10) == 0 &&
+        moe_plan_tile_rows(blk.context(), 11) == 64 && moe_plan_tile_rows(blk.context(), 64) == 64);
   for (int T : {8, 20, 48, 64, 200}) {
     std::vector<float> x((size_t)T * H), yref((size_t)T * H);
     moe_synth_normal(3, 99, 1.0f, 0, x.data(), x.size());

@@ -147,7 +147,7 @@ def test_streaming_four_experts(block, real_weights, oracle_mod):
 @pytest.mark.parametrize("T", [32, 40, 48, 57, 64])
 def test_streaming_wide_tasks(T, block, real_weights, oracle_mod):
     """32-64 tokens under the weight-streaming plan (forced: the automatic
-    plan takes 64-row MFMA tiles from 21 tokens): 64-row tasks, streamed as
+    plan takes 64-row MFMA tiles from 11 tokens): 64-row tasks, streamed as
     four 16-row groups that reuse one load of the token rows when every
     expert holds at most 16 tokens, else as four row groups at once over two
     token passes (one expert made hot by a bias so it holds all T tokens)."""
