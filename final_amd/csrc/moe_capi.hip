@@ -223,13 +223,16 @@ static int ctx_plan(const moe_ctx *ctx, int T) {
 // half of one; two, same box: T=21 252.6 -> 247.3 us, T=64 269.1 -> 266.5,
 // T=48 equal; then at 65-128 tokens (another box): T=80 271.6 -> 270.6,
 // T=128 273.4 -> 270.2, while T=192 lost 7 us and one block's worth lost 3
-// at T=128.  Twice as many in the 128-row plan: equal at T=2048-4096.
+// at T=128.  At 129-192 tokens one block's worth (same box, 2 rounds:
+// T=160 278.9 -> 273.4 us, T=192 282.9 -> 280.9; at 256 it lost 4.8, a
+// quarter of one lost 1.5-3 % at 160-1024).  Twice as many in the 128-row
+// plan: equal at T=2048-4096.
 static int tail_units(const moe_ctx *ctx, int tile_rows, int bn, int T) {
   const int pi = plan_index(tile_rows);
   if ((tile_rows != 128 && tile_rows != 64) || pi < 0) return 0;
   const int half_tiles_per_unit = 2 * (ctx->d.hidden / bn);
   const int block = ctx->grid[pi] / half_tiles_per_unit;  // one block's worth of units
-  const int k = tile_rows == 128 ? block : T <= 128 ? 2 * block : block / 2;
+  const int k = tile_rows == 128 ? block : T <= 128 ? 2 * block : T <= 192 ? block : block / 2;
   return k > 0 ? k : 1;
 }
 
