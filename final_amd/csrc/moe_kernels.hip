@@ -201,6 +201,20 @@ __device__ __forceinline__ int lane_scan32(int v, int lane, int *total) {
   return inc - v;
 }
 
+// Units whose gate/up tiles run as two half-width tiles (the launch's last
+// units, so its last gate/up tiles end sooner and the down tiles after them
+// wait less): in the 64-row plan up to kGateUpTailTokens tokens
+// kGateUpTailUnits of them, every unit at 37-52 tokens (against 8 of them,
+// two boxes: T=40 265.9 -> 260.7 and 264.5 -> 261.0 us, T=48 264.3 -> 261.1
+// and 262.9 -> 261.2; T=33 1.6 us and T=56 1 us slower); in the 128-row
+// plan up to kGateUpTailTokens128 tokens kGateUpTailUnits of them.
+__device__ __forceinline__ int gate_up_tail(int tile_rows, int T, int units) {
+  if (tile_rows == 64 && T <= kGateUpTailTokens)
+    return min(units, T > 36 && T <= 52 ? kExperts : kGateUpTailUnits);
+  if (tile_rows == 128 && T <= kGateUpTailTokens128) return min(units, kGateUpTailUnits);
+  return 0;
+}
+
 template <int RT>
 __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
                             PlanLocal loc = PlanLocal{nullptr, nullptr, nullptr}) {
@@ -293,9 +307,7 @@ __device__ void router_plan(const RouterArgs &a, int nb, int T, PlanShared &ps,
       // tiles; the 128-row plan's long tiles up to 1024 tokens): the last
       // units' gate/up tiles run at half width too, so the last gate/up tiles
       // end sooner and the down tiles after them wait less
-      const int gtail = tr == 64 && T <= kGateUpTailTokens ? min(units, kGateUpTailUnits)
-                        : tr == 128 && T <= kGateUpTailTokens128 ? min(units, kGateUpTailUnits)
-                                                                 : 0;
+      const int gtail = gate_up_tail(tr, T, units);
       ctrl->gu_tail = gtail;
       ctrl->n_p1 = (units + gtail) * p1u;
       ctrl->n_p2 = (units - tail + tail * tail_mult) * p2u;
@@ -1430,7 +1442,7 @@ __device__ __forceinline__ void bounds_local_plan(const ExpertArgs &a, Ctrl *c, 
       const int units = utotal;
       const int p1u = a.I / (Tile<BM>::BN / 2), p2u = a.H / Tile<BM>::BN;
       const int tail = min(units, a.tail_units);
-      const int gtail = BM == 64 && T <= kGateUpTailTokens ? min(units, kGateUpTailUnits) : 0;
+      const int gtail = BM == 64 ? gate_up_tail(BM, T, units) : 0;
       const int n1 = (units + gtail) * p1u, n2 = (units - tail + 2 * tail) * p2u;
       bp.plan[0] = nb;
       bp.plan[1] = n1;
