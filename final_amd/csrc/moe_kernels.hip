@@ -855,12 +855,16 @@ void router_decode_kernel(RouterArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, H = a.H, P = H + 4;
+  // tokens per block: a deferred routing of 5-8 tokens runs two blocks of up
+  // to 4 per expert slice (half the rows to stage, and its bound sums have
+  // twice the threads per pair)
+  const int rtb = a.defer == 2 && T > kDecRT / 2 ? kDecRT / 2 : kDecRT;
   if (a.defer == 2) {
     // blocks past the token block's 8: the streaming kernel's rows to
     // kUnwritten (its readers reload a value until it is written), and the
     // token routing it publishes to "not yet" (kRouteUnset), apart from the
     // blocks that stage rows, whose loads those stores would hold up
-    const int ncomp = kDecES * ((T + kDecRT - 1) / kDecRT);
+    const int ncomp = kDecES * ((T + rtb - 1) / rtb);
     if ((int)blockIdx.x >= ncomp) {
       const int fb = (int)blockIdx.x - ncomp, nfb = (int)gridDim.x - ncomp;
       fill_unwritten(a, fb, nfb, tid, kThreads);
@@ -873,8 +877,8 @@ void router_decode_kernel(RouterArgs a) {
     }
   }
   const int tb = blockIdx.x / kDecES, es = blockIdx.x % kDecES;
-  const int t0 = tb * kDecRT, e0 = es * kDecEPB;
-  const int nt = min(kDecRT, T - t0);
+  const int t0 = tb * rtb, e0 = es * kDecEPB;
+  const int nt = min(rtb, T - t0);
   float *gs = lds, *xs = lds + kDecEPB * P;
   // the score bias, read now so the finishing block finds it in LDS
   if (tid < kExperts) s_bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
@@ -951,19 +955,22 @@ void router_decode_kernel(RouterArgs a) {
     __syncthreads();
   }
   if (a.defer >= 2) {
-    // 2'. score bounds in place of the chains (score_bounds): 8 threads per
-    // (token, expert) pair, k interleaved in float4s, four float sums of
-    // products and four of magnitudes each (H / 32 FMAs per sum, then 2
-    // adds and 3 shuffle levels).  The 8 threads of a pair are 8 consecutive
-    // lanes, so the pairs of tokens past the batch are skipped whole: at
-    // T=1 only wave 0's first half reads LDS (the sums were LDS-bound)
-    const int pr = tid >> 3, part = tid & 7;
+    // 2'. score bounds in place of the chains (score_bounds): tpp threads
+    // per (token, expert) pair (all 256 threads on the block's nt tokens: 64
+    // at one token, 8 at 5-8), k interleaved in float4s, four float sums of
+    // products and four of magnitudes each (H / (4 tpp) FMAs per sum, then
+    // 2 adds and log2(tpp) shuffle levels).  A pair's threads are
+    // consecutive lanes.  Each thread's chains were the sums' critical path:
+    // at one token 32 threads ran 64 steps each.
+    const int tpp = nt == 1 ? 64 : nt == 2 ? 32 : nt <= 4 ? 16 : 8;
+    const int lg = tpp == 64 ? 6 : tpp == 32 ? 5 : tpp == 16 ? 4 : 3;
+    const int pr = tid >> lg, part = tid & (tpp - 1);
     const int tl = pr / kDecEPB, el = pr % kDecEPB;
     if (tl < nt) {
       const float *gp = gs + el * P, *xp = xs + tl * P;
       float sq[4] = {0.0f, 0.0f, 0.0f, 0.0f}, mq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll 8
-      for (int k = part * 4; k < H; k += 32) {
+      for (int k = part * 4; k < H; k += 4 * tpp) {
         const f32x4 g = ld4(gp + k), xv = ld4(xp + k);
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -972,17 +979,16 @@ void router_decode_kernel(RouterArgs a) {
         }
       }
       float sum = (sq[0] + sq[1]) + (sq[2] + sq[3]), mag = (mq[0] + mq[1]) + (mq[2] + mq[3]);
-#pragma unroll
-      for (int o = 1; o < 8; o <<= 1) {
-        sum += __shfl_xor(sum, o, 8);
-        mag += __shfl_xor(mag, o, 8);
+      for (int o = 1; o < tpp; o <<= 1) {
+        sum += __shfl_xor(sum, o, tpp);
+        mag += __shfl_xor(mag, o, tpp);
       }
       if (part == 0) {
         float lo, hi;
-        score_bounds(sum, mag, H, H / 32 + 5, s_bias[e0 + el], &lo, &hi);
+        score_bounds(sum, mag, H, H / (4 * tpp) + 2 + lg, s_bias[e0 + el], &lo, &hi);
         if (a.defer == 2) {
-          a.s.ctrl->sbound[0][tl][e0 + el] = lo;
-          a.s.ctrl->sbound[1][tl][e0 + el] = hi;
+          a.s.ctrl->sbound[0][t0 + tl][e0 + el] = lo;
+          a.s.ctrl->sbound[1][t0 + tl][e0 + el] = hi;
         } else {  // read by the token block's finishing block
           float *b = a.s.bounds + (size_t)(t0 + tl) * 2 * kExperts + e0 + el;
           st_agent(b, lo);
@@ -3140,9 +3146,11 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
-    const int nb = (a.T + kDecRT - 1) / kDecRT;
-    // a deferred routing: kDeferFillBlocks more blocks prepare the
-    // streaming kernel's rows
+    // a deferred routing of 5-8 tokens: two blocks of up to 4 tokens per
+    // expert slice (router_decode_kernel's rtb), and kDeferFillBlocks more
+    // blocks prepare the streaming kernel's rows
+    const int rtb = a.defer == 2 && a.T > kDecRT / 2 ? kDecRT / 2 : kDecRT;
+    const int nb = (a.T + rtb - 1) / rtb;
     const int fill = a.defer == 2 ? kDeferFillBlocks : 0;
     hipLaunchKernelGGL(router_decode_kernel, dim3(nb * kDecES + fill), dim3(kThreads), lds, st, a);
     return hipGetLastError();
