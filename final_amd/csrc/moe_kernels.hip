@@ -700,6 +700,11 @@ static_assert(kDecRT == kDeferTokens && kDecES == kChainJobs, "a chain job is on
 // Blocks of a deferred decode routing's router that only fill the streaming
 // kernel's rows (kSpecSlots * T rows of I + H floats: 983 KB at T=8).
 constexpr int kDeferFillBlocks = 56;
+// Tokens per router block of a deferred decode routing (more blocks, each
+// staging fewer token rows, 64 threads per pair in its bound sums; from 8
+// per block, 4 took T=8 183.2 -> 182.0 us, 2 then T=4 117.1 -> 116.4, T=6
+// 159.6 -> 158.7, T=8 182.4 -> 181.6, and 1 a further 0.3-0.4 us at T=2-8).
+constexpr int kDeferBlockTokens = 1;
 constexpr int kChainClaimBlocks = 16;  // streaming-kernel blocks that try for a chain job as they start
 
 // Bounds of the score fl(ref_sigmoid(l) + bias) of the float logit l that an
@@ -855,10 +860,10 @@ void router_decode_kernel(RouterArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int T = a.T, H = a.H, P = H + 4;
-  // tokens per block: a deferred routing of 5-8 tokens runs two blocks of up
-  // to 4 per expert slice (half the rows to stage, and its bound sums have
-  // twice the threads per pair)
-  const int rtb = a.defer == 2 && T > kDecRT / 2 ? kDecRT / 2 : kDecRT;
+  // tokens per block: a deferred routing of more than kDeferBlockTokens
+  // tokens runs blocks of kDeferBlockTokens per expert slice (fewer rows to
+  // stage, and more threads per pair in its bound sums)
+  const int rtb = a.defer == 2 && T > kDeferBlockTokens ? kDeferBlockTokens : kDecRT;
   if (a.defer == 2) {
     // blocks past the token block's 8: the streaming kernel's rows to
     // kUnwritten (its readers reload a value until it is written), and the
@@ -3146,10 +3151,10 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
                                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
       if (e != hipSuccess) return e;
     }
-    // a deferred routing of 5-8 tokens: two blocks of up to 4 tokens per
+    // a deferred routing: blocks of up to kDeferBlockTokens tokens per
     // expert slice (router_decode_kernel's rtb), and kDeferFillBlocks more
     // blocks prepare the streaming kernel's rows
-    const int rtb = a.defer == 2 && a.T > kDecRT / 2 ? kDecRT / 2 : kDecRT;
+    const int rtb = a.defer == 2 && a.T > kDeferBlockTokens ? kDeferBlockTokens : kDecRT;
     const int nb = (a.T + rtb - 1) / rtb;
     const int fill = a.defer == 2 ? kDeferFillBlocks : 0;
     hipLaunchKernelGGL(router_decode_kernel, dim3(nb * kDecES + fill), dim3(kThreads), lds, st, a);
