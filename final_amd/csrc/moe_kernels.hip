@@ -705,6 +705,17 @@ constexpr int kDeferFillBlocks = 56;
 // per block, 4 took T=8 183.2 -> 182.0 us, 2 then T=4 117.1 -> 116.4, T=6
 // 159.6 -> 158.7, T=8 182.4 -> 181.6, and 1 a further 0.3-0.4 us at T=2-8).
 constexpr int kDeferBlockTokens = 1;
+// Tokens per block of a routing from score bounds for the MFMA plans up to
+// kBoundSplitTokens tokens: two blocks per token block of 8 and expert
+// slice (the last of a token block's blocks plans it; same box against one:
+// T=11 231.4 -> 229.1 us, T=21 245.2 -> 243.7, T=64 264.7 -> 263.9; at 128
+// and 256 about 1 us slower, so larger batches keep one).
+constexpr int kBoundBlockTokens = 4, kBoundSplitTokens = 64;
+__host__ __device__ inline int router_block_tokens(int defer, int T) {
+  if (defer == 2) return T > kDeferBlockTokens ? kDeferBlockTokens : kDecRT;
+  if (defer == 3) return T > kBoundBlockTokens && T <= kBoundSplitTokens ? kBoundBlockTokens : kDecRT;
+  return kDecRT;
+}
 constexpr int kChainClaimBlocks = 16;  // streaming-kernel blocks that try for a chain job as they start
 
 // Bounds of the score fl(ref_sigmoid(l) + bias) of the float logit l that an
@@ -863,7 +874,7 @@ void router_decode_kernel(RouterArgs a) {
   // tokens per block: a deferred routing of more than kDeferBlockTokens
   // tokens runs blocks of kDeferBlockTokens per expert slice (fewer rows to
   // stage, and more threads per pair in its bound sums)
-  const int rtb = a.defer == 2 && T > kDeferBlockTokens ? kDeferBlockTokens : kDecRT;
+  const int rtb = router_block_tokens(a.defer, T);
   if (a.defer == 2) {
     // blocks past the token block's 8: the streaming kernel's rows to
     // kUnwritten (its readers reload a value until it is written), and the
@@ -1012,12 +1023,16 @@ void router_decode_kernel(RouterArgs a) {
     // writes each token's mask and the block's count per expert (a copy per
     // die); every block of the expert kernel plans from them
     // (bounds_local_plan).
+    // the token block of 8 this block's tokens belong to, and its blocks
+    // (kDecES per rtb tokens)
+    const int tb8 = t0 / kDecRT, t08 = tb8 * kDecRT, nt8 = min(kDecRT, T - t08);
+    const int nblk8 = kDecES * ((nt8 + rtb - 1) / rtb);
     __builtin_amdgcn_s_waitcnt(0);  // this block's bounds are stored
     __syncthreads();
     if (tid == 0) {
-      s_flag = fetch_add(&a.s.tb_done[tb], 1) == kDecES - 1;
+      s_flag = fetch_add(&a.s.tb_done[tb8], 1) == nblk8 - 1;
       if (s_flag) {
-        a.s.tb_done[tb] = 0;  // all blocks counted in: reset
+        a.s.tb_done[tb8] = 0;  // all blocks counted in: reset
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
       }
     }
@@ -1025,8 +1040,8 @@ void router_decode_kernel(RouterArgs a) {
     if (!s_flag) return;
     {
       const int tl = tid >> 5, e = tid & (kExperts - 1);
-      const bool tv = tl < nt;
-      const float *b = a.s.bounds + (size_t)(t0 + min(tl, nt - 1)) * 2 * kExperts + e;
+      const bool tv = tl < nt8;
+      const float *b = a.s.bounds + (size_t)(t08 + min(tl, nt8 - 1)) * 2 * kExperts + e;
       const float hi = b[kExperts];
       rs.prob[tl][e] = b[0];
       __syncthreads();
@@ -1043,7 +1058,7 @@ void router_decode_kernel(RouterArgs a) {
       const uint32_t m = (uint32_t)(__ballot(poss) >> (32 * ((tid & 63) >> 5)));
       rs.sel[tl][e] = poss ? 1 : 0;
       // one copy per die (kPlanCopies): lane e < 8 of each token's row
-      if (tv && e < kPlanCopies) a.s.bplan[(size_t)e * kPlanCopyInts + t0 + tl] = m;
+      if (tv && e < kPlanCopies) a.s.bplan[(size_t)e * kPlanCopyInts + t08 + tl] = m;
       __syncthreads();
       {
         int cnt = 0;
@@ -1051,7 +1066,7 @@ void router_decode_kernel(RouterArgs a) {
         for (int t2 = 0; t2 < kDecRT; ++t2) cnt += rs.sel[t2][e];
         // thread (copy tl, expert e)
         static_assert(kPlanCopies == kDecRT, "a copy per token row of the block");
-        a.s.bplan[(size_t)tl * kPlanCopyInts + kBoundTokens + tb * kExperts + e] = (uint32_t)cnt;
+        a.s.bplan[(size_t)tl * kPlanCopyInts + kBoundTokens + tb8 * kExperts + e] = (uint32_t)cnt;
       }
     }
     return;
@@ -3154,7 +3169,7 @@ hipError_t launch_router(const RouterArgs &a, bool from_logits, hipStream_t st) 
     // a deferred routing: blocks of up to kDeferBlockTokens tokens per
     // expert slice (router_decode_kernel's rtb), and kDeferFillBlocks more
     // blocks prepare the streaming kernel's rows
-    const int rtb = a.defer == 2 && a.T > kDeferBlockTokens ? kDeferBlockTokens : kDecRT;
+    const int rtb = router_block_tokens(a.defer, a.T);
     const int nb = (a.T + rtb - 1) / rtb;
     const int fill = a.defer == 2 ? kDeferFillBlocks : 0;
     hipLaunchKernelGGL(router_decode_kernel, dim3(nb * kDecES + fill), dim3(kThreads), lds, st, a);
