@@ -35,6 +35,16 @@ __device__ __forceinline__ int fetch_add(int *p, int v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Block barrier that orders LDS only: each wave waits for its own LDS
+// operations, not for its outstanding global loads and atomics, whose
+// results are waited for where they are used (a full __syncthreads waits for
+// those too).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Task-queue claim: the index publishes no data, so no fence is needed.
 __device__ __forceinline__ int claim(int *p) {
   return __hip_atomic_fetch_add(p, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

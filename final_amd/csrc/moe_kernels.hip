@@ -2869,7 +2869,7 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
   extern __shared__ __align__(16) float res[];
   __shared__ RingShared sh;
   __shared__ RouteShared rsh;  // deferred routing only
-  __shared__ int s_nact, s_maxcnt, s_job, s_fin;
+  __shared__ int s_nact, s_maxcnt, s_job, s_fin, s_notok;
   const Ctrl *c = a.s.ctrl;
   const int tid = threadIdx.x;
   // 2: the router wrote score bounds, and the logits are this kernel's chain
@@ -2888,13 +2888,31 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     sh.flushed = 0;
     sh.abort = 0;
     sh.local = local ? 1 : 0;
+    s_notok = 0;
     const int job = chain_try ? claim(&a.s.ctrl->chain_head) : kChainJobs;
     s_job = job;
     // every task, the first included, is claimed from the queue, so only a
     // block that is running owns one (blocks not yet resident own nothing
     // another block waits for)
-    if (job >= kChainJobs) sh.seq[0] = claim(&a.s.ctrl->head);
+    if (chain_try && job >= kChainJobs) sh.seq[0] = claim(&a.s.ctrl->head);
     sh.nseq = 1;
+  }
+  // Other blocks claim their first row task now and store it only after the
+  // plan: 256 blocks' first claims on one counter serialise (a reply came
+  // back up to ~4 us after the block started), and the plan's barriers
+  // order LDS only (lds_barrier), so the claim's round trip overlaps it.
+  // Wave 4, which loads nothing for the plan (a wait for a later load would
+  // wait for the claim too: loads complete in issue order), issues it with
+  // its first lane's offset the only one in range (the other lanes' are
+  // no-ops), so nothing waits for it before its use.
+  constexpr int kClaimWave0 = kDecRT * kExperts;  // the first thread past the plan's pairs
+  static_assert(kClaimWave0 % 64 == 0 && kClaimWave0 + 64 <= kRingThreads, "a wave of its own");
+  int first_task = 0;
+  if (!chain_try && tid >= kClaimWave0 && tid < kClaimWave0 + 64) {
+    const __amdgpu_buffer_rsrc_t cr0 =
+        __builtin_amdgcn_make_buffer_rsrc(a.s.ctrl, 0, (int)sizeof(Ctrl), kBufferRsrcWord3);
+    first_task = __builtin_amdgcn_raw_ptr_buffer_atomic_add_i32(
+        1, cr0, tid == kClaimWave0 ? (uint32_t)offsetof(Ctrl, head) : kRingOff, 0, 0);
   }
   bool claim_late = false;  // the first row task is claimed after a chain job
   RingPlan pl;
@@ -2931,11 +2949,11 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
         hi = c->sbound[1][tl][e];
       }
       if (tid < kExperts) sh.bias[tid] = a.w.bias ? a.w.bias[tid] : 0.0f;
-      __syncthreads();
+      lds_barrier();
       claim_late = s_job < kChainJobs;
       if (claim_late) ring_chain_job(a, sh, rsh, &s_fin, s_job, res);
       if (pair) rsh.prob[tl][e] = lo;
-      __syncthreads();
+      lds_barrier();
       if (pair && tl < a.T) {
         int beat = 0;
 #pragma unroll
@@ -2951,7 +2969,9 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
       const int half = (tid & 63) >> 5;
       const uint32_t gin = (uint32_t)(__ballot(chosen) >> (32 * half));
       const bool tok_ok = !pair || tl >= a.T || __popc(gin) <= kSpecSlots;
-      planned = __syncthreads_and(tok_ok) != 0;
+      if (!tok_ok) s_notok = 1;
+      lds_barrier();
+      planned = s_notok == 0;
       if (!planned) {
         // a token with more than kSpecSlots possible experts (non-finite
         // inputs or bias): run the chain jobs nobody has claimed, wait for
@@ -2993,7 +3013,7 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
       // per-expert counts and each possible pair's rank among the block's
       // tokens
       if (pair) rsh.sel[tl][e] = chosen ? 1 : 0;
-      __syncthreads();
+      lds_barrier();
       int before = 0;
       if (pair && tl < a.T) {
         int all = 0;
@@ -3005,9 +3025,9 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
         }
         if (tl == 0) rsh.cnt[e] = all;
       }
-      __syncthreads();
+      lds_barrier();
       ring_expert_table(a, sh, rsh, blockIdx.x == 0, &s_nact, &s_maxcnt);
-      __syncthreads();
+      lds_barrier();
       if (pair) {
         const int slot = chosen ? sh.offsets[e] + before : -1;
         sh.slotmap[tl][e] = slot;
@@ -3036,7 +3056,7 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
         }
       }
     }
-    __syncthreads();
+    lds_barrier();
     const int units = s_nact;  // read after the barrier above
     pl.rows = kStreamRows;
     pl.p1u = a.I / (kStreamRows / 2);
@@ -3082,6 +3102,7 @@ __global__ __launch_bounds__(kRingThreads) void expert_ring_kernel(ExpertArgs a)
     }
   }
   if (claim_late && tid == 0) sh.seq[0] = claim(&a.s.ctrl->head);
+  if (!chain_try && tid == kClaimWave0) sh.seq[0] = first_task;
   __syncthreads();
   const long long ticks = (long long)a.wait_limit * kRingTicksPerLimit;
   if (pl.rows == kStreamRows) {
