@@ -705,15 +705,21 @@ constexpr int kDeferFillBlocks = 56;
 // per block, 4 took T=8 183.2 -> 182.0 us, 2 then T=4 117.1 -> 116.4, T=6
 // 159.6 -> 158.7, T=8 182.4 -> 181.6, and 1 a further 0.3-0.4 us at T=2-8).
 constexpr int kDeferBlockTokens = 1;
-// Tokens per block of a routing from score bounds for the MFMA plans up to
-// kBoundSplitTokens tokens: two blocks per token block of 8 and expert
-// slice (the last of a token block's blocks plans it; same box against one:
-// T=11 231.4 -> 229.1 us, T=21 245.2 -> 243.7, T=64 264.7 -> 263.9; at 128
-// and 256 about 1 us slower, so larger batches keep one).
-constexpr int kBoundBlockTokens = 4, kBoundSplitTokens = 64;
+// Tokens per block of a routing from score bounds for the MFMA plans: up to
+// 32 tokens four blocks per token block of 8 and expert slice, up to 64 two
+// (the last of a token block's blocks plans it).  Same box against one:
+// T=11 231.4 -> 229.1 us, T=21 245.2 -> 243.7, T=64 264.7 -> 263.9 with two;
+// four then T=11 228.7 -> 227.7, T=16 235.2 -> 234.0 (another box: T=11
+// 229.3 -> 228.7, T=16 234.7 -> 234.1, T=24-48 equal; 1 us slower at 64,
+// and eight 6 us slower there); at 128 and 256 two were about 1 us slower,
+// so larger batches keep one.
+constexpr int kBoundSplitTokens = 64, kBoundSplit4Tokens = 32;
 __host__ __device__ inline int router_block_tokens(int defer, int T) {
   if (defer == 2) return T > kDeferBlockTokens ? kDeferBlockTokens : kDecRT;
-  if (defer == 3) return T > kBoundBlockTokens && T <= kBoundSplitTokens ? kBoundBlockTokens : kDecRT;
+  if (defer == 3) {
+    if (T > 2 && T <= kBoundSplit4Tokens) return 2;
+    if (T > 4 && T <= kBoundSplitTokens) return 4;
+  }
   return kDecRT;
 }
 constexpr int kChainClaimBlocks = 16;  // streaming-kernel blocks that try for a chain job as they start
